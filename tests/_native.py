@@ -1,0 +1,220 @@
+"""ctypes bindings shared by the tests: the oracle (oracle/liboracle.so), the
+reference engine built from its own sources (oracle/_ref/*.so, present only
+where oracle/Makefile could build it) and the product library.
+
+The oracle and the reference builds are checkers; only the product library is
+the thing under test.
+"""
+import ctypes as C
+import os
+import numpy as np
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_SO = os.path.join(REPO, "oracle", "liboracle.so")
+REF_SO = {
+    "scalar": os.path.join(REPO, "oracle", "_ref", "libvxref_scalar.so"),
+    "avx2": os.path.join(REPO, "oracle", "_ref", "libvxref_avx2.so"),
+}
+PRODUCT_SO = os.path.join(REPO, "veltrix-engine_amd", "lib", "libveltrix_amd.so")
+
+f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+u8p = np.ctypeslib.ndpointer(dtype=np.uint8, flags="C_CONTIGUOUS")
+i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+
+
+def _ptr(a):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+# --------------------------------------------------------------------------
+# struct layouts (match include/veltrix.h, which matches the reference's)
+# --------------------------------------------------------------------------
+class VxModelConfig(C.Structure):
+    _fields_ = [
+        ("n_layers", C.c_int), ("n_heads", C.c_int), ("n_kv_heads", C.c_int),
+        ("n_embd", C.c_int), ("n_head_dim", C.c_int), ("n_ff", C.c_int),
+        ("n_vocab", C.c_int), ("n_ctx", C.c_int), ("rope_theta", C.c_float),
+        ("rope_freq_base", C.c_float), ("n_threads", C.c_int), ("arch", C.c_int),
+        ("mlp_type", C.c_int), ("norm_type", C.c_int), ("rope_partial_dims", C.c_int),
+        ("has_q_bias", C.c_bool), ("has_k_bias", C.c_bool), ("has_v_bias", C.c_bool),
+        ("has_post_attn_norm", C.c_bool), ("has_post_ffn_norm", C.c_bool),
+        ("has_ffn_bias", C.c_bool),
+    ]
+
+
+class VxModel(C.Structure):
+    _fields_ = [("config", VxModelConfig), ("tensors", C.c_void_p), ("n_tensors", C.c_int),
+                ("tensor_data", C.c_void_p)] + [
+        (n, C.c_void_p) for n in (
+            "tok_embd", "attn_q", "attn_k", "attn_v", "attn_o", "attn_q_bias", "attn_k_bias",
+            "attn_v_bias", "ffn_gate", "ffn_up", "ffn_down", "ffn_gate_bias", "ffn_up_bias",
+            "ffn_down_bias", "attn_norm", "ffn_norm", "attn_norm_bias", "ffn_norm_bias",
+            "norm_w", "norm_bias_w", "output_w", "layer_predictors", "attn_pattern_predictor",
+            "token_exit_predictor", "k_cache", "v_cache")
+    ] + [("cache_len", C.c_int), ("scratch", C.c_void_p), ("scratch_size", C.c_size_t),
+         ("dequant_tmp", C.c_void_p), ("dequant_tmp_size", C.c_size_t),
+         ("tokenizer", C.c_void_p)]
+
+
+class VxModelDev(C.Structure):
+    """The product's vx_model: the reference layout plus the appended `dev`."""
+    _fields_ = VxModel._fields_ + [("dev", C.c_void_p)]
+
+
+class OrMat(C.Structure):
+    _fields_ = [("type", C.c_int), ("data", C.c_void_p), ("rows", C.c_int), ("cols", C.c_int)]
+
+
+class OrModel(C.Structure):
+    _fields_ = [
+        ("n_layers", C.c_int), ("n_heads", C.c_int), ("n_kv_heads", C.c_int), ("n_embd", C.c_int),
+        ("n_head_dim", C.c_int), ("n_ff", C.c_int), ("n_vocab", C.c_int), ("n_ctx", C.c_int),
+        ("rope_theta", C.c_float), ("q4_mode", C.c_int), ("attn_cap", C.c_int),
+        ("attn_o_inplace", C.c_int), ("gate_thr", C.c_float), ("wscale", C.c_float),
+        ("tok_embd", OrMat), ("output", OrMat), ("out_norm", C.c_void_p), ("has_out_norm", C.c_int),
+        ("wq", C.c_void_p), ("wk", C.c_void_p), ("wv", C.c_void_p), ("wo", C.c_void_p),
+        ("wg", C.c_void_p), ("wu", C.c_void_p), ("wd", C.c_void_p),
+        ("attn_norm", C.c_void_p), ("ffn_norm", C.c_void_p),
+        ("bq", C.c_void_p), ("bk", C.c_void_p), ("bv", C.c_void_p),
+        ("k_cache", C.c_void_p), ("v_cache", C.c_void_p), ("cache_len", C.c_int),
+    ]
+
+
+# --------------------------------------------------------------------------
+# loaders
+# --------------------------------------------------------------------------
+_libs = {}
+
+
+def oracle():
+    if "oracle" not in _libs:
+        L = C.CDLL(ORACLE_SO)
+        L.or_fp16_to_fp32.restype = C.c_float
+        L.or_fp16_to_fp32.argtypes = [C.c_uint16]
+        L.or_fp32_to_fp16.restype = C.c_uint16
+        L.or_fp32_to_fp16.argtypes = [C.c_float]
+        for n in ("or_quantize_row_q4_0",):
+            getattr(L, n).argtypes = [f32p, C.c_void_p, C.c_int]
+        for n in ("or_dequantize_row_q4_0", "or_dequantize_row_q8_0"):
+            getattr(L, n).argtypes = [C.c_void_p, f32p, C.c_int, C.c_float]
+        for n in ("or_gemv_q4_0", "or_gemv_q4_0_avx2lanes"):
+            getattr(L, n).argtypes = [C.c_void_p, f32p, f32p, C.c_int, C.c_int]
+        for n in ("or_gemv_q4_0_sparse_rows", "or_gemv_q4_0_avx2lanes_sparse_rows"):
+            getattr(L, n).argtypes = [C.c_void_p, f32p, f32p, C.c_int, C.c_int, f32p, C.c_float]
+        for n in ("or_gemv_f32", "or_gemv_f32_avx2lanes"):
+            getattr(L, n).argtypes = [f32p, f32p, f32p, C.c_int, C.c_int]
+        L.or_gemv_f32_sparse_rows.argtypes = [f32p, f32p, f32p, C.c_int, C.c_int, f32p, C.c_float]
+        L.or_rms_norm.argtypes = [f32p, f32p, f32p, C.c_int]
+        L.or_softmax.argtypes = [f32p, C.c_int]
+        L.or_silu.argtypes = [f32p, C.c_int]
+        L.or_rope.argtypes = [f32p, f32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float]
+        L.or_forward.argtypes = [C.POINTER(OrModel), i32p, C.c_int, f32p]
+        L.or_forward_all.argtypes = [C.POINTER(OrModel), i32p, C.c_int, f32p]
+        L.or_argmax.restype = C.c_int
+        L.or_argmax.argtypes = [f32p, C.c_int]
+        L.or_softmax_temp.argtypes = [f32p, C.c_int, C.c_float, f32p]
+        L.or_sample_top_p.restype = C.c_int
+        L.or_sample_top_p.argtypes = [f32p, C.c_int, C.c_float, C.c_float, C.c_float, C.c_void_p]
+        L.or_inverse_cdf_fixed.restype = C.c_int
+        L.or_inverse_cdf_fixed.argtypes = [f32p, C.c_int, C.c_float]
+        L.or_accept_greedy.restype = C.c_int
+        L.or_accept_greedy.argtypes = [f32p, C.c_int, i32p, C.c_int, i32p]
+        L.or_accept_sampled.restype = C.c_int
+        L.or_accept_sampled.argtypes = [f32p, C.c_int, f32p, C.c_int, i32p, C.c_int, C.c_float,
+                                        f32p, i32p, C.POINTER(C.c_int)]
+        _libs["oracle"] = L
+    return _libs["oracle"]
+
+
+def ref_available(kind="scalar"):
+    return os.path.exists(REF_SO[kind])
+
+
+def ref(kind="scalar"):
+    key = "ref_" + kind
+    if key not in _libs:
+        L = C.CDLL(REF_SO[kind])
+        L.vx_fp16_to_fp32.restype = C.c_float
+        L.vx_fp16_to_fp32.argtypes = [C.c_uint16]
+        L.vx_fp32_to_fp16.restype = C.c_uint16
+        L.vx_fp32_to_fp16.argtypes = [C.c_float]
+        L.vx_quantize_row_q4_0.argtypes = [f32p, C.c_void_p, C.c_int]
+        L.vx_dequantize_row_q4_0.argtypes = [C.c_void_p, f32p, C.c_int]
+        L.vx_dequantize_row_q8_0.argtypes = [C.c_void_p, f32p, C.c_int]
+        L.vx_set_synthetic_weight_scale.argtypes = [C.c_float]
+        L.vx_gemv_q4_0.argtypes = [C.c_void_p, f32p, f32p, C.c_int, C.c_int]
+        L.vx_gemv_q4_0_sparse_rows.argtypes = [C.c_void_p, f32p, f32p, C.c_int, C.c_int, f32p, C.c_float]
+        L.vx_gemv_f32.argtypes = [f32p, f32p, f32p, C.c_int, C.c_int]
+        L.vx_rms_norm.argtypes = [f32p, f32p, f32p, C.c_int]
+        L.vx_softmax.argtypes = [f32p, C.c_int]
+        L.vx_silu.argtypes = [f32p, C.c_int]
+        L.vx_rope.argtypes = [f32p, f32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float]
+        L.vx_dot_q4_0.argtypes = [C.c_void_p, f32p, C.POINTER(C.c_float), C.c_int]
+        L.vx_model_create.restype = C.c_int
+        L.vx_model_create.argtypes = [C.c_char_p, C.POINTER(C.POINTER(VxModel))]
+        L.vx_model_destroy.argtypes = [C.POINTER(VxModel)]
+        L.vx_model_forward.restype = C.c_int
+        L.vx_model_forward.argtypes = [C.POINTER(VxModel), i32p, C.c_int, f32p]
+        L.vx_set_n_threads.argtypes = [C.c_int]
+        if kind == "avx2":
+            L.vx_gemv_q4_0_avx2.argtypes = [C.c_void_p, f32p, f32p, C.c_int, C.c_int]
+            L.vx_gemv_q4_0_avx2_sparse_rows.argtypes = [C.c_void_p, f32p, f32p, C.c_int, C.c_int,
+                                                        f32p, C.c_float]
+            L.vx_gemv_f32_avx2.argtypes = [f32p, f32p, f32p, C.c_int, C.c_int]
+        _libs[key] = L
+    return _libs[key]
+
+
+# --------------------------------------------------------------------------
+# data helpers
+# --------------------------------------------------------------------------
+Q4_BLOCK = np.dtype([("d", "<u2"), ("qs", "u1", (16,))])
+Q8_BLOCK = np.dtype([("d", "<u2"), ("qs", "i1", (32,))])
+assert Q4_BLOCK.itemsize == 18 and Q8_BLOCK.itemsize == 34
+
+
+def rand_q4_0(rng, rows, cols, d_std=0.02):
+    """Q4_0 blocks with d = fp16(|N(0, d_std)|) and nibbles uniform 0..15."""
+    nb = cols // 32
+    b = np.zeros((rows, nb), dtype=Q4_BLOCK)
+    b["d"] = np.abs(rng.normal(0.0, d_std, size=(rows, nb))).astype(np.float16).view(np.uint16)
+    b["qs"] = rng.integers(0, 256, size=(rows, nb, 16), dtype=np.uint8)
+    return b
+
+
+def rand_q8_0(rng, rows, cols, d_std=0.02):
+    nb = cols // 32
+    b = np.zeros((rows, nb), dtype=Q8_BLOCK)
+    b["d"] = np.abs(rng.normal(0.0, d_std, size=(rows, nb))).astype(np.float16).view(np.uint16)
+    b["qs"] = rng.integers(-127, 128, size=(rows, nb, 32), dtype=np.int8)
+    return b
+
+
+def q4_values(blocks):
+    """Exact float64 dequantised matrix (rows, cols): d*(s-8), adjacent pairs."""
+    d = blocks["d"].view(np.float16).astype(np.float64)
+    qs = blocks["qs"]
+    s = np.empty(qs.shape[:-1] + (32,), dtype=np.int64)
+    s[..., 0::2] = qs & 15
+    s[..., 1::2] = qs >> 4
+    v = (s - 8) * d[..., None]
+    return v.reshape(blocks.shape[0], -1)
+
+
+def q8_values(blocks):
+    d = blocks["d"].view(np.float16).astype(np.float64)
+    v = blocks["qs"].astype(np.int64) * d[..., None]
+    return v.reshape(blocks.shape[0], -1)
+
+
+def close(a, b, atol=1e-4, rtol=1e-3):
+    """The parity bar for floating-point outputs: |a-b| <= atol + rtol*|b|."""
+    a = np.asarray(a, dtype=np.float64)
+    b = np.asarray(b, dtype=np.float64)
+    return bool(np.all(np.abs(a - b) <= atol + rtol * np.abs(b)))
+
+
+def max_violation(a, b, atol=1e-4, rtol=1e-3):
+    a = np.asarray(a, dtype=np.float64)
+    b = np.asarray(b, dtype=np.float64)
+    return float(np.max((np.abs(a - b) - (atol + rtol * np.abs(b)))))

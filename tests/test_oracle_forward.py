@@ -1,0 +1,113 @@
+"""Pin the oracle's composed forward (oracle/oracle.c or_forward) against the
+reference engine's own vx_model_forward (src/model.c:391-628), built from its
+sources without AVX2 (oracle/_ref/libvxref_scalar.so), one OpenMP thread.
+
+The reference calls attn_o in place (src/model.c:544); with one thread that is
+a deterministic row-by-row recurrence, which the oracle reproduces under
+attn_o_inplace=1.  With attn_o_inplace=0 (the engine's out-of-place semantics)
+the oracle is compared against the reference on models without an
+attn_output tensor, where the reference skips that product.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+import pytest
+
+import _native as N
+from _gguf import llama_gguf, GGML_Q8_0, GGML_Q4_0
+from _oracle_model import OracleModel
+
+O = N.oracle()
+pytestmark = pytest.mark.skipif(not N.ref_available("scalar"), reason="reference build absent")
+
+
+def ref_forward_logits(path, tokens, n_vocab, n_ctx=None, chunks=None):
+    R = N.ref("scalar")
+    R.vx_set_n_threads(1)
+    mp = C.POINTER(N.VxModel)()
+    err = R.vx_model_create(path.encode(), C.byref(mp))
+    assert err == 0, err
+    if n_ctx is not None:
+        mp.contents.config.n_ctx = n_ctx
+    outs = []
+    try:
+        chunks = chunks or [1] * len(tokens)
+        i = 0
+        for c in chunks:
+            lg = np.zeros(n_vocab, np.float32)
+            t = np.ascontiguousarray(tokens[i:i + c], dtype=np.int32)
+            assert R.vx_model_forward(mp, t, c, lg) == 0
+            outs.append(lg)
+            i += c
+        cfg = mp.contents.config
+        conf = (cfg.n_layers, cfg.n_heads, cfg.n_kv_heads, cfg.n_embd, cfg.n_head_dim, cfg.n_ff,
+                cfg.n_vocab, cfg.n_ctx)
+        return np.stack(outs), conf, mp.contents.cache_len
+    finally:
+        R.vx_model_destroy(mp)
+
+
+CASES = [
+    # layers, d, heads, kv, ff, vocab, attn_output, emb, out
+    (2, 64, 4, 2, 128, 96, True, GGML_Q4_0, GGML_Q4_0),
+    (2, 128, 4, 1, 256, 160, False, GGML_Q4_0, GGML_Q4_0),
+    (1, 96, 3, 3, 192, 64, True, GGML_Q8_0, GGML_Q8_0),
+]
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_oracle_forward_matches_reference(tmp_path, case):
+    L, d, h, kv, ff, V, with_o, et, ot = case
+    rng = np.random.default_rng(sum(case[:6]))
+    path = str(tmp_path / "m.gguf")
+    raw = llama_gguf(path, rng, L, d, h, kv, ff, V, std=0.05, with_attn_output=with_o,
+                     norm_random=True, emb_type=et, out_type=ot)
+    tokens = rng.integers(0, V, 12).astype(np.int32)
+    ref_logits, conf, ref_len = ref_forward_logits(path, tokens, V)
+    assert conf[:7] == (L, h, kv, d, d // h, ff, V)
+    om = OracleModel(raw, L, d, h, kv, ff, V, n_ctx=4096, attn_o_inplace=1)
+    got = np.zeros((len(tokens), V), np.float32)
+    for i, t in enumerate(tokens):
+        assert O.or_forward(om.ptr, np.array([t], np.int32), 1, got[i]) == 0
+    assert om.cache_len == ref_len == len(tokens)
+    assert N.close(got, ref_logits, atol=1e-5, rtol=1e-5), N.max_violation(got, ref_logits, 1e-5, 1e-5)
+    if not with_o:
+        # no attn_output: in-place vs out-of-place is moot, both must agree
+        om2 = OracleModel(raw, L, d, h, kv, ff, V, n_ctx=4096, attn_o_inplace=0)
+        got2 = np.zeros((len(tokens), V), np.float32)
+        O.or_forward_all(om2.ptr, tokens, len(tokens), got2)
+        assert np.array_equal(got2, got)
+
+
+def test_oracle_forward_multi_token_call_and_all(tmp_path):
+    """vx_model_forward with n_tokens > 1 returns the LAST token's logits and
+    advances cache_len by n; or_forward_all's rows equal one-token calls."""
+    rng = np.random.default_rng(21)
+    L, d, h, kv, ff, V = 2, 64, 4, 2, 128, 80
+    path = str(tmp_path / "m.gguf")
+    raw = llama_gguf(path, rng, L, d, h, kv, ff, V, std=0.05, with_attn_output=False)
+    tokens = rng.integers(0, V, 10).astype(np.int32)
+    ref_logits, _, ref_len = ref_forward_logits(path, tokens, V, chunks=[4, 6])
+    om = OracleModel(raw, L, d, h, kv, ff, V, n_ctx=4096)
+    allv = np.zeros((10, V), np.float32)
+    O.or_forward_all(om.ptr, tokens, 10, allv)
+    assert ref_len == 10
+    assert N.close(allv[3], ref_logits[0], atol=1e-5, rtol=1e-5)
+    assert N.close(allv[9], ref_logits[1], atol=1e-5, rtol=1e-5)
+
+
+def test_oracle_forward_context_clamp_and_cap(tmp_path):
+    """Positions beyond n_ctx overwrite slot n_ctx-1 (src/model.c:279-286)."""
+    rng = np.random.default_rng(22)
+    L, d, h, kv, ff, V = 1, 64, 2, 1, 128, 48
+    path = str(tmp_path / "m.gguf")
+    raw = llama_gguf(path, rng, L, d, h, kv, ff, V, std=0.05, with_attn_output=False)
+    tokens = rng.integers(0, V, 9).astype(np.int32)
+    ref_logits, _, ref_len = ref_forward_logits(path, tokens, V, n_ctx=6)
+    om = OracleModel(raw, L, d, h, kv, ff, V, n_ctx=6)
+    got = np.zeros((9, V), np.float32)
+    for i, t in enumerate(tokens):
+        O.or_forward(om.ptr, np.array([t], np.int32), 1, got[i])
+    assert om.cache_len == ref_len
+    assert N.close(got, ref_logits, atol=1e-5, rtol=1e-5)
