@@ -1,0 +1,244 @@
+/*
+ * vxh.h -- the thin C ABI between the engine's C host code (model.c,
+ * speculative.c, quantize.c) and its hand-written gfx950 HIP kernels.
+ *
+ * Plain C: device memory is passed as void* / float* device addresses, sizes
+ * as int / size_t, streams as an opaque handle.  No HIP or torch type appears
+ * here.  Every entry point returns VXH_OK (0) or a negative VXH_ERR_* code;
+ * vxh_last_error() describes the last failure of the calling thread.
+ *
+ * The reference engine has no device layer; these entry points replace the
+ * bodies of its CPU kernels (see the per-group comments for which).
+ */
+#ifndef VXH_H
+#define VXH_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    VXH_OK = 0,
+    VXH_ERR_NODEVICE = -1,
+    VXH_ERR_ALLOC = -2,
+    VXH_ERR_PARAM = -3,
+    VXH_ERR_LAUNCH = -4,
+    VXH_ERR_UNSUPPORTED = -5,
+};
+
+typedef struct vxh_stream_s *vxh_stream;   /* a HIP stream; NULL = the default stream */
+
+/* ---- runtime ------------------------------------------------------------ */
+int vxh_init(void);                               /* idempotent; selects device 0 */
+const char *vxh_last_error(void);
+/* Records a printf-style message for vxh_last_error() and returns code. */
+int vxh_set_error(int code, const char *fmt, ...);
+int vxh_device_name(char *buf, int len);
+int vxh_malloc(void **dptr, size_t bytes);
+int vxh_free(void *dptr);
+int vxh_upload(void *dst, const void *src, size_t bytes, vxh_stream s);
+int vxh_download(void *dst, const void *src, size_t bytes, vxh_stream s);
+int vxh_copy(void *dst, const void *src, size_t bytes, vxh_stream s);
+int vxh_fill_f32(float *dst, float value, size_t n, vxh_stream s);   /* kernel, graph-safe */
+int vxh_stream_create(vxh_stream *s);
+int vxh_stream_destroy(vxh_stream s);
+int vxh_stream_sync(vxh_stream s);
+int vxh_device_sync(void);                         /* waits for every stream */
+
+/* Events on a stream, for timing the launches recorded between them. */
+typedef struct vxh_event_s *vxh_event;
+int vxh_event_create(vxh_event *e);
+int vxh_event_destroy(vxh_event e);
+int vxh_event_record(vxh_event e, vxh_stream s);
+int vxh_event_elapsed_ms(vxh_event start, vxh_event stop, float *ms);
+
+/* Graph capture of a stream's launches (no memset nodes are ever recorded). */
+typedef struct vxh_graph_s *vxh_graph;
+int vxh_capture_begin(vxh_stream s);
+int vxh_capture_end(vxh_stream s, vxh_graph *g);
+int vxh_graph_launch(vxh_graph g, vxh_stream s);
+int vxh_graph_destroy(vxh_graph g);
+
+/* ---- quantised matrices in HBM --------------------------------------------
+ * Replaces the row-major GGUF block arrays the reference's GEMV kernels read
+ * (src/simd/avx2.c:324, src/quantize.c:738).  Rows are grouped in tiles of
+ * 32; within a tile the data is stored in the order one wavefront consumes
+ * it, so every weight load of a wavefront is a contiguous 1 KiB:
+ *
+ *   Q4_0  qs: [tile][block pair p][lane 64][16 B]   lane l = row (l%32) of the
+ *             tile, half h = l/32; its 16 B are bytes 8h..8h+7 of blocks 2p
+ *             and 2p+1 with the nibbles of each dword permuted so the
+ *             in-register unpack yields elements in natural order.
+ *   Q8_0  qs: [tile][block b][lane 64][16 B]        bytes 16h..16h+15 of block
+ *             b (bytes permuted within each dword).
+ *   both  d : [tile][block pair p][row 32] -> (d[2p], d[2p+1]) as two fp16.
+ *
+ * Byte count equals GGUF's (18 or 34 bytes per 32 weights) apart from padding
+ * rows to a multiple of 32 and blocks to an even count (padding has d = 0). */
+typedef struct {
+    int type;          /* 2 = Q4_0, 8 = Q8_0 (vx_type / GGML ids)           */
+    int n_rows;        /* physical rows, a multiple of 32                     */
+    int n_cols;        /* K, a multiple of 32                                 */
+    int n_pairs;       /* ceil(K/64): block pairs per row                     */
+    void *qs;          /* device                                              */
+    void *d;           /* device                                              */
+} vxh_qmat;
+
+int vxh_qmat_alloc(vxh_qmat *m, int type, int n_rows, int n_cols);
+int vxh_qmat_free(vxh_qmat *m);
+/* Copy n_rows GGUF rows (n_cols/32 blocks each, host or device memory per
+ * `src_on_device`) into the tiled layout.  Logical row r lands on physical
+ * row (r / group) * group_stride + row_offset + r % group; group = n_rows,
+ * group_stride = 0 is a plain copy at row_offset. */
+int vxh_qmat_set_rows(vxh_qmat *m, const void *src, int src_on_device, int n_rows, int group,
+                      int group_stride, int row_offset, vxh_stream s);
+/* Inverse of vxh_qmat_set_rows: rebuild n_rows GGUF rows into host memory. */
+int vxh_qmat_get_rows(const vxh_qmat *m, void *host_dst, int n_rows, int group,
+                      int group_stride, int row_offset, vxh_stream s);
+/* Fill n_rows x n_cols of GGUF blocks on the device with seeded weights
+ * N(0, std^2) (Box-Muller on a splitmix64 counter stream keyed by seed) run
+ * through the Q4_0 writer of the reference (src/quantize.c:88-114) or, for
+ * Q8_0, d = amax/127 rounded to fp16 and q = round(x/d). */
+int vxh_synth_blocks(void *dev_blocks, int type, int n_rows, int n_cols, uint64_t seed,
+                     float std, vxh_stream s);
+/* Gather rows of a tiled matrix as fp32: out[i][:] = scale * dequant(row
+ * ids[i]) for i < n (ids read from device memory; out-of-range ids -> zeros).
+ * Replaces the embedding lookup of src/model.c:454-500. */
+int vxh_qmat_gather_rows(const vxh_qmat *m, const int *dev_ids, int n, float scale,
+                         float *out, int ld_out, vxh_stream s);
+
+/* ---- activation panels -----------------------------------------------------
+ * A GEMM input of M rows (1 <= M <= 16) x K, as the fp16 hi/lo operand the
+ * MFMA kernel reads from LDS: x' = hi + lo with hi = fp16(x'), lo =
+ * fp16(x' - hi), x' = x * 2^-e_m (power-of-two row scale, exact).  Layout [block][mfma s][half h][slot][8 x fp16], slot m =
+ * hi of row m, slot M+m = lo of row m.  AVX2-lane panels hold w_t*x_t (w_t =
+ * 2 when t%8 >= 4) and a per-(block,row) correction, see vxh_prep_panel. */
+typedef struct {
+    void *data;        /* device, vxh_panel_bytes(M, K)                       */
+    float *corr;       /* device, [K/32][M] (AVX2-lane panels)                */
+    float *rscale;     /* device, [M]: row m of the panel holds x * 2^-e_m and
+                          rscale[m] = 2^e_m is applied to the GEMM output, so
+                          max |x * 2^-e_m| < 1 whatever the magnitude of x */
+    float *xs;         /* device, fp32 copy for the dot-product path          */
+    int M, K;
+    int avx2;          /* 1: lane-pattern weights and corrections             */
+} vxh_panel;
+
+size_t vxh_panel_bytes(int M, int K);
+int vxh_panel_alloc(vxh_panel *p, int max_M, int K);
+int vxh_panel_free(vxh_panel *p);
+/* Build a panel from fp32 rows x[M][ldx].  avx2 = 1 applies the lane
+ * pattern of vx_gemv_q4_0_avx2 (src/simd/avx2.c:336-363): per block the
+ * correction is sum of x at offsets 8..11, 16..19, 24..27, 32..35, where
+ * offsets >= K read tail[m][0..3] (tail may be NULL: zeros). */
+int vxh_prep_panel(vxh_panel *p, const float *x, int ldx, int M, int K, int avx2,
+                   const float *tail, int ld_tail, vxh_stream s);
+/* Fused RMSNorm + panel: xn[m] = w .* x[m] / sqrt(mean(x[m]^2) + 1e-5)
+ * (src/tensor.c:128-142; w NULL = ones, src/model.c:253-258), written as a
+ * panel; xn (fp32) is also stored when xn_out != NULL.  In AVX2 mode the
+ * 4-float tail of row m is tail[m][0..3] (NULL: zeros). */
+int vxh_rmsnorm_panel(const float *x, int ldx, int M, int K, const float *w, int avx2,
+                      const float *tail, int ld_tail, vxh_panel *p, float *xn_out, int ld_xn,
+                      vxh_stream s);
+
+/* ---- skinny-M dequant GEMM ---------------------------------------------------
+ * Y[m][n] = sum_k X[m][k] * W[n][k] for m < M, n < N, W quantised, X a panel.
+ * Replaces vx_gemv_q4_0_avx2 / vx_gemv_q4_0 / dequantize+vx_gemv_f32
+ * (src/model.c:203-245) for M rows at once.  Epilogues: */
+enum {
+    VXH_EPI_STORE = 0,    /* y = scale*acc                                         */
+    VXH_EPI_RESID = 1,    /* y = r + scale*acc          (residual add, model.c:546) */
+    VXH_EPI_GATE = 2,     /* y = |g| < thr ? 0 : scale*acc   (src/model.c:169-201)  */
+    VXH_EPI_SWIGLU = 3,   /* rows interleaved 16 gate / 16 up per tile:
+                             h = |silu(g)| < thr ? 0 : silu(g)*u (src/model.c:582-585) */
+};
+typedef struct {
+    int kind;
+    float *y; int ldy;             /* output rows                                   */
+    const float *r; int ldr;       /* residual (RESID) or gate (GATE)               */
+    float thr;
+    float scale;                   /* output multiplier (synthetic weight scale)     */
+    int n_out;                     /* logical output columns (N, or F for SWIGLU)    */
+} vxh_epilogue;
+
+enum { VXH_PATH_AUTO = 0, VXH_PATH_MFMA = 1, VXH_PATH_DOT = 2 };
+
+/* Workspace for split-K partials and arrival counters; one per stream. */
+typedef struct {
+    float *part;
+    size_t part_floats;
+    unsigned *counters;
+    int n_counters;
+} vxh_workspace;
+int vxh_workspace_alloc(vxh_workspace *w, size_t part_floats, int n_counters);
+int vxh_workspace_free(vxh_workspace *w);
+
+int vxh_gemm(const vxh_qmat *W, const vxh_panel *X, int M, const vxh_epilogue *ep,
+             vxh_workspace *ws, int path, vxh_stream s);
+/* Workspace (floats, counters) one vxh_gemm call of this shape needs. */
+size_t vxh_gemm_workspace_floats(int n_rows, int n_cols, int M);
+int vxh_gemm_workspace_counters(int n_rows);
+
+/* ---- attention block ---------------------------------------------------------
+ * RoPE + KV write (src/tensor.c:173-271 portable branch, src/model.c:291-296):
+ * qkv[m] = [q | k | v] (+ optional F32 biases).  Row m sits at position
+ * pos_m = min(n_past + m, n_ctx - 1), rotated at rope position
+ * rope_pos_m = n_past + m; cos/sin come from a host-built table
+ * [n_pos][head_dim/2] (cosf/sinf of pos * (1/powf(theta, 2i/hd))).  Writes the
+ * rotated q to q_out[m] and k, v to the layer's cache rows pos_m. */
+int vxh_rope_kv(const float *qkv, int ld_qkv, int M, int n_past, int n_ctx, int n_heads,
+                int n_kv_heads, int head_dim, const float *bq, const float *bk, const float *bv,
+                const float *cos_tab, const float *sin_tab, int n_pos,
+                float *q_out, float *k_cache_layer, float *v_cache_layer, vxh_stream s);
+/* Causal attention of M rows against the layer's KV cache
+ * (src/model.c:300-338): row m reads positions [0, min(pos_m + 1, cap)),
+ * head h uses kv head h*n_kv/n_heads, softmax with 1/(sum + 1e-10). */
+int vxh_attention(const float *q, int M, int n_past, int n_ctx, int n_heads, int n_kv_heads,
+                  int head_dim, int cap, const float *k_cache_layer,
+                  const float *v_cache_layer, float *out, int ld_out,
+                  vxh_workspace *ws, vxh_stream s);
+
+size_t vxh_attention_workspace_floats(int M, int n_ctx, int cap, int n_heads, int n_kv_heads,
+                                      int head_dim);
+
+/* ---- elementwise ------------------------------------------------------------- */
+/* y[m][i] += x[m][i] for i < n (residual add, src/model.c:546, :589). */
+int vxh_add_rows(float *y, int ldy, const float *x, int ldx, int M, int n, vxh_stream s);
+/* dst[m][i] = src[m][i] for i < n. */
+int vxh_copy_rows(float *dst, int ld_dst, const float *src, int ld_src, int M, int n,
+                  vxh_stream s);
+int vxh_rmsnorm(const float *x, int ldx, int M, int K, const float *w, float *out, int ld_out,
+                vxh_stream s);
+int vxh_fill_rows(float *y, int ld, int M, int col0, int n, float value, vxh_stream s);
+
+/* ---- acceptance ----------------------------------------------------------------
+ * Row statistics of logits L[R][V] at temperature T > 0: max, sum of
+ * exp((l-max)/T) and the first argmax (src/speculative.c:44-53, :93-98).
+ * stats[r] = {max, sum, argmax(as float bits)} (3 floats per row). */
+int vxh_row_stats(const float *L, int ldl, int R, int V, float T, float *stats, vxh_stream s);
+/* Draft sampler (src/speculative.c:35-91): token = inverse CDF at uniform
+ * u_dev[0] over the nucleus of softmax(l/T) (the shortest prefix of tokens
+ * sorted by descending probability, ties by index, whose fixed-point mass
+ * reaches top_p; every token when top_p >= 1), drawn in index order.  T <= 0:
+ * argmax.  Writes the token to token_out[0] and the nucleus descriptor
+ * nuc[0..7] = {max, 1/(sum+1e-30), tau, tie_cut, mass, argmax, 0, 0}: token v
+ * is in the nucleus iff p_v > tau or (p_v == tau and v <= tie_cut); tau < 0
+ * means all tokens. */
+int vxh_sample(const float *l, int V, float T, float top_p, const float *u_dev,
+               int *token_out, float *nuc, vxh_stream s);
+/* Verify decisions for k drafts (src/speculative.c:186-233 on probabilities):
+ * L: target logits [k+1][ldl] with their vxh_row_stats, D: draft logits
+ * [k][ldd] with nucleus descriptors nuc[k][8], drafts[k], uniforms u[k+1]
+ * (device).  T <= 0 = greedy.  Writes out[0] = emitted count, out[1] =
+ * accepted count, out[2..] = emitted tokens. */
+int vxh_accept(const float *L, int ldl, int V, const float *stats, const float *D, int ldd,
+               int Vd, const float *nuc, const int *drafts, int k, float T, const float *u,
+               int *out, vxh_stream s);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -431,7 +431,8 @@ static void apply_norm(float *x, float *tmp, const float *w, int n, float *ones)
 
 /* One head loop of the reference attention (src/model.c:275-341): write k,v at
  * pos = cache_len (clamped to n_ctx-1), then every query head h reads kv head
- * h*n_kv/n_heads over positions [0, min(pos+1, 4096)). */
+ * h*n_kv/n_heads over positions [0, min(pos+1, cap)), cap = 4096 in the
+ * reference (src/model.c:304-305). */
 static void attention(or_model *m, const float *q, const float *k, const float *v,
                       float *out, int layer, float *scores)
 {
@@ -446,7 +447,7 @@ static void attention(or_model *m, const float *q, const float *k, const float *
     memcpy(m->v_cache + loff + (size_t)pos * kvd, v, sizeof(float) * (size_t)kvd);
     memset(out, 0, sizeof(float) * (size_t)nh * hd);
     int cs = cache_size;
-    if (m->attn_cap && cs > 4096) cs = 4096;
+    if (m->attn_cap > 0 && cs > m->attn_cap) cs = m->attn_cap;
     float scale = 1.0f / sqrtf((float)hd);
     for (int h = 0; h < nh; h++) {
         const float *qh = q + (size_t)h * hd;

@@ -70,7 +70,8 @@ typedef struct {
     int n_layers, n_heads, n_kv_heads, n_embd, n_head_dim, n_ff, n_vocab, n_ctx;
     float rope_theta;
     int   q4_mode;           /* OR_Q4_EXACT / OR_Q4_AVX2LANES                    */
-    int   attn_cap;          /* 1: attend to the first min(pos+1, 4096) positions */
+    int   attn_cap;          /* attend to the first min(pos+1, attn_cap) positions;
+                                4096 in the reference, 0 = no cap                  */
     int   attn_o_inplace;    /* 1: reproduce the portable build's in-place attn_o  */
     float gate_thr;          /* FFN up-row skip threshold, 0.01 in the reference  */
     float wscale;            /* synthetic weight scale (dequantize paths)         */

@@ -218,3 +218,153 @@ def max_violation(a, b, atol=1e-4, rtol=1e-3):
     a = np.asarray(a, dtype=np.float64)
     b = np.asarray(b, dtype=np.float64)
     return float(np.max((np.abs(a - b) - (atol + rtol * np.abs(b)))))
+
+
+# --------------------------------------------------------------------------
+# product library
+# --------------------------------------------------------------------------
+class VxModelOptions(C.Structure):
+    _fields_ = [("q4_kernel", C.c_int), ("attn_cap", C.c_int), ("ffn_gate_threshold", C.c_float),
+                ("use_graphs", C.c_int)]
+
+
+class VxSynthSpec(C.Structure):
+    _fields_ = [("seed", C.c_uint64), ("std", C.c_float), ("matrix_type", C.c_int),
+                ("embd_type", C.c_int), ("output_type", C.c_int)]
+
+
+class VxGemmProfile(C.Structure):
+    _fields_ = [("launches", C.c_int), ("ms", C.c_double), ("bytes", C.c_double), ("flops", C.c_double)]
+
+
+class VxSpecStats(C.Structure):
+    _fields_ = [("rounds", C.c_int), ("drafted", C.c_int), ("accepted", C.c_int),
+                ("emitted", C.c_int), ("verify_ms", C.c_double), ("draft_ms", C.c_double),
+                ("prefill_ms", C.c_double)]
+
+
+def product_available():
+    return os.path.exists(PRODUCT_SO)
+
+
+def product():
+    if "product" not in _libs:
+        L = C.CDLL(PRODUCT_SO)
+        L.vx_last_error.restype = C.c_char_p
+        L.vxh_last_error.restype = C.c_char_p
+        L.vxh_init.restype = C.c_int
+        L.vx_fp16_to_fp32.restype = C.c_float
+        L.vx_fp16_to_fp32.argtypes = [C.c_uint16]
+        L.vx_fp32_to_fp16.restype = C.c_uint16
+        L.vx_fp32_to_fp16.argtypes = [C.c_float]
+        L.vx_quantize_row_q4_0.argtypes = [f32p, C.c_void_p, C.c_int]
+        L.vx_quantized_size.restype = C.c_size_t
+        L.vx_quantized_size.argtypes = [C.c_int, C.c_int]
+        L.vx_dequantize_row_q4_0.argtypes = [C.c_void_p, f32p, C.c_int]
+        L.vx_dequantize_row_q8_0.argtypes = [C.c_void_p, f32p, C.c_int]
+        L.vx_set_synthetic_weight_scale.argtypes = [C.c_float]
+        L.vx_dot_q4_0.argtypes = [C.c_void_p, f32p, C.POINTER(C.c_float), C.c_int]
+        for n in ("vx_gemv_q4_0", "vx_gemv_q4_0_avx2"):
+            getattr(L, n).argtypes = [C.c_void_p, f32p, f32p, C.c_int, C.c_int]
+        for n in ("vx_gemv_q4_0_sparse_rows", "vx_gemv_q4_0_avx2_sparse_rows"):
+            getattr(L, n).argtypes = [C.c_void_p, f32p, f32p, C.c_int, C.c_int, f32p, C.c_float]
+        L.vx_gemm_q4_0.restype = C.c_int
+        L.vx_gemm_q4_0.argtypes = [C.c_void_p, f32p, C.c_int, f32p, C.c_int, C.c_int, C.c_int, C.c_int]
+        L.vx_gemm_q8_0.restype = C.c_int
+        L.vx_gemm_q8_0.argtypes = [C.c_void_p, f32p, C.c_int, f32p, C.c_int, C.c_int, C.c_int]
+        L.vx_model_create.restype = C.c_int
+        L.vx_model_create.argtypes = [C.c_char_p, C.POINTER(C.POINTER(VxModelDev))]
+        L.vx_model_create_synthetic.restype = C.c_int
+        L.vx_model_create_synthetic.argtypes = [C.POINTER(VxModelConfig), C.POINTER(VxSynthSpec),
+                                                C.POINTER(C.POINTER(VxModelDev))]
+        L.vx_model_destroy.argtypes = [C.POINTER(VxModelDev)]
+        L.vx_model_forward.restype = C.c_int
+        L.vx_model_forward.argtypes = [C.POINTER(VxModelDev), i32p, C.c_int, f32p]
+        L.vx_model_verify.restype = C.c_int
+        L.vx_model_verify.argtypes = [C.POINTER(VxModelDev), i32p, C.c_int, f32p]
+        L.vx_model_kv_truncate.argtypes = [C.POINTER(VxModelDev), C.c_int]
+        L.vx_model_get_options.argtypes = [C.POINTER(VxModelDev), C.POINTER(VxModelOptions)]
+        L.vx_model_set_options.restype = C.c_int
+        L.vx_model_set_options.argtypes = [C.POINTER(VxModelDev), C.POINTER(VxModelOptions)]
+        L.vx_model_read_tensor.restype = C.c_int
+        L.vx_model_read_tensor.argtypes = [C.POINTER(VxModelDev), C.c_char_p, C.c_void_p, C.c_size_t]
+        L.vx_model_read_kv.restype = C.c_int
+        L.vx_model_read_kv.argtypes = [C.POINTER(VxModelDev), C.c_int, C.c_int, f32p, f32p]
+        L.vx_speculative_create.restype = C.c_void_p
+        L.vx_speculative_create.argtypes = [C.POINTER(VxModelDev), C.POINTER(VxModelDev), C.c_int]
+        L.vx_speculative_destroy.argtypes = [C.c_void_p]
+        L.vx_speculative_set_temp.argtypes = [C.c_void_p, C.c_float, C.c_float]
+        L.vx_speculative_set_seed.argtypes = [C.c_void_p, C.c_uint64]
+        L.vx_speculative_generate.restype = C.c_int
+        L.vx_speculative_generate.argtypes = [C.c_void_p, i32p, C.c_int, i32p, C.c_int]
+        L.vx_speculative_prefill.restype = C.c_int
+        L.vx_speculative_prefill.argtypes = [C.c_void_p, i32p, C.c_int]
+        L.vx_speculative_decode.restype = C.c_int
+        L.vx_speculative_decode.argtypes = [C.c_void_p, i32p, C.c_int]
+        L.vx_model_set_profiling.argtypes = [C.POINTER(VxModelDev), C.c_int]
+        L.vx_model_get_profile.restype = C.c_int
+        L.vx_model_get_profile.argtypes = [C.POINTER(VxModelDev), C.c_void_p]
+        L.vxh_device_sync.restype = C.c_int
+        L.vx_speculative_get_stats.argtypes = [C.c_void_p, C.POINTER(VxSpecStats)]
+        L.vx_speculative_set_trace.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int]
+        L.vx_uniform.restype = C.c_float
+        L.vx_uniform.argtypes = [C.c_uint64, C.c_uint64, C.c_uint64]
+        _libs["product"] = L
+    return _libs["product"]
+
+
+def product_error():
+    return product().vx_last_error().decode(errors="replace")
+
+
+def bind_vxh(L):
+    """argtypes for the device-pointer C ABI (include/vxh.h) used by tests."""
+    vp = C.c_void_p
+    L.vxh_malloc.argtypes = [C.POINTER(vp), C.c_size_t]
+    L.vxh_free.argtypes = [vp]
+    L.vxh_upload.argtypes = [vp, vp, C.c_size_t, vp]
+    L.vxh_download.argtypes = [vp, vp, C.c_size_t, vp]
+    L.vxh_row_stats.argtypes = [vp, C.c_int, C.c_int, C.c_int, C.c_float, vp, vp]
+    L.vxh_sample.argtypes = [vp, C.c_int, C.c_float, C.c_float, vp, vp, vp, vp]
+    L.vxh_accept.argtypes = [vp, C.c_int, C.c_int, vp, vp, C.c_int, C.c_int, vp, vp, C.c_int,
+                             C.c_float, vp, vp, vp]
+    L.vxh_stream_sync.argtypes = [vp]
+    return L
+
+
+class DevBuf:
+    """A device buffer mirroring a numpy array (upload on creation)."""
+
+    def __init__(self, L, arr=None, nbytes=None):
+        self.L = L
+        self.ptr = C.c_void_p()
+        n = arr.nbytes if arr is not None else nbytes
+        assert L.vxh_malloc(C.byref(self.ptr), n) == 0, L.vxh_last_error()
+        self.nbytes = n
+        if arr is not None:
+            a = np.ascontiguousarray(arr)
+            assert L.vxh_upload(self.ptr, a.ctypes.data_as(C.c_void_p), n, None) == 0
+
+    def get(self, dtype, count):
+        out = np.zeros(count, dtype)
+        assert self.L.vxh_download(out.ctypes.data_as(C.c_void_p), self.ptr, out.nbytes, None) == 0
+        return out
+
+    def free(self):
+        if self.ptr:
+            self.L.vxh_free(self.ptr)
+            self.ptr = C.c_void_p()
+
+
+def parity(gpu, oracle, exact, atol=1e-4, rtol=1e-3):
+    """The floating-point parity bar.  Elementwise |gpu - oracle| <= atol +
+    rtol*|oracle|; where the oracle's own fp32 rounding error against the fp64
+    exact value already exceeds that bar (large-magnitude dot products with
+    near-zero results), the element passes only if the GPU is at least as
+    close to the exact value as the oracle is.  Returns (ok, n_fallback)."""
+    g = np.asarray(gpu, np.float64)
+    o = np.asarray(oracle, np.float64)
+    e = np.asarray(exact, np.float64)
+    ok_bar = np.abs(g - o) <= atol + rtol * np.abs(o)
+    ok_fb = np.abs(g - e) <= np.abs(o - e)
+    return bool(np.all(ok_bar | ok_fb)), int(np.count_nonzero(~ok_bar))

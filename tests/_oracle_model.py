@@ -29,7 +29,7 @@ class OracleModel:
     """
 
     def __init__(self, weights, n_layers, n_embd, n_heads, n_kv_heads, n_ff, n_vocab, n_ctx,
-                 rope_theta=10000.0, q4_mode=0, attn_cap=1, attn_o_inplace=0, gate_thr=0.01,
+                 rope_theta=10000.0, q4_mode=0, attn_cap=4096, attn_o_inplace=0, gate_thr=0.01,
                  wscale=1.0):
         self.keep = []
         hd = n_embd // n_heads

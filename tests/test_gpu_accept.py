@@ -1,0 +1,179 @@
+"""GPU acceptance sampling (vxh_row_stats / vxh_sample / vxh_accept) against
+the oracle on identical logits and uniforms.
+
+Decisions must be identical.  A difference is accepted only as a certified
+tie: the uniform sits within 1e-5 of the acceptance ratio, or the fixed-point
+CDF threshold sits within 1e-6 of the mass of a token boundary -- places where
+the last-ulp differences of expf between the GPU and the host libm may flip
+the outcome.  Every such case is counted and reported.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import _native as N
+
+pytestmark = pytest.mark.gpu
+O = N.oracle()
+
+
+@pytest.fixture(scope="module")
+def P():
+    if not N.product_available():
+        pytest.fail("product library not built")
+    L = N.bind_vxh(N.product())
+    assert L.vxh_init() == 0, L.vxh_last_error()
+    return L
+
+
+def fixed(w):
+    w = np.asarray(w, np.float64)
+    return np.where(w > 0, np.floor(w * 2.0 ** 32 + 0.5), 0).astype(np.uint64)
+
+
+def near_boundary(w, u):
+    """True when the inverse-CDF threshold of u lies within 1e-6 of the total
+    mass of a prefix boundary (a certified tie)."""
+    W = fixed(w)
+    S = int(W.sum())
+    if S == 0:
+        return False
+    U = int(np.float32(u) * np.float32(16777216.0))
+    thr = max(1, (U * S + 16777215) >> 24)
+    c = np.cumsum(W.astype(np.float64))
+    return bool(np.min(np.abs(c - thr)) <= 1e-6 * S + 2)
+
+
+def sample_gpu(P, l, T, top_p, u):
+    V = l.shape[0]
+    dl, du = N.DevBuf(P, l), N.DevBuf(P, np.array([u], np.float32))
+    dt, dn = N.DevBuf(P, nbytes=4), N.DevBuf(P, nbytes=32)
+    assert P.vxh_sample(dl.ptr, V, T, top_p, du.ptr, dt.ptr, dn.ptr, None) == 0, P.vxh_last_error()
+    tok = int(dt.get(np.int32, 1)[0])
+    nuc = dn.get(np.float32, 8)
+    for b in (dl, du, dt, dn):
+        b.free()
+    return tok, nuc
+
+
+@pytest.mark.parametrize("V,T,top_p", [(32000, 0.8, 1.0), (32000, 1.0, 0.9), (5000, 0.7, 0.5),
+                                       (152064, 1.0, 1.0), (152064, 1.0, 0.95), (1000, 0.0, 1.0)])
+def test_sampler_matches_oracle(P, V, T, top_p):
+    print(f"sampler V={V} T={T} top_p={top_p}", flush=True)
+    rng = np.random.default_rng(V + int(T * 10) + int(top_p * 100))
+    ties = boundary = 0
+    for trial in range(6):
+        l = (rng.normal(0, 2.0, V)).astype(np.float32)
+        for u in rng.integers(0, 1 << 24, 4) / float(1 << 24):
+            u = float(np.float32(u))
+            q = np.zeros(V, np.float32)
+            want = O.or_sample_top_p(l, V, T, top_p, u, q.ctypes.data_as(C.c_void_p))
+            got, nuc = sample_gpu(P, l, T, top_p, u)
+            if got != want:
+                w = np.where(q > 0, q, 0)
+                assert near_boundary(w, u), (trial, u, got, want)
+                ties += 1
+            if T > 0 and top_p < 1.0:
+                # nucleus membership from the GPU descriptor equals the oracle's
+                p = np.zeros(V, np.float32)
+                O.or_softmax_temp(l, V, T, p)
+                tau, tie = nuc[2], nuc[3:4].view(np.int32)[0]
+                member = (p > tau) | ((p == tau) & (np.arange(V) <= tie))
+                diff = member != (q > 0)
+                # a sequential fp32 sum over V terms (the reference's softmax)
+                # carries ~sqrt(V)*6e-8 relative error, which moves the top-p
+                # boundary by a few tokens of near-equal probability: every
+                # differing token must sit at the boundary value
+                if np.any(diff):
+                    rel = np.abs(p[diff].astype(np.float64) - tau) / tau
+                    assert np.all(rel < 1e-3), (np.count_nonzero(diff), rel.max())
+                    boundary += 1
+    print(f"certified draw ties: {ties}; draws with boundary-only nucleus differences: {boundary}")
+    assert ties <= 2
+
+
+def run_accept(P, L, D, drafts, T, top_p, u):
+    k = D.shape[0]
+    V, Vd = L.shape[1], D.shape[1]
+    dL, dD = N.DevBuf(P, L), N.DevBuf(P, D)
+    dstats = N.DevBuf(P, nbytes=4 * 3 * (k + 1))
+    dnuc = N.DevBuf(P, nbytes=4 * 8 * max(k, 1))
+    ddr = N.DevBuf(P, np.asarray(drafts, np.int32))
+    du1 = N.DevBuf(P, nbytes=4)
+    dtok = N.DevBuf(P, nbytes=4)
+    dout = N.DevBuf(P, nbytes=4 * (k + 3))
+    # nucleus descriptors of the draft rows via the sampler (draws discarded)
+    for j in range(k):
+        P.vxh_upload(du1.ptr, np.array([0.5], np.float32).ctypes.data_as(C.c_void_p), 4, None)
+        row = C.c_void_p(dD.ptr.value + j * Vd * 4)
+        nj = C.c_void_p(dnuc.ptr.value + j * 32)
+        assert P.vxh_sample(row, Vd, T, top_p, du1.ptr, dtok.ptr, nj, None) == 0
+    du = N.DevBuf(P, np.asarray(u, np.float32))
+    assert P.vxh_row_stats(dL.ptr, V, k + 1, V, T, dstats.ptr, None) == 0
+    assert P.vxh_accept(dL.ptr, V, V, dstats.ptr, dD.ptr, Vd, Vd, dnuc.ptr, ddr.ptr, k, T, du.ptr,
+                        dout.ptr, None) == 0, P.vxh_last_error()
+    out = dout.get(np.int32, k + 3)
+    for b in (dL, dD, dstats, dnuc, ddr, du1, dtok, dout, du):
+        b.free()
+    return int(out[0]), int(out[1]), list(out[2:2 + out[0]])
+
+
+def oracle_accept(L, D, drafts, T, top_p, u):
+    k, Vd = D.shape
+    V = L.shape[1]
+    Q = np.zeros((k, Vd), np.float32)
+    for j in range(k):
+        O.or_sample_top_p(np.ascontiguousarray(D[j]), Vd, T, top_p, 0.5, Q[j].ctypes.data_as(C.c_void_p))
+    out = np.zeros(k + 1, np.int32)
+    na = C.c_int()
+    if T > 0:
+        n = O.or_accept_sampled(np.ascontiguousarray(L.ravel()), V, np.ascontiguousarray(Q.ravel()), Vd,
+                                np.asarray(drafts, np.int32), k, T, np.asarray(u, np.float32), out,
+                                C.byref(na))
+    else:
+        n = O.or_accept_greedy(np.ascontiguousarray(L.ravel()), V, np.asarray(drafts, np.int32), k, out)
+        na.value = n - 1
+    return n, na.value, list(out[:n]), Q
+
+
+@pytest.mark.parametrize("V,k,T,top_p", [(32000, 8, 0.8, 1.0), (32000, 4, 1.0, 0.95), (2000, 8, 0.8, 1.0),
+                                         (32000, 8, 0.0, 1.0), (152064, 8, 1.0, 1.0)])
+def test_accept_matches_oracle(P, V, k, T, top_p):
+    print(f"accept V={V} k={k} T={T} top_p={top_p}", flush=True)
+    rng = np.random.default_rng(V + k)
+    ties, n_acc_total, n_cases = 0, 0, 12
+    for case in range(n_cases):
+        L = rng.normal(0, 1.5, (k + 1, V)).astype(np.float32)
+        # drafts close to the target so that some, not all, drafts are accepted
+        D = (L[:k] + rng.normal(0, 0.3 + 0.2 * (case % 4), (k, V))).astype(np.float32)
+        drafts = []
+        for j in range(k):
+            if T > 0:
+                drafts.append(O.or_sample_top_p(np.ascontiguousarray(D[j]), V, T, top_p,
+                                                float(rng.integers(0, 1 << 24) / float(1 << 24)), None))
+            else:
+                am = int(np.argmax(L[j]))
+                drafts.append(am if rng.random() < 0.8 else (am + 1) % V)
+        u = (rng.integers(0, 1 << 24, k + 1) / float(1 << 24)).astype(np.float32)
+        g = run_accept(P, L, D, drafts, T, top_p, u)
+        n, na, toks, Q = oracle_accept(L, D, drafts, T, top_p, u)
+        n_acc_total += na
+        if (g[0], g[1], g[2]) != (n, na, toks):
+            # certify: ratio test tie or CDF-boundary tie at the decision that differs
+            j = min(g[1], na)
+            p = np.zeros(V, np.float32)
+            O.or_softmax_temp(np.ascontiguousarray(L[j]), V, T, p)
+            if j < k:
+                alpha = min(1.0, p[drafts[j]] / max(Q[j][drafts[j]], 1e-10))
+                tie = abs(float(u[j]) - alpha) < 1e-5
+                if not tie and g[1] == na:
+                    tie = near_boundary(np.maximum(0, p - Q[j]), float(u[k]))
+            else:
+                tie = near_boundary(p, float(u[k]))
+            assert tie, (case, g, (n, na, toks))
+            ties += 1
+    print(f"accepted {n_acc_total} of {k * n_cases} drafts; certified ties {ties}")
+    assert ties <= 1
+    if T > 0:
+        assert 0 < n_acc_total < k * n_cases

@@ -1,0 +1,144 @@
+"""GPU parity of the dequant GEMM / GEMV entry points against the oracle.
+
+Bar: |gpu - oracle| <= 1e-4 + 1e-3*|oracle| elementwise (floating point, the
+north-star tolerance); dequantisation and repacking are bit-exact.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import _native as N
+from _native import close, max_violation
+
+pytestmark = pytest.mark.gpu
+O = N.oracle()
+
+
+@pytest.fixture(scope="module")
+def P():
+    if not N.product_available():
+        pytest.fail("product library not built (run __graft_entry__.build())")
+    L = N.product()
+    assert L.vxh_init() == 0, L.vxh_last_error()
+    return L
+
+
+def oracle_rows(fn, W, X, rows, cols):
+    out = np.zeros((X.shape[0], rows), np.float32)
+    for m in range(X.shape[0]):
+        fn(N._ptr(W), np.ascontiguousarray(X[m]), out[m], rows, cols)
+    return out
+
+
+SHAPES = [(32, 64, 1), (96, 128, 5), (100, 96, 9), (130, 2048, 3), (256, 4096, 16),
+          (4096, 4096, 5), (11008, 4096, 9), (4096, 11008, 9), (512, 3584, 7), (64, 5632, 2)]
+
+
+@pytest.mark.parametrize("rows,cols,M", SHAPES)
+def test_gemm_q4_0_exact(P, rows, cols, M):
+    print(f"gemm_q4_0 exact rows={rows} cols={cols} M={M}", flush=True)
+    rng = np.random.default_rng(rows * 7 + cols + M)
+    W = N.rand_q4_0(rng, rows, cols)
+    X = rng.normal(0, 1, (M, cols)).astype(np.float32)
+    Y = np.zeros((M, rows), np.float32)
+    assert P.vx_gemm_q4_0(N._ptr(W), X, cols, Y, M, rows, cols, 0) == 0, N.product_error()
+    ref = oracle_rows(O.or_gemv_q4_0, W, X, rows, cols)
+    exact = X.astype(np.float64) @ N.q4_values(W).T
+    ok, nfb = N.parity(Y, ref, exact)
+    assert ok, max_violation(Y, ref)
+    print(f"elements on the exact-value fallback: {nfb}")
+    assert close(Y, exact, atol=2e-5, rtol=2e-5), max_violation(Y, exact, 2e-5, 2e-5)
+
+
+@pytest.mark.parametrize("rows,cols,M", SHAPES[:7])
+def test_gemm_q4_0_avx2_lanes(P, rows, cols, M):
+    print(f"gemm_q4_0 avx2 rows={rows} cols={cols} M={M}", flush=True)
+    rng = np.random.default_rng(rows * 5 + cols + M)
+    W = N.rand_q4_0(rng, rows, cols)
+    X = rng.normal(0, 1, (M, cols + 4)).astype(np.float32)   # 4-float tails are read
+    Y = np.zeros((M, rows), np.float32)
+    assert P.vx_gemm_q4_0(N._ptr(W), X, cols + 4, Y, M, rows, cols, 1) == 0, N.product_error()
+    ref = oracle_rows(O.or_gemv_q4_0_avx2lanes, W, X, rows, cols)
+    assert close(Y, ref), max_violation(Y, ref)
+
+
+@pytest.mark.parametrize("rows,cols,M", [(64, 128, 1), (300, 2048, 9), (4096, 11008, 5), (1000, 3584, 16)])
+def test_gemm_q8_0(P, rows, cols, M):
+    print(f"gemm_q8_0 rows={rows} cols={cols} M={M}", flush=True)
+    rng = np.random.default_rng(rows + cols * 3 + M)
+    W = N.rand_q8_0(rng, rows, cols)
+    X = rng.normal(0, 1, (M, cols)).astype(np.float32)
+    Y = np.zeros((M, rows), np.float32)
+    assert P.vx_gemm_q8_0(N._ptr(W), X, cols, Y, M, rows, cols) == 0, N.product_error()
+    A = np.zeros(rows * cols, np.float32)
+    O.or_dequantize_row_q8_0(N._ptr(W), A, rows * cols, 1.0)
+    A = A.reshape(rows, cols)
+    ref = np.zeros((M, rows), np.float32)
+    for m in range(M):
+        O.or_gemv_f32(ref[m], A, np.ascontiguousarray(X[m]), rows, cols)
+    exact = X.astype(np.float64) @ N.q8_values(W).T
+    ok, nfb = N.parity(Y, ref, exact)
+    assert ok, max_violation(Y, ref)
+    print(f"elements on the exact-value fallback: {nfb}")
+
+
+def test_gemv_entry_points(P):
+    rng = np.random.default_rng(31)
+    rows, cols = 200, 1024
+    W = N.rand_q4_0(rng, rows, cols)
+    x = rng.normal(0, 1, cols + 4).astype(np.float32)
+    y = np.zeros(rows, np.float32)
+    r = np.zeros(rows, np.float32)
+    P.vx_gemv_q4_0(N._ptr(W), x, y, rows, cols)
+    O.or_gemv_q4_0(N._ptr(W), x, r, rows, cols)
+    assert close(y, r)
+    gate = rng.normal(0, 0.02, rows).astype(np.float32)
+    P.vx_gemv_q4_0_sparse_rows(N._ptr(W), x, y, rows, cols, gate, 0.01)
+    O.or_gemv_q4_0_sparse_rows(N._ptr(W), x, r, rows, cols, gate, 0.01)
+    assert close(y, r) and np.all(y[np.abs(gate) < 0.01] == 0)
+    P.vx_gemv_q4_0_avx2(N._ptr(W), x, y, rows, cols)
+    O.or_gemv_q4_0_avx2lanes(N._ptr(W), x, r, rows, cols)
+    assert close(y, r)
+    P.vx_gemv_q4_0_avx2_sparse_rows(N._ptr(W), x, y, rows, cols, gate, 0.01)
+    O.or_gemv_q4_0_avx2lanes_sparse_rows(N._ptr(W), x, r, rows, cols, gate, 0.01)
+    assert close(y, r)
+    d = C.c_float()
+    P.vx_dot_q4_0(N._ptr(W[0]), x, C.byref(d), cols)
+    assert close([d.value], [r[0] if False else float(N.q4_values(W[:1])[0] @ x[:cols].astype(np.float64))])
+
+
+def test_dequantize_rows_bitexact(P):
+    rng = np.random.default_rng(32)
+    for scale in (1.0, 0.5):
+        P.vx_set_synthetic_weight_scale(scale)
+        for n in (32, 96, 4096):
+            W = N.rand_q4_0(rng, 1, n)
+            a = np.zeros(n, np.float32)
+            b = np.zeros(n, np.float32)
+            P.vx_dequantize_row_q4_0(N._ptr(W), a, n)
+            O.or_dequantize_row_q4_0(N._ptr(W), b, n, scale)
+            assert np.array_equal(a, b)
+            W8 = N.rand_q8_0(rng, 1, n)
+            P.vx_dequantize_row_q8_0(N._ptr(W8), a, n)
+            O.or_dequantize_row_q8_0(N._ptr(W8), b, n, scale)
+            assert np.array_equal(a, b)
+    P.vx_set_synthetic_weight_scale(1.0)
+
+
+def test_gemm_zero_and_one_hot(P):
+    # one-hot activations pick one dequantised column exactly; all-8 nibbles give zero
+    rng = np.random.default_rng(33)
+    rows, cols = 64, 256
+    W = N.rand_q4_0(rng, rows, cols)
+    X = np.zeros((3, cols), np.float32)
+    X[0, 0], X[1, 77], X[2, 255] = 1.0, 1.0, 1.0
+    Y = np.zeros((3, rows), np.float32)
+    assert P.vx_gemm_q4_0(N._ptr(W), X, cols, Y, 3, rows, cols, 0) == 0
+    vals = N.q4_values(W)
+    assert np.array_equal(Y[0].astype(np.float64), vals[:, 0])
+    assert np.array_equal(Y[1].astype(np.float64), vals[:, 77])
+    assert np.array_equal(Y[2].astype(np.float64), vals[:, 255])
+    W["qs"][:] = 0x88
+    X = rng.normal(0, 1, (2, cols)).astype(np.float32)
+    assert P.vx_gemm_q4_0(N._ptr(W), X, cols, Y[:2].copy(), 2, rows, cols, 0) == 0

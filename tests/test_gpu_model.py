@@ -1,0 +1,204 @@
+"""GPU parity of the model forward / batched verify against the oracle.
+
+Models are small random-init Llama GGUFs written by tests/_gguf.py.  The
+oracle runs the reference data flow token by token (oracle/oracle.c
+or_forward, pinned against the reference engine in test_oracle_forward.py);
+the GPU runs the same tokens in batches.  Bar: logits within
+1e-4 + 1e-3*|ref|; greedy argmax identical unless the top-2 gap is < 1e-4.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import _native as N
+from _gguf import llama_gguf, GGML_Q8_0, GGML_Q4_0
+from _native import close, max_violation
+from _oracle_model import OracleModel
+
+pytestmark = pytest.mark.gpu
+O = N.oracle()
+
+
+@pytest.fixture(scope="module")
+def P():
+    if not N.product_available():
+        pytest.fail("product library not built")
+    L = N.product()
+    assert L.vxh_init() == 0, L.vxh_last_error()
+    return L
+
+
+class GpuModel:
+    def __init__(self, P, path, n_ctx=None, q4_kernel=0, cap=4096):
+        self.P = P
+        self.mp = C.POINTER(N.VxModelDev)()
+        rc = P.vx_model_create(path.encode(), C.byref(self.mp))
+        assert rc == 0, (rc, N.product_error())
+        if n_ctx is not None:
+            self.mp.contents.config.n_ctx = n_ctx
+        opt = N.VxModelOptions()
+        P.vx_model_get_options(self.mp, C.byref(opt))
+        opt.q4_kernel = q4_kernel
+        opt.attn_cap = cap
+        assert P.vx_model_set_options(self.mp, C.byref(opt)) == 0
+        self.V = self.mp.contents.config.n_vocab
+
+    def forward(self, toks):
+        lg = np.zeros(self.V, np.float32)
+        t = np.ascontiguousarray(toks, np.int32)
+        assert self.P.vx_model_forward(self.mp, t, len(t), lg) == 0, N.product_error()
+        return lg
+
+    def verify(self, toks):
+        t = np.ascontiguousarray(toks, np.int32)
+        lg = np.zeros((len(t), self.V), np.float32)
+        assert self.P.vx_model_verify(self.mp, t, len(t), lg) == 0, N.product_error()
+        return lg
+
+    @property
+    def cache_len(self):
+        return self.mp.contents.cache_len
+
+    def close(self):
+        self.P.vx_model_destroy(self.mp)
+
+
+def make(tmp_path, seed, L=2, d=128, h=4, kv=2, ff=256, V=300, **kw):
+    rng = np.random.default_rng(seed)
+    path = str(tmp_path / f"m{seed}.gguf")
+    raw = llama_gguf(path, rng, L, d, h, kv, ff, V, std=0.05, norm_random=True, **kw)
+    return path, raw, (L, d, h, kv, ff, V)
+
+
+@pytest.mark.parametrize("q4_kernel", [0, 1])
+def test_forward_token_by_token(P, tmp_path, q4_kernel):
+    print(f"forward token-by-token q4_kernel={q4_kernel}", flush=True)
+    path, raw, (L, d, h, kv, ff, V) = make(tmp_path, 41)
+    g = GpuModel(P, path, q4_kernel=q4_kernel)
+    om = OracleModel(raw, L, d, h, kv, ff, V, n_ctx=4096, q4_mode=q4_kernel)
+    rng = np.random.default_rng(1)
+    toks = rng.integers(0, V, 20).astype(np.int32)
+    try:
+        for i, t in enumerate(toks):
+            a = g.forward([t])
+            b = np.zeros(V, np.float32)
+            O.or_forward(om.ptr, np.array([t], np.int32), 1, b)
+            assert close(a, b), (i, max_violation(a, b))
+        assert g.cache_len == om.cache_len == 20
+    finally:
+        g.close()
+
+
+@pytest.mark.parametrize("q4_kernel", [0, 1])
+def test_verify_batch_matches_sequential(P, tmp_path, q4_kernel):
+    """Batched verify of k+1 rows after a prefix == teacher-forced sequential
+    single-token forwards of the oracle (the reference verify semantics)."""
+    print(f"verify batch q4_kernel={q4_kernel}", flush=True)
+    path, raw, (L, d, h, kv, ff, V) = make(tmp_path, 42, L=3, d=256, h=8, kv=2, ff=512, V=500)
+    g = GpuModel(P, path, q4_kernel=q4_kernel)
+    om = OracleModel(raw, L, d, h, kv, ff, V, n_ctx=4096, q4_mode=q4_kernel)
+    rng = np.random.default_rng(2)
+    prefix = rng.integers(0, V, 37).astype(np.int32)
+    block = rng.integers(0, V, 9).astype(np.int32)
+    try:
+        g.forward(prefix)                      # batched prefill (16 + 16 + 5)
+        got = g.verify(block)
+        ref_all = np.zeros((37 + 9, V), np.float32)
+        O.or_forward_all(om.ptr, np.concatenate([prefix, block]), 46, ref_all)
+        ref = ref_all[37:]
+        assert close(got, ref), max_violation(got, ref)
+        for j in range(9):
+            top = np.sort(ref[j])[-2:]
+            if top[1] - top[0] > 1e-4:
+                assert got[j].argmax() == ref[j].argmax()
+        assert g.cache_len == 46
+        # KV cache contents match the oracle's
+        kvd = kv * (d // h)
+        for l in range(L):
+            k = np.zeros(46 * kvd, np.float32)
+            v = np.zeros(46 * kvd, np.float32)
+            assert P.vx_model_read_kv(g.mp, l, 46, k, v) == 0
+            off = l * 4096 * kvd
+            assert close(k, om.k_cache[off:off + 46 * kvd])
+            assert close(v, om.v_cache[off:off + 46 * kvd])
+    finally:
+        g.close()
+
+
+def test_q8_embedding_output_and_no_attn_output(P, tmp_path):
+    path, raw, (L, d, h, kv, ff, V) = make(tmp_path, 43, L=2, d=96, h=3, kv=3, ff=192, V=200,
+                                           emb_type=GGML_Q8_0, out_type=GGML_Q8_0,
+                                           with_attn_output=False)
+    g = GpuModel(P, path)
+    om = OracleModel(raw, L, d, h, kv, ff, V, n_ctx=4096)
+    toks = np.random.default_rng(3).integers(0, V, 12).astype(np.int32)
+    try:
+        got = g.verify(toks)
+        ref = np.zeros((12, V), np.float32)
+        O.or_forward_all(om.ptr, toks, 12, ref)
+        assert close(got, ref), max_violation(got, ref)
+    finally:
+        g.close()
+
+
+def test_context_clamp(P, tmp_path):
+    """Tokens past n_ctx overwrite the last slot (src/model.c:279-286)."""
+    path, raw, (L, d, h, kv, ff, V) = make(tmp_path, 44, L=1, d=64, h=2, kv=1, ff=128, V=64)
+    g = GpuModel(P, path, n_ctx=6)
+    om = OracleModel(raw, L, d, h, kv, ff, V, n_ctx=6)
+    toks = np.random.default_rng(4).integers(0, V, 9).astype(np.int32)
+    try:
+        got = g.verify(toks)
+        ref = np.zeros((9, V), np.float32)
+        O.or_forward_all(om.ptr, toks, 9, ref)
+        assert close(got, ref), max_violation(got, ref)
+        assert g.cache_len == om.cache_len
+    finally:
+        g.close()
+
+
+def test_attention_cap(P, tmp_path):
+    """Attention reads only the first `cap` positions (src/model.c:304-305)."""
+    path, raw, (L, d, h, kv, ff, V) = make(tmp_path, 45, L=1, d=64, h=4, kv=2, ff=128, V=80)
+    g = GpuModel(P, path, cap=8)
+    om = OracleModel(raw, L, d, h, kv, ff, V, n_ctx=4096, attn_cap=8)
+    toks = np.random.default_rng(5).integers(0, V, 21).astype(np.int32)
+    try:
+        got = g.verify(toks)
+        ref = np.zeros((21, V), np.float32)
+        O.or_forward_all(om.ptr, toks, 21, ref)
+        assert close(got, ref), max_violation(got, ref)
+    finally:
+        g.close()
+
+
+def test_read_tensor_roundtrip(P, tmp_path):
+    path, raw, (L, d, h, kv, ff, V) = make(tmp_path, 46, L=1, d=64, h=2, kv=1, ff=96, V=70)
+    g = GpuModel(P, path)
+    try:
+        for name in ("token_embd.weight", "output.weight", "blk.0.attn_q.weight", "blk.0.attn_k.weight",
+                     "blk.0.attn_v.weight", "blk.0.attn_output.weight", "blk.0.ffn_gate.weight",
+                     "blk.0.ffn_up.weight", "blk.0.ffn_down.weight"):
+            want = raw[name]
+            buf = np.zeros(want.nbytes, np.uint8)
+            assert P.vx_model_read_tensor(g.mp, name.encode(), N._ptr(buf), buf.nbytes) == 0, name
+            assert buf.tobytes() == want.tobytes(), name
+    finally:
+        g.close()
+
+
+def test_kv_truncate_and_reverify(P, tmp_path):
+    """Rolling cache_len back and re-running positions reproduces the logits."""
+    path, raw, (L, d, h, kv, ff, V) = make(tmp_path, 47)
+    g = GpuModel(P, path)
+    toks = np.random.default_rng(6).integers(0, V, 14).astype(np.int32)
+    try:
+        g.forward(toks[:5])
+        a = g.verify(toks[5:14])
+        P.vx_model_kv_truncate(g.mp, 5)
+        assert g.cache_len == 5
+        b = g.verify(toks[5:14])
+        assert np.array_equal(a, b)
+    finally:
+        g.close()

@@ -1,0 +1,44 @@
+// Internal helpers shared by the HIP translation units of the engine.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "vxh.h"
+
+typedef _Float16 vx_half2 __attribute__((ext_vector_type(2)));
+typedef _Float16 vx_half8 __attribute__((ext_vector_type(8)));
+typedef float vx_f32x16 __attribute__((ext_vector_type(16)));
+
+// Records a message for vxh_last_error() and returns `code`.
+#define vxh_fail vxh_set_error
+
+#define VXH_CHECK(expr)                                                              \
+    do {                                                                             \
+        hipError_t e_ = (expr);                                                      \
+        if (e_ != hipSuccess)                                                        \
+            return vxh_fail(e_ == hipErrorOutOfMemory ? VXH_ERR_ALLOC : VXH_ERR_LAUNCH, \
+                            "%s: %s (%s:%d)", #expr, hipGetErrorString(e_), __FILE__,   \
+                            __LINE__);                                               \
+    } while (0)
+
+#define VXH_LAUNCHED()                                                               \
+    do {                                                                             \
+        hipError_t e_ = hipGetLastError();                                           \
+        if (e_ != hipSuccess)                                                        \
+            return vxh_fail(VXH_ERR_LAUNCH, "launch: %s (%s:%d)", hipGetErrorString(e_), \
+                            __FILE__, __LINE__);                                     \
+    } while (0)
+
+static inline hipStream_t vxh_hs(vxh_stream s) { return (hipStream_t)s; }
+
+// Number of 16-byte panel units per block of 32 columns for M rows:
+// 2 MFMA halves (s) x 2 lane halves (h) x 2M slots.
+static inline int vxh_panel_units_per_block(int M) { return 2 * 2 * 2 * M; }
+
+__device__ __forceinline__ float vx_half_bits_to_float(uint32_t bits16)
+{
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}

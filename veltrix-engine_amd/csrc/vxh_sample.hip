@@ -1,0 +1,373 @@
+// Vocab-wide softmax statistics, the draft sampler and the verify decisions
+// (ratio test, residual resample, bonus draw) of speculative decoding.
+//
+// Probabilities follow the reference's sampler arithmetic
+// (src/speculative.c:44-53): p_v = expf((l_v - max)/T) * (1/(sum + 1e-30)).
+// Every draw is an inverse CDF over 2^32 fixed-point masses
+// W_v = round(w_v * 2^32): the first v whose prefix sum reaches
+// max(1, ceil(U*S/2^24)) for the uniform u = U/2^24.  Integer prefix sums do
+// not depend on the summation order, so the GPU and a sequential CPU pick the
+// same token from the same w.
+#include "vxh_internal.h"
+
+#define SB 1024   // threads per sampling workgroup
+
+__device__ __forceinline__ uint64_t vx_fixed32(float w)
+{
+    if (!(w > 0.0f)) return 0ull;
+    return (uint64_t)((double)w * 4294967296.0 + 0.5);
+}
+
+// --- workgroup reductions (SB threads, 16 waves) ----------------------------
+__device__ __forceinline__ float vx_wg_max(float v, float *red)
+{
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float r = red[0];
+    for (int i = 1; i < SB / 64; i++) r = fmaxf(r, red[i]);
+    __syncthreads();
+    return r;
+}
+
+__device__ __forceinline__ float vx_wg_sum(float v, float *red)
+{
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float r = 0.0f;
+    for (int i = 0; i < SB / 64; i++) r += red[i];
+    __syncthreads();
+    return r;
+}
+
+__device__ __forceinline__ uint64_t vx_shfl_xor_u64(uint64_t v, int o)
+{
+    uint32_t lo = __shfl_xor((uint32_t)v, o, 64), hi = __shfl_xor((uint32_t)(v >> 32), o, 64);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ uint64_t vx_wg_sum_u64(uint64_t v, uint64_t *red)
+{
+    for (int o = 32; o > 0; o >>= 1) v += vx_shfl_xor_u64(v, o);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    uint64_t r = 0;
+    for (int i = 0; i < SB / 64; i++) r += red[i];
+    __syncthreads();
+    return r;
+}
+
+// First index of the maximum (strict '>' scan order, src/speculative.c:93-98).
+__device__ __forceinline__ int vx_wg_argmax(float v, int idx, float *redv, int *redi)
+{
+    for (int o = 32; o > 0; o >>= 1) {
+        float ov = __shfl_xor(v, o, 64);
+        int oi = __shfl_xor(idx, o, 64);
+        if (ov > v || (ov == v && oi < idx)) { v = ov; idx = oi; }
+    }
+    if ((threadIdx.x & 63) == 0) { redv[threadIdx.x >> 6] = v; redi[threadIdx.x >> 6] = idx; }
+    __syncthreads();
+    float bv = redv[0];
+    int bi = redi[0];
+    for (int i = 1; i < SB / 64; i++)
+        if (redv[i] > bv || (redv[i] == bv && redi[i] < bi)) { bv = redv[i]; bi = redi[i]; }
+    __syncthreads();
+    return bi;
+}
+
+// Thread t owns the contiguous index range [t*chunk, min((t+1)*chunk, n)).
+// Returns the first index whose inclusive prefix of W reaches thr (n-1 if none).
+template <typename WF>
+__device__ int vx_wg_find_prefix(int n, uint64_t thr, WF W, uint64_t *scan, int *res)
+{
+    const int chunk = (n + SB - 1) / SB;
+    const int b = threadIdx.x * chunk, e = min(b + chunk, n);
+    uint64_t local = 0;
+    for (int v = b; v < e; v++) local += W(v);
+    scan[threadIdx.x] = local;
+    if (threadIdx.x == 0) *res = n - 1;
+    __syncthreads();
+    // inclusive scan over SB entries (Hillis-Steele in shared memory)
+    for (int o = 1; o < SB; o <<= 1) {
+        uint64_t add = threadIdx.x >= o ? scan[threadIdx.x - o] : 0ull;
+        __syncthreads();
+        scan[threadIdx.x] += add;
+        __syncthreads();
+    }
+    uint64_t before = threadIdx.x ? scan[threadIdx.x - 1] : 0ull;
+    uint64_t after = scan[threadIdx.x];
+    if (before < thr && after >= thr) {
+        uint64_t c = before;
+        for (int v = b; v < e; v++) {
+            c += W(v);
+            if (c >= thr) { *res = v; break; }
+        }
+    }
+    __syncthreads();
+    int r = *res;
+    __syncthreads();
+    return r;
+}
+
+__device__ __forceinline__ uint64_t vx_threshold(float u, uint64_t S)
+{
+    uint64_t U = (uint64_t)(u * 16777216.0f);
+    uint64_t t = (U * S + 16777215ull) >> 24;
+    return t ? t : 1ull;
+}
+
+// ---------------------------------------------------------------------------
+// row statistics: stats[r] = {max, sum exp((l-max)/T), argmax}
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(SB) void vx_row_stats_kernel(const float *__restrict__ L, int ldl, int V,
+                                                          float T, float *__restrict__ stats)
+{
+    __shared__ float redv[SB / 64];
+    __shared__ int redi[SB / 64];
+    const float *l = L + (size_t)blockIdx.x * ldl;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int v = threadIdx.x; v < V; v += SB) {
+        float x = l[v];
+        if (x > bv || (x == bv && v < bi)) { bv = x; bi = v; }
+    }
+    int am = vx_wg_argmax(bv, bi, redv, redi);
+    float mx = l[am];
+    float s = 0.0f;
+    if (T > 0.0f)
+        for (int v = threadIdx.x; v < V; v += SB) s += expf((l[v] - mx) / T);
+    s = vx_wg_sum(s, redv);
+    if (threadIdx.x == 0) {
+        stats[blockIdx.x * 3 + 0] = mx;
+        stats[blockIdx.x * 3 + 1] = s;
+        stats[blockIdx.x * 3 + 2] = __int_as_float(am);
+    }
+}
+
+extern "C" int vxh_row_stats(const float *L, int ldl, int R, int V, float T, float *stats,
+                             vxh_stream s)
+{
+    if (R <= 0) return VXH_OK;
+    vx_row_stats_kernel<<<R, SB, 0, vxh_hs(s)>>>(L, ldl, V, T, stats);
+    VXH_LAUNCHED();
+    return VXH_OK;
+}
+
+// ---------------------------------------------------------------------------
+// draft sampler
+// nuc = {max, inv, tau, tie_cut (int bits), mass, argmax (int bits), 0, 0}:
+// member(v) = p_v > tau || (p_v == tau && v <= tie_cut); tau < 0: all tokens.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float vx_prob(const float *l, int v, float mx, float inv, float T)
+{
+    return expf((l[v] - mx) / T) * inv;
+}
+
+__global__ __launch_bounds__(SB) void vx_sample_kernel(const float *__restrict__ l, int V, float T,
+                                                       float top_p, const float *__restrict__ u,
+                                                       int *__restrict__ token_out,
+                                                       float *__restrict__ nuc)
+{
+    __shared__ float redv[SB / 64];
+    __shared__ int redi[SB / 64];
+    __shared__ uint64_t red64[SB / 64];
+    __shared__ uint64_t scan[SB];
+    __shared__ int res;
+
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int v = threadIdx.x; v < V; v += SB) {
+        float x = l[v];
+        if (x > bv || (x == bv && v < bi)) { bv = x; bi = v; }
+    }
+    const int am = vx_wg_argmax(bv, bi, redv, redi);
+    if (!(T > 0.0f)) {
+        if (threadIdx.x == 0) {
+            token_out[0] = am;
+            nuc[0] = l[am]; nuc[1] = 0.0f; nuc[2] = -1.0f; nuc[3] = __int_as_float(V - 1);
+            nuc[4] = 0.0f; nuc[5] = __int_as_float(am); nuc[6] = 0.0f; nuc[7] = 0.0f;
+        }
+        return;
+    }
+    const float mx = l[am];
+    float s = 0.0f;
+    for (int v = threadIdx.x; v < V; v += SB) s += expf((l[v] - mx) / T);
+    s = vx_wg_sum(s, redv);
+    const float inv = 1.0f / (s + 1e-30f);
+
+    float tau = -1.0f;
+    int tie_cut = V - 1;
+    if (top_p < 1.0f) {
+        const uint64_t TP = (uint64_t)ceil((double)top_p * 4294967296.0);
+        // largest probability value tau with mass(p >= tau) >= TP (bisection
+        // over the bit patterns of non-negative floats, which are ordered)
+        uint32_t lo = 0u, hi = 0x3F800000u;     // mass(p >= 0) = all >= TP
+        while (lo < hi) {
+            uint32_t mid = lo + (hi - lo + 1) / 2;
+            float t = __uint_as_float(mid);
+            uint64_t acc = 0;
+            for (int v = threadIdx.x; v < V; v += SB) {
+                float p = vx_prob(l, v, mx, inv, T);
+                if (p >= t) acc += vx_fixed32(p);
+            }
+            acc = vx_wg_sum_u64(acc, red64);
+            if (acc >= TP) lo = mid; else hi = mid - 1;
+        }
+        tau = __uint_as_float(lo);
+        uint64_t gt = 0;
+        for (int v = threadIdx.x; v < V; v += SB) {
+            float p = vx_prob(l, v, mx, inv, T);
+            if (p > tau) gt += vx_fixed32(p);
+        }
+        gt = vx_wg_sum_u64(gt, red64);
+        const uint64_t pt = vx_fixed32(tau);
+        if (pt == 0 || gt >= TP) {
+            tie_cut = V - 1;   // cannot happen for tau > 0; keep every tie
+        } else {
+            // ties at tau enter in index order until the mass reaches TP
+            const uint64_t need_units = TP - gt;
+            const uint64_t j = (need_units + pt - 1) / pt;    // number of ties needed
+            tie_cut = vx_wg_find_prefix(V, j, [&](int v) -> uint64_t {
+                return vx_prob(l, v, mx, inv, T) == tau ? 1ull : 0ull;
+            }, scan, &res);
+        }
+        if (tau <= 0.0f) { tau = -1.0f; tie_cut = V - 1; }
+    }
+    auto member_w = [&](int v) -> uint64_t {
+        float p = vx_prob(l, v, mx, inv, T);
+        bool in = tau < 0.0f || p > tau || (p == tau && v <= tie_cut);
+        return in ? vx_fixed32(p) : 0ull;
+    };
+    uint64_t S = 0;
+    for (int v = threadIdx.x; v < V; v += SB) S += member_w(v);
+    S = vx_wg_sum_u64(S, red64);
+    int tok;
+    if (S == 0) tok = am;
+    else tok = vx_wg_find_prefix(V, vx_threshold(u[0], S), member_w, scan, &res);
+    if (threadIdx.x == 0) {
+        token_out[0] = tok;
+        nuc[0] = mx; nuc[1] = inv; nuc[2] = tau; nuc[3] = __int_as_float(tie_cut);
+        nuc[4] = (float)((double)S / 4294967296.0); nuc[5] = __int_as_float(am);
+        nuc[6] = 0.0f; nuc[7] = 0.0f;
+    }
+}
+
+extern "C" int vxh_sample(const float *l, int V, float T, float top_p, const float *u_dev,
+                          int *token_out, float *nuc, vxh_stream s)
+{
+    if (V <= 0) return vxh_fail(VXH_ERR_PARAM, "sample: V %d", V);
+    vx_sample_kernel<<<1, SB, 0, vxh_hs(s)>>>(l, V, T, top_p, u_dev, token_out, nuc);
+    VXH_LAUNCHED();
+    return VXH_OK;
+}
+
+// ---------------------------------------------------------------------------
+// verify decisions
+// ---------------------------------------------------------------------------
+// q_j(v) of the draft: the renormalised nucleus of softmax(D_j/T).
+__device__ __forceinline__ float vx_draft_q(const float *d, const float *nuc, int v, float T)
+{
+    float p = expf((d[v] - nuc[0]) / T) * nuc[1];
+    float tau = nuc[2];
+    int tie = __float_as_int(nuc[3]);
+    bool in = tau < 0.0f || p > tau || (p == tau && v <= tie);
+    return in ? p / nuc[4] : 0.0f;
+}
+
+__global__ __launch_bounds__(SB) void vx_accept_kernel(const float *__restrict__ L, int ldl, int V,
+                                                       const float *__restrict__ stats,
+                                                       const float *__restrict__ D, int ldd, int Vd,
+                                                       const float *__restrict__ nuc,
+                                                       const int *__restrict__ drafts, int k,
+                                                       float T, const float *__restrict__ u,
+                                                       int *__restrict__ out)
+{
+    __shared__ float redv[SB / 64];
+    __shared__ int redi[SB / 64];
+    __shared__ uint64_t red64[SB / 64];
+    __shared__ uint64_t scan[SB];
+    __shared__ int res;
+    __shared__ int s_rej;
+
+    if (!(T > 0.0f)) {
+        // greedy: accept d_j while it is the first argmax of L_j
+        if (threadIdx.x == 0) {
+            int j = 0;
+            for (; j < k; j++) {
+                int a = __float_as_int(stats[j * 3 + 2]);
+                out[2 + j] = a;
+                if (a != drafts[j]) break;
+            }
+            if (j == k) out[2 + k] = __float_as_int(stats[k * 3 + 2]);
+            out[0] = j < k ? j + 1 : k + 1;
+            out[1] = j;
+        }
+        return;
+    }
+    if (threadIdx.x == 0) {
+        int j = 0;
+        for (; j < k; j++) {
+            const float *lj = L + (size_t)j * ldl;
+            const float mx = stats[j * 3 + 0], inv = 1.0f / (stats[j * 3 + 1] + 1e-30f);
+            int d = drafts[j];
+            float pt = (d >= 0 && d < V) ? expf((lj[d] - mx) / T) * inv : 0.0f;
+            float qd = (d >= 0 && d < Vd) ? vx_draft_q(D + (size_t)j * ldd, nuc + j * 8, d, T) : 0.0f;
+            float alpha = fminf(1.0f, pt / fmaxf(qd, 1e-10f));
+            if (!(u[j] < alpha)) break;
+            out[2 + j] = d;
+        }
+        s_rej = j;
+    }
+    __syncthreads();
+    const int j = s_rej;
+    const float *lj = L + (size_t)j * ldl;
+    const float mx = stats[j * 3 + 0], inv = 1.0f / (stats[j * 3 + 1] + 1e-30f);
+    int tok;
+    if (j < k) {
+        const float *dj = D + (size_t)j * ldd;
+        const float *nj = nuc + j * 8;
+        auto resid = [&](int v) -> float {
+            float p = expf((lj[v] - mx) / T) * inv;
+            float q = v < Vd ? vx_draft_q(dj, nj, v, T) : 0.0f;
+            return fmaxf(0.0f, p - q);
+        };
+        auto W = [&](int v) -> uint64_t { return vx_fixed32(resid(v)); };
+        uint64_t S = 0;
+        for (int v = threadIdx.x; v < V; v += SB) S += W(v);
+        S = vx_wg_sum_u64(S, red64);
+        if (S == 0) {
+            float bv = -INFINITY;
+            int bi = 0x7fffffff;
+            for (int v = threadIdx.x; v < V; v += SB) {
+                float r = resid(v);
+                if (r > bv || (r == bv && v < bi)) { bv = r; bi = v; }
+            }
+            tok = vx_wg_argmax(bv, bi, redv, redi);
+        } else {
+            tok = vx_wg_find_prefix(V, vx_threshold(u[k], S), W, scan, &res);
+        }
+    } else {
+        auto W = [&](int v) -> uint64_t { return vx_fixed32(expf((lj[v] - mx) / T) * inv); };
+        uint64_t S = 0;
+        for (int v = threadIdx.x; v < V; v += SB) S += W(v);
+        S = vx_wg_sum_u64(S, red64);
+        if (S == 0) tok = __float_as_int(stats[j * 3 + 2]);
+        else tok = vx_wg_find_prefix(V, vx_threshold(u[k], S), W, scan, &res);
+    }
+    if (threadIdx.x == 0) {
+        out[2 + j] = tok;
+        out[0] = j + 1;
+        out[1] = j;
+    }
+}
+
+extern "C" int vxh_accept(const float *L, int ldl, int V, const float *stats, const float *D,
+                          int ldd, int Vd, const float *nuc, const int *drafts, int k, float T,
+                          const float *u, int *out, vxh_stream s)
+{
+    if (k < 0 || V <= 0) return vxh_fail(VXH_ERR_PARAM, "accept: k %d V %d", k, V);
+    vx_accept_kernel<<<1, SB, 0, vxh_hs(s)>>>(L, ldl, V, stats, D, ldd, Vd, nuc, drafts, k, T, u, out);
+    VXH_LAUNCHED();
+    return VXH_OK;
+}

@@ -1,0 +1,116 @@
+/*
+ * vx_host.h -- internal declarations shared by the engine's C host files.
+ * Not installed; the public surface is the headers in ../../include.
+ */
+#ifndef VX_HOST_H
+#define VX_HOST_H
+
+#include <stdint.h>
+#include <stdio.h>
+
+#include "quantize.h"
+#include "veltrix.h"
+#include "veltrix_gpu.h"
+#include "vxh.h"
+
+#define VX_MAX_BATCH 16
+
+/* ---- errors ----------------------------------------------------------------- */
+void vx_set_error(const char *fmt, ...);
+vx_error vx_from_vxh(int rc);          /* maps VXH_ERR_* -> vx_error, keeps the message */
+int vx_gpu_ready(void);                /* vxh_init() once; 0 or VXH_ERR_*            */
+
+/* ---- GGUF loading (host/gguf.c) ------------------------------------------------- */
+typedef struct {
+    char name[VX_MAX_NAME];
+    int type;                          /* ggml type id                          */
+    int n_dims;
+    int64_t ne[4];
+    const uint8_t *data;               /* points into the file buffer            */
+    size_t nbytes;                     /* bytes available for this tensor        */
+} vx_gguf_tensor;
+
+typedef struct {
+    uint8_t *buf;
+    size_t size;
+    int n_tensors;
+    vx_gguf_tensor *tensors;
+    vx_model_config cfg;
+} vx_gguf;
+
+vx_error vx_gguf_open(const char *path, vx_gguf *g);
+void vx_gguf_close(vx_gguf *g);
+const vx_gguf_tensor *vx_gguf_find(const vx_gguf *g, const char *name);
+/* The arch table / weight-name patterns of the reference (src/format.c:84-203). */
+void vx_apply_arch(vx_model_config *cfg, const char *arch);
+const vx_gguf_tensor *vx_gguf_find_role(const vx_gguf *g, const char *role, int layer);
+
+/* ---- device model state (host/model.c) -------------------------------------------- */
+typedef struct {
+    vxh_qmat wqkv;                     /* rows [q | k | v], d + 2*kvd              */
+    vxh_qmat wo;                       /* d x d, may be absent                     */
+    vxh_qmat wgu;                      /* gate/up, 16-row interleaved tiles        */
+    vxh_qmat wd;                       /* d x F                                    */
+    int has_o;
+    float *attn_norm, *ffn_norm;       /* device F32 or NULL (ones)                */
+    float *bq, *bk, *bv;               /* device F32 biases or NULL                */
+} vx_dev_layer;
+
+typedef struct vx_dev {
+    vxh_stream stream;
+    int n_layers, d, n_heads, n_kv, hd, kvd, F, V;
+    vx_dev_layer *layers;
+    vxh_qmat embd;
+    int has_embd;
+    vxh_qmat out;
+    int has_out, out_rows;
+    float *out_norm;
+    int has_out_norm;
+    /* KV cache and RoPE tables, allocated on first use */
+    int n_ctx_alloc;
+    float *rope_cos, *rope_sin;
+    int n_pos;
+    /* activations, VX_MAX_BATCH rows */
+    int *tok;                          /* [16]                                      */
+    float *x, *xn, *xtail, *qkv, *q, *att, *h, *logits;
+    vxh_panel pan_d, pan_f;
+    vxh_workspace ws;
+    /* sampling buffers */
+    float *stats;                      /* [16][3]                                   */
+    int *acc_out;                      /* [2 + 16]                                  */
+    /* options */
+    vx_model_options opt;
+    /* graphs per batch shape: [M][logit mode] */
+    vxh_graph graphs[VX_MAX_BATCH + 1][3];
+    int graph_pos[VX_MAX_BATCH + 1][3];
+    int *pos_dev;                      /* n_past for graph replays                  */
+    /* GEMM profiling (vx_model_set_profiling) */
+    int prof_on;
+    int prof_n, prof_cap;
+    vxh_event *prof_ev;                /* [2 * prof_cap]                            */
+    int *prof_cls;
+    double *prof_bytes, *prof_flops;
+    vx_gemm_profile prof[VX_PROF_N];
+} vx_dev;
+
+#define VX_LOGITS_NONE 0
+#define VX_LOGITS_LAST 1
+#define VX_LOGITS_ALL 2
+
+/* Runs M <= 16 tokens (device ids in dev->tok) at positions n_past..;
+ * logits land in dev->logits ([M][V] for ALL, row 0 for LAST).  Does not
+ * touch cache_len. */
+vx_error vx_dev_forward(vx_model *m, int M, int n_past, int logits_mode);
+/* Host-token convenience: uploads tokens, runs all batches, advances
+ * cache_len with the reference's clamp rule. */
+vx_error vx_dev_run_tokens(vx_model *m, const int *tokens, int n, int logits_mode,
+                           float *logits_host);
+vx_error vx_dev_ensure_kv(vx_model *m);
+/* Exposed to speculative.c */
+vx_dev *vx_dev_of(const vx_model *m);
+double vx_now_ms(void);
+
+/* ---- splitmix64 uniforms ---------------------------------------------------------- */
+uint64_t vx_splitmix64(uint64_t x);
+
+#endif
