@@ -316,8 +316,9 @@ def run_spec(args):
 
 
 def run_gemm(args):
-    """Isolated verify-shaped GEMMs (configs 1-2 shapes at M = k+1), weights
-    rotated over > 256 MiB so the Infinity Cache does not serve them."""
+    """Isolated verify-shaped GEMM kernels (vxh_gemm_acc) at M = k+1 on the
+    7B shapes, weights rotated over > 300 MB so the Infinity Cache does not
+    serve them."""
     N, P = load_product()
     import ctypes as CC
     vp = CC.c_void_p
@@ -327,11 +328,8 @@ def run_gemm(args):
     L.vxh_qmat_set_rows.argtypes = [vp, vp, CC.c_int, CC.c_int, CC.c_int, CC.c_int, CC.c_int, vp]
     L.vxh_panel_alloc.argtypes = [vp, CC.c_int, CC.c_int]
     L.vxh_prep_panel.argtypes = [vp, vp, CC.c_int, CC.c_int, CC.c_int, CC.c_int, vp, CC.c_int, vp]
-    L.vxh_workspace_alloc.argtypes = [vp, CC.c_size_t, CC.c_int]
-    L.vxh_gemm_workspace_floats.restype = CC.c_size_t
-    L.vxh_gemm_workspace_floats.argtypes = [CC.c_int, CC.c_int, CC.c_int]
-    L.vxh_gemm_workspace_counters.argtypes = [CC.c_int]
-    L.vxh_gemm.argtypes = [vp, vp, CC.c_int, vp, vp, CC.c_int, vp]
+    L.vxh_gemm_acc.argtypes = [vp, vp, CC.c_int, vp, CC.c_int, CC.c_int, CC.c_float, vp, CC.c_int,
+                               CC.c_float, CC.c_int, vp]
     L.vxh_event_create.argtypes = [vp]
     L.vxh_event_record.argtypes = [vp, vp]
     L.vxh_event_elapsed_ms.argtypes = [vp, vp, vp]
@@ -344,17 +342,10 @@ def run_gemm(args):
         _fields_ = [("data", vp), ("corr", vp), ("rscale", vp), ("xs", vp), ("M", CC.c_int),
                     ("K", CC.c_int), ("avx2", CC.c_int)]
 
-    class Epi(CC.Structure):
-        _fields_ = [("kind", CC.c_int), ("y", vp), ("ldy", CC.c_int), ("r", vp), ("ldr", CC.c_int),
-                    ("thr", CC.c_float), ("scale", CC.c_float), ("n_out", CC.c_int)]
-
-    class WS(CC.Structure):
-        _fields_ = [("part", vp), ("part_floats", CC.c_size_t), ("counters", vp), ("n_counters", CC.c_int)]
-
     M = args.k + 1
     results = []
-    for rows, cols, qt in ((4096, 4096, 2), (11008, 4096, 2), (4096, 11008, 2), (22016, 4096, 2),
-                           (11008, 4096, 8), (4096, 11008, 8)):
+    for rows, cols, qt in ((4096, 4096, 2), (12288, 4096, 2), (4096, 11008, 2), (22016, 4096, 2),
+                           (32000, 4096, 2), (11008, 4096, 8), (4096, 11008, 8)):
         bpw = 18 if qt == 2 else 34
         mat_bytes = rows * cols // 32 * bpw
         n_rot = max(2, int(np.ceil(300e6 / mat_bytes)))
@@ -368,25 +359,25 @@ def run_gemm(args):
             mats.append(q)
         stage.free()
         x = N.DevBuf(L, np.random.default_rng(1).normal(0, 1, (M, cols)).astype(np.float32))
-        y = N.DevBuf(L, nbytes=4 * M * rows)
+        acc = N.DevBuf(L, np.zeros(M * rows, np.float64))
         pan = Panel()
         assert L.vxh_panel_alloc(CC.byref(pan), 16, cols) == 0
         assert L.vxh_prep_panel(CC.byref(pan), x.ptr, cols, M, cols, 0, None, 0, None) == 0
-        ws = WS()
-        assert L.vxh_workspace_alloc(CC.byref(ws), L.vxh_gemm_workspace_floats(rows, cols, 16),
-                                     L.vxh_gemm_workspace_counters(rows)) == 0
-        ep = Epi(0, y.ptr, rows, None, 0, 0.0, 1.0, rows)
         e0, e1 = vp(), vp()
         L.vxh_event_create(CC.byref(e0))
         L.vxh_event_create(CC.byref(e1))
+
+        def launch(q):
+            return L.vxh_gemm_acc(CC.byref(q), CC.byref(pan), M, acc.ptr, rows, rows, 1.0, None, 0, 0.0,
+                                  0, None)
         for q in mats:
-            assert L.vxh_gemm(CC.byref(q), CC.byref(pan), M, CC.byref(ep), CC.byref(ws), 0, None) == 0
+            assert launch(q) == 0, L.vxh_last_error()
         reps = args.steps * 10
         L.vxh_device_sync()
         L.vxh_event_record(e0, None)
         for r in range(reps):
             for q in mats:
-                L.vxh_gemm(CC.byref(q), CC.byref(pan), M, CC.byref(ep), CC.byref(ws), 0, None)
+                launch(q)
         L.vxh_event_record(e1, None)
         ms = CC.c_float()
         L.vxh_event_elapsed_ms(e0, e1, CC.byref(ms))

@@ -110,6 +110,9 @@ int vxh_synth_blocks(void *dev_blocks, int type, int n_rows, int n_cols, uint64_
 int vxh_qmat_gather_rows(const vxh_qmat *m, const int *dev_ids, int n, float scale,
                          float *out, int ld_out, vxh_stream s);
 
+/* Longest row a panel or a row kernel takes (elements). */
+#define VXH_MAX_K 24576
+
 /* ---- activation panels -----------------------------------------------------
  * A GEMM input of M rows (1 <= M <= 16) x K, as the fp16 hi/lo operand the
  * MFMA kernel reads from LDS: x' = hi + lo with hi = fp16(x'), lo =
@@ -143,11 +146,49 @@ int vxh_prep_panel(vxh_panel *p, const float *x, int ldx, int M, int K, int avx2
 int vxh_rmsnorm_panel(const float *x, int ldx, int M, int K, const float *w, int avx2,
                       const float *tail, int ld_tail, vxh_panel *p, float *xn_out, int ld_xn,
                       vxh_stream s);
+/* Residual add + RMSNorm + panel: x[m] += (float)acc[m] (the pending output
+ * of a residual GEMM, src/model.c:546, :589; acc is cleared), then as
+ * vxh_rmsnorm_panel on the updated x.  tail_self = 1 takes the AVX2 tail from
+ * the updated x[m][0..3] (src/model.c:425-435). */
+int vxh_resid_rmsnorm_panel(float *x, int ldx, double *acc, int ld_acc, int M, int K,
+                            const float *w, int avx2, int tail_self, vxh_panel *p, float *xn_out,
+                            int ld_xn, vxh_stream s);
+/* SwiGLU + panel: h[m][i] = |silu(g)| < thr ? 0 : silu(g) * u (src/model.c:
+ * 582-585, :169-201) for i < F, with g, u the fp32 roundings of the gate/up
+ * accumulator (tile-interleaved: physical row 32(i/16) + i%16 is gate row i,
+ * 16 rows further is up row i; cleared after reading), written as a panel
+ * (and to h_out when not NULL).  The AVX2 tail of h is zeros. */
+int vxh_swiglu_panel(double *acc, int ld_acc, int M, int F, float thr, int avx2, vxh_panel *p,
+                     float *h_out, int ldh, vxh_stream s);
 
 /* ---- skinny-M dequant GEMM ---------------------------------------------------
  * Y[m][n] = sum_k X[m][k] * W[n][k] for m < M, n < N, W quantised, X a panel.
  * Replaces vx_gemv_q4_0_avx2 / vx_gemv_q4_0 / dequantize+vx_gemv_f32
- * (src/model.c:203-245) for M rows at once.  Epilogues: */
+ * (src/model.c:203-245) for M rows at once.
+ *
+ * vxh_gemm_acc adds scale * Y into an fp64 accumulator acc[M][ld_acc] for
+ * n < n_out.  The K range is split over workgroups whose fp32 partial sums are
+ * added with fp64 atomics; they add exactly, so the result is independent of
+ * arrival order.  gate != NULL leaves acc[m][n] untouched where |gate[m][n]|
+ * < thr (src/model.c:169-201).  The consumers below (and vxh_rope_kv,
+ * vxh_resid_rmsnorm_panel, vxh_swiglu_panel) round the accumulator to fp32
+ * and clear it, so an accumulator that starts zeroed stays zeroed between
+ * uses. */
+enum { VXH_PATH_AUTO = 0, VXH_PATH_MFMA = 1, VXH_PATH_DOT = 2 };
+
+int vxh_gemm_acc(const vxh_qmat *W, const vxh_panel *X, int M, double *acc, int ld_acc,
+                 int n_out, float scale, const float *gate, int ld_gate, float thr, int path,
+                 vxh_stream s);
+/* y[m][i] = (r ? r[m][i] : 0) + (float)acc[m][i] for i < n; acc cleared. */
+int vxh_acc_store(double *acc, int ld_acc, int M, int n, float *y, int ldy, const float *r,
+                  int ldr, vxh_stream s);
+/* h[m][i] = SwiGLU of the tile-interleaved gate/up accumulator (see
+ * vxh_swiglu_panel) for i < F; acc cleared. */
+int vxh_acc_swiglu(double *acc, int ld_acc, int M, int F, float thr, float *h, int ldh,
+                   vxh_stream s);
+
+/* One-call GEMM with an fp32 result: vxh_gemm_acc into the workspace's
+ * accumulator followed by the epilogue: */
 enum {
     VXH_EPI_STORE = 0,    /* y = scale*acc                                         */
     VXH_EPI_RESID = 1,    /* y = r + scale*acc          (residual add, model.c:546) */
@@ -164,38 +205,39 @@ typedef struct {
     int n_out;                     /* logical output columns (N, or F for SWIGLU)    */
 } vxh_epilogue;
 
-enum { VXH_PATH_AUTO = 0, VXH_PATH_MFMA = 1, VXH_PATH_DOT = 2 };
-
-/* Workspace for split-K partials and arrival counters; one per stream. */
+/* Per-stream scratch: the fp64 GEMM accumulator of vxh_gemm (allocated
+ * zeroed, left zeroed by every call) and the attention partials. */
 typedef struct {
+    double *acc;
+    size_t acc_elems;
     float *part;
     size_t part_floats;
-    unsigned *counters;
-    int n_counters;
 } vxh_workspace;
-int vxh_workspace_alloc(vxh_workspace *w, size_t part_floats, int n_counters);
+int vxh_workspace_alloc(vxh_workspace *w, size_t acc_elems, size_t part_floats);
 int vxh_workspace_free(vxh_workspace *w);
+/* Accumulator elements vxh_gemm needs for an n_rows matrix and M rows. */
+size_t vxh_gemm_workspace_elems(int n_rows, int M);
 
 int vxh_gemm(const vxh_qmat *W, const vxh_panel *X, int M, const vxh_epilogue *ep,
              vxh_workspace *ws, int path, vxh_stream s);
-/* Workspace (floats, counters) one vxh_gemm call of this shape needs. */
-size_t vxh_gemm_workspace_floats(int n_rows, int n_cols, int M);
-int vxh_gemm_workspace_counters(int n_rows);
 
 /* ---- attention block ---------------------------------------------------------
  * RoPE + KV write (src/tensor.c:173-271 portable branch, src/model.c:291-296):
- * qkv[m] = [q | k | v] (+ optional F32 biases).  Row m sits at position
+ * qkv[m] = [q | k | v] (+ optional F32 biases), read from the fp64 GEMM
+ * accumulator (rounded to fp32, then cleared).  Row m sits at position
  * pos_m = min(n_past + m, n_ctx - 1), rotated at rope position
  * rope_pos_m = n_past + m; cos/sin come from a host-built table
  * [n_pos][head_dim/2] (cosf/sinf of pos * (1/powf(theta, 2i/hd))).  Writes the
  * rotated q to q_out[m] and k, v to the layer's cache rows pos_m. */
-int vxh_rope_kv(const float *qkv, int ld_qkv, int M, int n_past, int n_ctx, int n_heads,
+int vxh_rope_kv(double *qkv, int ld_qkv, int M, int n_past, int n_ctx, int n_heads,
                 int n_kv_heads, int head_dim, const float *bq, const float *bk, const float *bv,
                 const float *cos_tab, const float *sin_tab, int n_pos,
                 float *q_out, float *k_cache_layer, float *v_cache_layer, vxh_stream s);
 /* Causal attention of M rows against the layer's KV cache
  * (src/model.c:300-338): row m reads positions [0, min(pos_m + 1, cap)),
- * head h uses kv head h*n_kv/n_heads, softmax with 1/(sum + 1e-10). */
+ * head h uses kv head h*n_kv/n_heads, softmax with 1/(sum + 1e-10).  Two
+ * launches: per-chunk partial softmax, then the cross-chunk combine; the
+ * partials live in ws->part.  head_dim: a multiple of 4, at most 128. */
 int vxh_attention(const float *q, int M, int n_past, int n_ctx, int n_heads, int n_kv_heads,
                   int head_dim, int cap, const float *k_cache_layer,
                   const float *v_cache_layer, float *out, int ld_out,

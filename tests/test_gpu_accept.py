@@ -177,3 +177,22 @@ def test_accept_matches_oracle(P, V, k, T, top_p):
     assert ties <= 1
     if T > 0:
         assert 0 < n_acc_total < k * n_cases
+
+
+def test_argmax_of_rows_without_a_maximum_is_index_zero(P):
+    """A row with no value above -inf (all NaN, all -inf) has no first max;
+    the kernels return index 0 (the reference's scan stays on its first
+    element, src/speculative.c:93-98) instead of an index outside the row."""
+    V = 3000
+    rows = np.stack([np.full(V, np.nan, np.float32), np.full(V, -np.inf, np.float32)])
+    dL = N.DevBuf(P, rows)
+    dstats = N.DevBuf(P, nbytes=4 * 3 * 2)
+    assert P.vxh_row_stats(dL.ptr, V, 2, V, 1.0, dstats.ptr, None) == 0, P.vxh_last_error()
+    st = dstats.get(np.float32, 6)
+    assert st[2:3].view(np.int32)[0] == 0 and st[5:6].view(np.int32)[0] == 0
+    for T in (0.0, 1.0):
+        for r in rows:
+            tok, _ = sample_gpu(P, r, T, 1.0, 0.5)
+            assert 0 <= tok < V
+    dL.free()
+    dstats.free()

@@ -3,9 +3,11 @@
 #include "vxh_internal.h"
 
 // ---------------------------------------------------------------------------
-// RoPE + KV write.  One thread per (row, pair) of q and k; v is copied.
+// RoPE + KV write.  One thread per (row, pair) of q and k; v is copied.  The
+// q/k/v rows are read from the fp64 GEMM accumulator, rounded to fp32 (the
+// reference's GEMV output) and cleared.
 // ---------------------------------------------------------------------------
-__global__ void vx_rope_kv_kernel(const float *__restrict__ qkv, int ld_qkv, int M, int n_past,
+__global__ void vx_rope_kv_kernel(double *__restrict__ qkv, int ld_qkv, int M, int n_past,
                                   int n_ctx, int n_heads, int n_kv_heads, int hd,
                                   const float *__restrict__ bq, const float *__restrict__ bk,
                                   const float *__restrict__ bv, const float *__restrict__ cs,
@@ -20,39 +22,40 @@ __global__ void vx_rope_kv_kernel(const float *__restrict__ qkv, int ld_qkv, int
     int m = idx / per_row, r = idx % per_row;
     int rope_pos = n_past + m;
     int pos = rope_pos < n_ctx ? rope_pos : n_ctx - 1;
-    const float *row = qkv + (size_t)m * ld_qkv;
+    double *row = qkv + (size_t)m * ld_qkv;
     if (r < (qd + kvd) / 2) {
         int e = 2 * r;                       // element index within [q | k]
         bool isq = e < qd;
         int el = isq ? e : e - qd;
         int i = (el % hd) / 2;               // pair index within the head
-        float a = row[e], b = row[e + 1];
+        double2 ab = *(const double2 *)(row + e);
+        *(double2 *)(row + e) = make_double2(0.0, 0.0);
+        float a = (float)ab.x, b = (float)ab.y;
         const float *bias = isq ? bq : bk;
         if (bias) { a += bias[el]; b += bias[el + 1]; }
         float c = cs[(size_t)rope_pos * half + i], s = sn[(size_t)rope_pos * half + i];
         float o0 = a * c - b * s;
         float o1 = a * s + b * c;
         if (isq) {
-            q_out[(size_t)m * qd + el] = o0;
-            q_out[(size_t)m * qd + el + 1] = o1;
+            *(float2 *)(q_out + (size_t)m * qd + el) = make_float2(o0, o1);
         } else {
-            kc[(size_t)pos * kvd + el] = o0;
-            kc[(size_t)pos * kvd + el + 1] = o1;
+            *(float2 *)(kc + (size_t)pos * kvd + el) = make_float2(o0, o1);
         }
     } else {
         int el = r - (qd + kvd) / 2;
-        float v = row[qd + kvd + el];
+        float v = (float)row[qd + kvd + el];
+        row[qd + kvd + el] = 0.0;
         if (bv) v += bv[el];
         vc[(size_t)pos * kvd + el] = v;
     }
 }
 
-extern "C" int vxh_rope_kv(const float *qkv, int ld_qkv, int M, int n_past, int n_ctx, int n_heads,
+extern "C" int vxh_rope_kv(double *qkv, int ld_qkv, int M, int n_past, int n_ctx, int n_heads,
                            int n_kv_heads, int head_dim, const float *bq, const float *bk,
                            const float *bv, const float *cos_tab, const float *sin_tab, int n_pos,
                            float *q_out, float *k_cache_layer, float *v_cache_layer, vxh_stream s)
 {
-    if (M < 1 || head_dim % 2 || n_past < 0 || n_past + M - 1 >= n_pos)
+    if (M < 1 || head_dim % 2 || ld_qkv % 2 || n_past < 0 || n_past + M - 1 >= n_pos)
         return vxh_fail(VXH_ERR_PARAM, "rope_kv: M %d n_past %d n_pos %d", M, n_past, n_pos);
     int qd = n_heads * head_dim, kvd = n_kv_heads * head_dim;
     int n = M * ((qd + kvd) / 2 + kvd);
@@ -64,22 +67,23 @@ extern "C" int vxh_rope_kv(const float *qkv, int ld_qkv, int M, int n_past, int 
 }
 
 // ---------------------------------------------------------------------------
-// Verify attention.  Workgroup = (kv head g, chunk of ACH positions).  The
-// G = n_heads/n_kv query heads of the group times the M rows form QM query
-// vectors; K/V rows of the chunk are staged in LDS once and used by all of
-// them.  Each workgroup writes (max, sum, acc[hd]) per query; the last
-// workgroup of the kv head combines the chunks (online-softmax rescale).
+// Verify attention, split over the context.  Workgroup = (kv head g, chunk
+// of ACH positions, query group).  The G = n_heads/n_kv query heads of the
+// kv head times the M rows form QM query vectors; the chunk's K and V rows
+// are loaded once (all loads issued before the first use) into LDS and used
+// by all of them.  Each workgroup writes (max, sum, acc[hd]) per query; a
+// second kernel combines the chunks with the online-softmax rescale.
 // ---------------------------------------------------------------------------
 #define ACH 32
+#define ATT_THREADS 256
+#define ATT_MAX_HD 128
 
-__global__ __launch_bounds__(256) void vx_attention_kernel(
+__global__ __launch_bounds__(ATT_THREADS) void vx_attention_kernel(
     const float *__restrict__ q, int M, int n_past, int n_ctx, int n_heads, int n_kv, int hd,
-    int cap, const float *__restrict__ kc, const float *__restrict__ vc, float *__restrict__ out,
-    int ld_out, int n_chunks, int qpg, int n_qg, float *__restrict__ part,
-    unsigned *__restrict__ counters)
+    int cap, const float *__restrict__ kc, const float *__restrict__ vc, int n_chunks, int qpg,
+    int n_qg, float *__restrict__ part)
 {
     extern __shared__ float sm[];
-    __shared__ int s_last;
     const int per_g = n_chunks * n_qg;
     const int g = blockIdx.x / per_g;
     const int ch = (blockIdx.x % per_g) / n_qg, qg = blockIdx.x % n_qg;
@@ -96,21 +100,39 @@ __global__ __launch_bounds__(256) void vx_attention_kernel(
     float *ss = sv + ACH * hd;            // [nq][ACH]
     const float scale = 1.0f / sqrtf((float)hd);
 
-    for (int i = threadIdx.x; i < nq * hd; i += blockDim.x) {
-        int qi = q0 + i / hd, d = i % hd;
-        int hl = qi / M, m = qi % M;
-        sq[i] = q[(size_t)m * n_heads * hd + (size_t)(g * G + hl) * hd + d];
+    // K/V chunk: ACH*hd/4 float4 each, at most 4 per thread; rows past the
+    // cache end read as zeros (their scores are masked below)
+    constexpr int KV4 = ACH * ATT_MAX_HD / 4 / ATT_THREADS;
+    const int hd4 = hd / 4;
+    float4 kr[KV4], vr[KV4];
+#pragma unroll
+    for (int j = 0; j < KV4; j++) {
+        const int i = j * ATT_THREADS + threadIdx.x;
+        const int t = i / hd4, d4 = i % hd4;
+        const bool ok = t < ACH && t0 + t < n_ctx;
+        const size_t off = (size_t)(t0 + t) * kvd + (size_t)g * hd + 4 * d4;
+        kr[j] = ok ? *(const float4 *)(kc + off) : make_float4(0.f, 0.f, 0.f, 0.f);
+        vr[j] = ok ? *(const float4 *)(vc + off) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    for (int i = threadIdx.x; i < ACH * hd; i += blockDim.x) {
-        int t = i / hd, d = i % hd;
-        int ta = t0 + t;
-        bool ok = ta < n_ctx;
-        sk[t * hdp + d] = ok ? kc[(size_t)ta * kvd + (size_t)g * hd + d] : 0.0f;
-        sv[t * hd + d] = ok ? vc[(size_t)ta * kvd + (size_t)g * hd + d] : 0.0f;
+    for (int i = threadIdx.x; i < nq * hd4; i += ATT_THREADS) {
+        const int ql = i / hd4, d4 = i % hd4;
+        const int qi = q0 + ql, hl = qi / M, m = qi % M;
+        const float4 v = *(const float4 *)(q + (size_t)m * n_heads * hd + (size_t)(g * G + hl) * hd + 4 * d4);
+        *(float4 *)(sq + ql * hd + 4 * d4) = v;
+    }
+#pragma unroll
+    for (int j = 0; j < KV4; j++) {
+        const int i = j * ATT_THREADS + threadIdx.x;
+        const int t = i / hd4, d4 = i % hd4;
+        if (t < ACH) {
+            float *k = sk + t * hdp + 4 * d4;
+            k[0] = kr[j].x; k[1] = kr[j].y; k[2] = kr[j].z; k[3] = kr[j].w;
+            *(float4 *)(sv + t * hd + 4 * d4) = vr[j];
+        }
     }
     __syncthreads();
 
-    for (int i = threadIdx.x; i < nq * ACH; i += blockDim.x) {
+    for (int i = threadIdx.x; i < nq * ACH; i += ATT_THREADS) {
         int ql = i / ACH, t = i % ACH;
         int m = (q0 + ql) % M;
         int pos = n_past + m < n_ctx ? n_past + m : n_ctx - 1;
@@ -129,7 +151,7 @@ __global__ __launch_bounds__(256) void vx_attention_kernel(
     __syncthreads();
 
     float *pstat = part + ((size_t)g * n_chunks + ch) * QM * (hd + 2);
-    for (int ql = threadIdx.x; ql < nq; ql += blockDim.x) {
+    for (int ql = threadIdx.x; ql < nq; ql += ATT_THREADS) {
         float mx = -INFINITY;
         for (int t = 0; t < ACH; t++) mx = fmaxf(mx, ss[ql * ACH + t]);
         float l = 0.0f;
@@ -142,29 +164,28 @@ __global__ __launch_bounds__(256) void vx_attention_kernel(
         pstat[(size_t)(q0 + ql) * (hd + 2) + 1] = l;
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < nq * hd; i += blockDim.x) {
+    for (int i = threadIdx.x; i < nq * hd; i += ATT_THREADS) {
         int ql = i / hd, d = i % hd;
         float a = 0.0f;
         for (int t = 0; t < ACH; t++) a = fmaf(ss[ql * ACH + t], sv[t * hd + d], a);
         pstat[(size_t)(q0 + ql) * (hd + 2) + 2 + d] = a;
     }
+}
 
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        unsigned prev = __hip_atomic_fetch_add(&counters[g], 1u, __ATOMIC_ACQ_REL,
-                                               __HIP_MEMORY_SCOPE_AGENT);
-        s_last = prev == (unsigned)(per_g - 1);
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
+// One workgroup per (row m, head): rescale the chunks' partial results to
+// the global max and normalise by 1/(sum + 1e-10) (src/tensor.c:156-171).
+__global__ void vx_attention_combine_kernel(const float *__restrict__ part, int M, int n_heads,
+                                            int n_kv, int hd, int n_chunks, float *__restrict__ out,
+                                            int ld_out)
+{
+    const int m = blockIdx.x % M, head = blockIdx.x / M;
+    const int G = n_heads / n_kv, QM = G * M;
+    const int g = head / G, hl = head % G;
+    const int qi = hl * M + m;
     const float *pg = part + (size_t)g * n_chunks * QM * (hd + 2);
-    for (int i = threadIdx.x; i < QM * hd; i += blockDim.x) {
-        int qi = i / hd, d = i % hd;
-        int hl = qi / M, m = qi % M;
-        float gm = -INFINITY;
-        for (int c2 = 0; c2 < n_chunks; c2++) gm = fmaxf(gm, pg[((size_t)c2 * QM + qi) * (hd + 2)]);
+    float gm = -INFINITY;
+    for (int c2 = 0; c2 < n_chunks; c2++) gm = fmaxf(gm, pg[((size_t)c2 * QM + qi) * (hd + 2)]);
+    for (int d = threadIdx.x; d < hd; d += blockDim.x) {
         float l = 0.0f, a = 0.0f;
         for (int c2 = 0; c2 < n_chunks; c2++) {
             const float *pc = pg + ((size_t)c2 * QM + qi) * (hd + 2);
@@ -174,9 +195,8 @@ __global__ __launch_bounds__(256) void vx_attention_kernel(
             l = fmaf(f, pc[1], l);
             a = fmaf(f, pc[2 + d], a);
         }
-        out[(size_t)m * ld_out + (size_t)(g * G + hl) * hd + d] = a * (1.0f / (l + 1e-10f));
+        out[(size_t)m * ld_out + (size_t)head * hd + d] = a * (1.0f / (l + 1e-10f));
     }
-    if (threadIdx.x == 0) counters[g] = 0u;
 }
 
 // LDS of a workgroup holding nq queries; the query split keeps it <= 64 KiB.
@@ -207,6 +227,9 @@ extern "C" int vxh_attention(const float *q, int M, int n_past, int n_ctx, int n
 {
     if (M < 1 || n_kv_heads < 1 || n_heads % n_kv_heads)
         return vxh_fail(VXH_ERR_PARAM, "attention: M %d heads %d kv %d", M, n_heads, n_kv_heads);
+    if (head_dim % 4 || head_dim > ATT_MAX_HD)
+        return vxh_fail(VXH_ERR_UNSUPPORTED, "attention: head_dim %d (multiple of 4, <= %d)",
+                        head_dim, ATT_MAX_HD);
     int last = n_past + M - 1 < n_ctx ? n_past + M - 1 : n_ctx - 1;
     int ctx = last + 1;
     if (cap > 0 && ctx > cap) ctx = cap;
@@ -214,16 +237,18 @@ extern "C" int vxh_attention(const float *q, int M, int n_past, int n_ctx, int n
     int G = n_heads / n_kv_heads;
     int QM = G * M;
     int qpg = vx_attn_qpg(head_dim);
-    if (qpg < 1) return vxh_fail(VXH_ERR_UNSUPPORTED, "attention: head_dim %d too large", head_dim);
     if (qpg > QM) qpg = QM;
     int n_qg = (QM + qpg - 1) / qpg;
     size_t need = (size_t)n_kv_heads * n_chunks * QM * (head_dim + 2);
-    if (need > ws->part_floats || n_kv_heads > ws->n_counters)
+    if (need > ws->part_floats)
         return vxh_fail(VXH_ERR_PARAM, "attention workspace too small (%zu floats needed)", need);
     size_t lds = vx_attn_lds(qpg, head_dim);
-    vx_attention_kernel<<<n_kv_heads * n_chunks * n_qg, 256, lds, vxh_hs(s)>>>(
-        q, M, n_past, n_ctx, n_heads, n_kv_heads, head_dim, cap, kc, vc, out, ld_out, n_chunks, qpg,
-        n_qg, ws->part, ws->counters);
+    vx_attention_kernel<<<n_kv_heads * n_chunks * n_qg, ATT_THREADS, lds, vxh_hs(s)>>>(
+        q, M, n_past, n_ctx, n_heads, n_kv_heads, head_dim, cap, kc, vc, n_chunks, qpg, n_qg,
+        ws->part);
+    VXH_LAUNCHED();
+    vx_attention_combine_kernel<<<M * n_heads, head_dim < 64 ? 64 : head_dim, 0, vxh_hs(s)>>>(
+        ws->part, M, n_heads, n_kv_heads, head_dim, n_chunks, out, ld_out);
     VXH_LAUNCHED();
     return VXH_OK;
 }

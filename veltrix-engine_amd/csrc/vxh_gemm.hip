@@ -1,25 +1,31 @@
-// Skinny-M dequant GEMM for GGUF Q4_0 / Q8_0 weights on gfx950.
+// Skinny-M dequant GEMM for GGUF Q4_0 / Q8_0 weights on gfx950, and the
+// row kernels that build its activation panels.
 //
-//   Y[m][n] = sum_k X[m][k] * W[n][k],  1 <= M <= 16
+//   acc[m][n] += scale * sum_k X[m][k] * W[n][k],  1 <= M <= 16
 //
 // MFMA path: v_mfma_f32_32x32x16_f16 with the activations as the A operand
-// (32 columns: rows m as fp16 hi parts in columns 0..15, lo parts in 16..31)
+// (32 rows: rows m as fp16 hi parts in slots 0..M-1, lo parts in M..2M-1)
 // and 32 weight rows as the B operand.  Weights are exact small integers in
 // fp16 (s-8 for Q4_0, q for Q8_0) unpacked in registers from the tiled
 // nibble/byte plane; one Q4_0/Q8_0 block is exactly K=32 = two MFMAs, after
 // which the 32x32 block product is scaled by the block's fp16 scale d and
 // accumulated in fp32.  x = hi + lo carries 22 significant bits, so the
-// products match fp32 arithmetic to ~1e-7 relative (see DESIGN.md).
+// products match fp32 arithmetic to ~1e-7 relative.
 //
-// Work split: a workgroup is 4 wavefronts = 4 tiles of 32 weight rows, all on
-// the same K range (the activation panel slice for that range is staged in
-// LDS once per workgroup); the K range is split across workgroups and the
-// partial sums are reduced by the last workgroup to arrive (atomic counter),
-// which also applies the epilogue.
+// Work split: a workgroup is 4 wavefronts = 4 tiles of 32 weight rows that
+// share one K slice of PPW block pairs.  Each wavefront keeps RING pairs of
+// weight loads in flight.  The K slices of a tile (split-K) are summed with
+// fp64 atomic adds into an fp64 accumulator: a handful of fp32 partials add
+// exactly in fp64, so the result does not depend on their arrival order and
+// no workgroup waits for another.  Consumers read the accumulator and clear
+// it (vxh_acc_*, the residual/SwiGLU panels, RoPE), so it is all zeros again
+// before the next GEMM that targets it.
+#include <string.h>
+
 #include "vxh_internal.h"
 
 // ---------------------------------------------------------------------------
-// panel prep
+// panels
 // ---------------------------------------------------------------------------
 extern "C" size_t vxh_panel_bytes(int M, int K)
 {
@@ -36,7 +42,7 @@ extern "C" int vxh_panel_alloc(vxh_panel *p, int max_M, int K)
     p->M = 0;
     p->K = K;
     p->avx2 = 0;
-    if (max_M < 1 || max_M > 16 || K % 32)
+    if (max_M < 1 || max_M > 16 || K % 32 || K > VXH_MAX_K)
         return vxh_fail(VXH_ERR_PARAM, "panel_alloc: M %d K %d", max_M, K);
     int rc = vxh_malloc(&p->data, vxh_panel_bytes(max_M, K));
     if (rc) return rc;
@@ -65,124 +71,55 @@ extern "C" int vxh_panel_free(vxh_panel *p)
     return VXH_OK;
 }
 
-// Writes one 16-byte unit pair (hi, lo) of row m for elements
-// 32b + 16h + 8s + 0..7, given their fp32 values v[8].
-__device__ __forceinline__ void vx_panel_store(uint4 *__restrict__ panel, int M, int b, int s, int h,
-                                               int m, const float v[8])
-{
-    vx_half8 hi, lo;
-#pragma unroll
-    for (int kk = 0; kk < 8; kk++) {
-        _Float16 a = (_Float16)v[kk];
-        hi[kk] = a;
-        lo[kk] = (_Float16)(v[kk] - (float)a);
-    }
-    int NS = 2 * M;
-    size_t base = ((size_t)(b * 2 + s) * 2 + h) * NS;
-    panel[base + m] = __builtin_bit_cast(uint4, hi);
-    panel[base + M + m] = __builtin_bit_cast(uint4, lo);
-}
-
-__device__ __forceinline__ float vx_block_max(float v, float *red);
-
-// Power-of-two row scale: s = 2^-e with amax = f * 2^e, f in [0.5, 1), so
-// that every scaled value has magnitude < 1 (fp16 hi/lo keep 22 bits).
-__device__ __forceinline__ float vx_row_scale(float amax, float *rs_out)
-{
-    if (!(amax > 0.0f) || !isfinite(amax)) { *rs_out = 1.0f; return 1.0f; }
-    int e;
-    frexpf(amax, &e);
-    *rs_out = ldexpf(1.0f, e);
-    return ldexpf(1.0f, -e);
-}
-
-// One workgroup per row.  AVX2-lane weights: elements with t % 8 >= 4 count
-// twice (kk >= 4 within a unit); the per-(block,row) correction is the sum of
-// x at offsets 8..11, 16..19, 24..27, 32..35 (offsets >= K read the tail).
-__global__ void vx_prep_panel_kernel(const float *__restrict__ x, int ldx, int M, int K, int avx2,
-                                     const float *__restrict__ tail, int ld_tail,
-                                     uint4 *__restrict__ panel, float *__restrict__ corr,
-                                     float *__restrict__ rscale)
-{
-    __shared__ float red[16];
-    const int m = blockIdx.x;
-    const int nb = K / 32, nbp = (nb + 1) / 2 * 2;
-    const float *xr = x + (size_t)m * ldx;
-    float amax = 0.0f;
-    for (int i = threadIdx.x; i < K; i += blockDim.x) amax = fmaxf(amax, fabsf(xr[i]));
-    amax = vx_block_max(amax, red);
-    float rs;
-    const float sc = vx_row_scale(avx2 ? 2.0f * amax : amax, &rs);
-    if (threadIdx.x == 0) rscale[m] = rs;
-    for (int u = threadIdx.x; u < nbp * 4; u += blockDim.x) {
-        const int b = u / 4, h = (u / 2) % 2, s = u % 2;
-        const int t0 = 32 * b + 16 * h + 8 * s;
-        float v[8];
-#pragma unroll
-        for (int kk = 0; kk < 8; kk++) {
-            float xv = b < nb ? xr[t0 + kk] * sc : 0.0f;   // the padding block of an odd count is zero
-            v[kk] = (avx2 && kk >= 4) ? 2.0f * xv : xv;
-        }
-        vx_panel_store(panel, M, b, s, h, m, v);
-    }
-    if (avx2) {
-        for (int b = threadIdx.x; b < nbp; b += blockDim.x) {
-            float c = 0.0f;
-            if (b < nb)
-                for (int g = 1; g <= 4; g++)
-                    for (int q = 0; q < 4; q++) {
-                        int t = 32 * b + 8 * g + q;
-                        float xv = t < K ? xr[t] : (tail ? tail[(size_t)m * ld_tail + (t - K)] : 0.0f);
-                        c += xv;
-                    }
-            corr[(size_t)b * M + m] = c * sc;
-        }
-    }
-}
-
-extern "C" int vxh_prep_panel(vxh_panel *p, const float *x, int ldx, int M, int K, int avx2,
-                              const float *tail, int ld_tail, vxh_stream s)
-{
-    if (M < 1 || M > 16 || K != p->K || K % 32)
-        return vxh_fail(VXH_ERR_PARAM, "prep_panel: M %d K %d (panel K %d)", M, K, p->K);
-    p->M = M;
-    p->avx2 = avx2;
-    vx_prep_panel_kernel<<<M, 256, 0, vxh_hs(s)>>>(x, ldx, M, K, avx2, tail, ld_tail,
-                                                  (uint4 *)p->data, p->corr, p->rscale);
-    VXH_LAUNCHED();
-    return VXH_OK;
-}
-
 // ---------------------------------------------------------------------------
-// fused RMSNorm + panel (one workgroup per row)
+// row kernels: one 1024-thread workgroup per row; every thread first loads
+// the groups of 8 elements it owns (so a row costs one memory round trip),
+// then the row reductions run in registers and LDS.
 // ---------------------------------------------------------------------------
+#define VX_ROW_THREADS 1024
+
+enum { VX_ROW_PLAIN = 0, VX_ROW_NORM = 1, VX_ROW_RESID_NORM = 2, VX_ROW_SWIGLU = 3 };
+
+struct vx_row_args {
+    float *x;            // PLAIN/NORM: input rows; RESID_NORM: residual rows (updated in place)
+    int ldx;
+    double *acc;         // RESID_NORM: pending GEMM sum added to x; SWIGLU: gate/up accumulator
+    int ld_acc;
+    int K;               // row length (F for SWIGLU)
+    const float *w;      // norm weight (NULL = ones)
+    int avx2;
+    const float *tail;   // AVX2 tail rows [M][ld_tail] (NULL = zeros)
+    int ld_tail;
+    int tail_self;       // AVX2 tail = this row's own values 0..3 before normalisation
+    float thr;           // SWIGLU gate threshold
+    int M;
+    uint4 *panel;
+    float *corr;
+    float *rscale;
+    float *out;          // optional fp32 copy of the panel's values (normalised x / h)
+    int ld_out;
+};
+
 __device__ __forceinline__ float vx_block_sum(float v, float *red)
 {
-    // wave reduction then across the (up to 16) waves of the block
     for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     if (lane == 0) red[w] = v;
     __syncthreads();
-    int nw = (blockDim.x + 63) >> 6;
+    const int nw = (blockDim.x + 63) >> 6;
     float t = 0.0f;
-    if (threadIdx.x < 64) {
-        t = threadIdx.x < nw ? red[threadIdx.x] : 0.0f;
-        for (int off = 32; off > 0; off >>= 1) t += __shfl_xor(t, off, 64);
-        if (threadIdx.x == 0) red[0] = t;
-    }
+    for (int i = 0; i < nw; i++) t += red[i];
     __syncthreads();
-    float r = red[0];
-    __syncthreads();
-    return r;
+    return t;
 }
 
 __device__ __forceinline__ float vx_block_max(float v, float *red)
 {
     for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     if (lane == 0) red[w] = v;
     __syncthreads();
-    int nw = (blockDim.x + 63) >> 6;
+    const int nw = (blockDim.x + 63) >> 6;
     float r = red[0];
     for (int i = 1; i < nw; i++) r = fmaxf(r, red[i]);
     __syncthreads();
@@ -197,76 +134,285 @@ __device__ __forceinline__ float vx_rms_inv(float ss, int K)
     return rms < 1e-10f ? 0.0f : 1.0f / rms;
 }
 
-__global__ void vx_rmsnorm_panel_kernel(const float *__restrict__ x, int ldx, int M, int K,
-                                        const float *__restrict__ w, int avx2,
-                                        const float *__restrict__ tail, int ld_tail,
-                                        uint4 *__restrict__ panel, float *__restrict__ corr,
-                                        float *__restrict__ rscale, float *__restrict__ xn_out,
-                                        int ld_xn)
+// Power-of-two row scale: s = 2^-e with amax = f * 2^e, f in [0.5, 1), so
+// that every scaled value has magnitude < 1 (fp16 hi/lo keep 22 bits).
+__device__ __forceinline__ float vx_row_scale(float amax, float *rs_out)
 {
-    __shared__ float red[16];
-    int m = blockIdx.x;
-    const float *xr = x + (size_t)m * ldx;
-    float ss = 0.0f;
-    for (int i = threadIdx.x; i < K; i += blockDim.x) ss += xr[i] * xr[i];
-    ss = vx_block_sum(ss, red);
-    float inv = vx_rms_inv(ss, K);
+    if (!(amax > 0.0f) || !isfinite(amax)) { *rs_out = 1.0f; return 1.0f; }
+    int e;
+    frexpf(amax, &e);
+    *rs_out = ldexpf(1.0f, e);
+    return ldexpf(1.0f, -e);
+}
+
+__device__ __forceinline__ float vx_silu(float g) { return g / (1.0f + expf(-g)); }
+
+// Panel unit of group g (elements 8g..8g+7): block b = g/4, lane half h =
+// (g/2)%2, MFMA half s = g%2; hi at slot m, lo at slot M+m.
+__device__ __forceinline__ void vx_panel_store(uint4 *__restrict__ panel, int M, int g, int m,
+                                               const float v[8])
+{
+    vx_half8 hi, lo;
+#pragma unroll
+    for (int kk = 0; kk < 8; kk++) {
+        _Float16 a = (_Float16)v[kk];
+        hi[kk] = a;
+        lo[kk] = (_Float16)(v[kk] - (float)a);
+    }
+    const int b = g >> 2, h = (g >> 1) & 1, s = g & 1;
+    const size_t base = ((size_t)(b * 2 + s) * 2 + h) * (2 * M);
+    panel[base + m] = __builtin_bit_cast(uint4, hi);
+    panel[base + M + m] = __builtin_bit_cast(uint4, lo);
+}
+
+// G = groups of 8 elements per thread (K <= 8192 * G <= VXH_MAX_K).
+template <int MODE, int G>
+__global__ __launch_bounds__(VX_ROW_THREADS) void vx_row_panel_kernel(vx_row_args a)
+{
+    __shared__ float red[VX_ROW_THREADS / 64];
+    __shared__ float s4[VXH_MAX_K / 8 + 8];
+    __shared__ float s_tail;
+    const int m = blockIdx.x;
+    const int K = a.K, nb = K / 32, nbp = (nb + 1) / 2 * 2;
+    const int ng = nb * 4, ngp = nbp * 4;
+    float v[G][8];
+
+    // ---- load (and, for the accumulator modes, consume) ----
+#pragma unroll
+    for (int j = 0; j < G; j++) {
+        const int g = threadIdx.x + j * VX_ROW_THREADS;
+#pragma unroll
+        for (int kk = 0; kk < 8; kk++) v[j][kk] = 0.0f;
+        if (g >= ng) continue;
+        const int e0 = 8 * g;
+        if (MODE == VX_ROW_SWIGLU) {
+            // h index i -> tile i/16: gate at physical row 32(i/16) + i%16, up 16 rows later
+            double *ar = a.acc + (size_t)m * a.ld_acc;
+            const int pg = 32 * (e0 / 16) + e0 % 16;
+            double2 gv[4], uv[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                gv[q] = *(const double2 *)(ar + pg + 2 * q);
+                uv[q] = *(const double2 *)(ar + pg + 16 + 2 * q);
+            }
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                *(double2 *)(ar + pg + 2 * q) = make_double2(0.0, 0.0);
+                *(double2 *)(ar + pg + 16 + 2 * q) = make_double2(0.0, 0.0);
+            }
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                float g0 = vx_silu((float)gv[q].x), g1 = vx_silu((float)gv[q].y);
+                v[j][2 * q] = fabsf(g0) < a.thr ? 0.0f : g0 * (float)uv[q].x;
+                v[j][2 * q + 1] = fabsf(g1) < a.thr ? 0.0f : g1 * (float)uv[q].y;
+            }
+        } else {
+            float *xr = a.x + (size_t)m * a.ldx + e0;
+            float4 x0 = *(const float4 *)xr, x1 = *(const float4 *)(xr + 4);
+            float t[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            if (MODE == VX_ROW_RESID_NORM) {
+                double *ar = a.acc + (size_t)m * a.ld_acc + e0;
+                double2 p[4];
+#pragma unroll
+                for (int q = 0; q < 4; q++) p[q] = *(const double2 *)(ar + 2 * q);
+#pragma unroll
+                for (int q = 0; q < 4; q++) *(double2 *)(ar + 2 * q) = make_double2(0.0, 0.0);
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    t[2 * q] = t[2 * q] + (float)p[q].x;
+                    t[2 * q + 1] = t[2 * q + 1] + (float)p[q].y;
+                }
+                *(float4 *)xr = make_float4(t[0], t[1], t[2], t[3]);
+                *(float4 *)(xr + 4) = make_float4(t[4], t[5], t[6], t[7]);
+            }
+#pragma unroll
+            for (int kk = 0; kk < 8; kk++) v[j][kk] = t[kk];
+        }
+    }
+    if (a.avx2 && a.tail_self && threadIdx.x == 0)
+        s_tail = v[0][0] + v[0][1] + v[0][2] + v[0][3];
+
+    // ---- RMSNorm ----
+    if (MODE == VX_ROW_NORM || MODE == VX_ROW_RESID_NORM) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < G; j++)
+#pragma unroll
+            for (int kk = 0; kk < 8; kk++) ss += v[j][kk] * v[j][kk];
+        ss = vx_block_sum(ss, red);
+        const float inv = vx_rms_inv(ss, K);
+#pragma unroll
+        for (int j = 0; j < G; j++) {
+            const int g = threadIdx.x + j * VX_ROW_THREADS;
+            if (g >= ng) continue;
+            float wv[8];
+            if (a.w) {
+                float4 w0 = *(const float4 *)(a.w + 8 * g), w1 = *(const float4 *)(a.w + 8 * g + 4);
+                wv[0] = w0.x; wv[1] = w0.y; wv[2] = w0.z; wv[3] = w0.w;
+                wv[4] = w1.x; wv[5] = w1.y; wv[6] = w1.z; wv[7] = w1.w;
+            } else {
+#pragma unroll
+                for (int kk = 0; kk < 8; kk++) wv[kk] = 1.0f;
+            }
+#pragma unroll
+            for (int kk = 0; kk < 8; kk++) v[j][kk] = wv[kk] * (v[j][kk] * inv);
+        }
+    }
+    if (a.out) {
+#pragma unroll
+        for (int j = 0; j < G; j++) {
+            const int g = threadIdx.x + j * VX_ROW_THREADS;
+            if (g >= ng) continue;
+            float *o = a.out + (size_t)m * a.ld_out + 8 * g;
+            *(float4 *)o = make_float4(v[j][0], v[j][1], v[j][2], v[j][3]);
+            *(float4 *)(o + 4) = make_float4(v[j][4], v[j][5], v[j][6], v[j][7]);
+        }
+    }
+
+    // ---- row scale and panel ----
     float amax = 0.0f;
-    for (int i = threadIdx.x; i < K; i += blockDim.x) amax = fmaxf(amax, fabsf((w ? w[i] : 1.0f) * (xr[i] * inv)));
+#pragma unroll
+    for (int j = 0; j < G; j++)
+#pragma unroll
+        for (int kk = 0; kk < 8; kk++) amax = fmaxf(amax, fabsf(v[j][kk]));
     amax = vx_block_max(amax, red);
     float rs;
-    const float sc = vx_row_scale(avx2 ? 2.0f * amax : amax, &rs);
-    if (threadIdx.x == 0) rscale[m] = rs;
-    int nb = K / 32, nbp = (nb + 1) / 2 * 2;
-    // units (b, h, s): 8 elements each; the padding block of an odd count is zero
-    for (int u = threadIdx.x; u < nbp * 4; u += blockDim.x) {
-        int b = u / 4, h = (u / 2) % 2, s = u % 2;
-        int t0 = 32 * b + 16 * h + 8 * s;
-        float v[8];
+    const float sc = vx_row_scale(a.avx2 ? 2.0f * amax : amax, &rs);
+    if (threadIdx.x == 0) a.rscale[m] = rs;
+#pragma unroll
+    for (int j = 0; j < G; j++) {
+        const int g = threadIdx.x + j * VX_ROW_THREADS;
+        if (g >= ngp) continue;   // groups of the padding block are zeros
+        float u[8];
 #pragma unroll
         for (int kk = 0; kk < 8; kk++) {
-            float xv = 0.0f;
-            if (b < nb) {
-                float wv = w ? w[t0 + kk] : 1.0f;
-                xv = wv * (xr[t0 + kk] * inv);
-                if (xn_out) xn_out[(size_t)m * ld_xn + t0 + kk] = xv;
-                xv *= sc;
-            }
-            v[kk] = (avx2 && kk >= 4) ? 2.0f * xv : xv;
+            const float xv = v[j][kk] * sc;
+            u[kk] = (a.avx2 && kk >= 4) ? 2.0f * xv : xv;
         }
-        vx_panel_store(panel, M, b, s, h, m, v);
+        vx_panel_store(a.panel, a.M, g, m, u);
+        if (a.avx2) s4[g] = (v[j][0] + v[j][1] + v[j][2] + v[j][3]) * sc;
     }
-    if (avx2) {
-        // corrections need normalised values of the next block and, for the
-        // last block, the caller's tail values (src/model.c:425-435)
+    if (a.avx2) {
+        // AVX2-lane correction of block b: x at offsets 8..11, 16..19, 24..27
+        // and 32..35 (the next block's first four, or the caller's tail).
+        __syncthreads();
         for (int b = threadIdx.x; b < nbp; b += blockDim.x) {
             float c = 0.0f;
-            if (b < nb)
-            for (int g = 1; g <= 4; g++)
-                for (int q = 0; q < 4; q++) {
-                    int t = 32 * b + 8 * g + q;
-                    float xv = t < K ? (w ? w[t] : 1.0f) * (xr[t] * inv)
-                                     : (tail ? tail[(size_t)m * ld_tail + (t - K)] : 0.0f);
-                    c += xv;
+            if (b < nb) {
+                c = s4[4 * b + 1] + s4[4 * b + 2] + s4[4 * b + 3];
+                if (b + 1 < nb) {
+                    c += s4[4 * b + 4];
+                } else if (a.tail_self) {
+                    c += s_tail * sc;
+                } else if (a.tail) {
+                    const float *t = a.tail + (size_t)m * a.ld_tail;
+                    c += (t[0] + t[1] + t[2] + t[3]) * sc;
                 }
-            corr[(size_t)b * M + m] = c * sc;
+            }
+            a.corr[(size_t)b * a.M + m] = c;
         }
     }
+}
+
+template <int MODE>
+static int vx_launch_row(const vx_row_args &a, vxh_stream s)
+{
+    const int ng = a.K / 8;
+    if (ng <= VX_ROW_THREADS)
+        vx_row_panel_kernel<MODE, 1><<<a.M, VX_ROW_THREADS, 0, vxh_hs(s)>>>(a);
+    else if (ng <= 2 * VX_ROW_THREADS)
+        vx_row_panel_kernel<MODE, 2><<<a.M, VX_ROW_THREADS, 0, vxh_hs(s)>>>(a);
+    else if (ng <= 3 * VX_ROW_THREADS)
+        vx_row_panel_kernel<MODE, 3><<<a.M, VX_ROW_THREADS, 0, vxh_hs(s)>>>(a);
+    else
+        return vxh_fail(VXH_ERR_PARAM, "row length %d above %d", a.K, VXH_MAX_K);
+    VXH_LAUNCHED();
+    return VXH_OK;
+}
+
+static int vx_row_check(const vxh_panel *p, int M, int K, const char *what)
+{
+    if (M < 1 || M > 16 || K != p->K || K % 32 || K > VXH_MAX_K)
+        return vxh_fail(VXH_ERR_PARAM, "%s: M %d K %d (panel K %d)", what, M, K, p->K);
+    return VXH_OK;
+}
+
+static vx_row_args vx_row_base(vxh_panel *p, int M, int K, int avx2)
+{
+    vx_row_args a;
+    memset(&a, 0, sizeof(a));
+    a.K = K;
+    a.M = M;
+    a.avx2 = avx2;
+    a.panel = (uint4 *)p->data;
+    a.corr = p->corr;
+    a.rscale = p->rscale;
+    p->M = M;
+    p->avx2 = avx2;
+    return a;
+}
+
+extern "C" int vxh_prep_panel(vxh_panel *p, const float *x, int ldx, int M, int K, int avx2,
+                              const float *tail, int ld_tail, vxh_stream s)
+{
+    int rc = vx_row_check(p, M, K, "prep_panel");
+    if (rc) return rc;
+    vx_row_args a = vx_row_base(p, M, K, avx2);
+    a.x = (float *)x;
+    a.ldx = ldx;
+    a.tail = tail;
+    a.ld_tail = ld_tail;
+    return vx_launch_row<VX_ROW_PLAIN>(a, s);
 }
 
 extern "C" int vxh_rmsnorm_panel(const float *x, int ldx, int M, int K, const float *w, int avx2,
                                  const float *tail, int ld_tail, vxh_panel *p, float *xn_out,
                                  int ld_xn, vxh_stream s)
 {
-    if (M < 1 || M > 16 || K != p->K || K % 32)
-        return vxh_fail(VXH_ERR_PARAM, "rmsnorm_panel: M %d K %d (panel K %d)", M, K, p->K);
-    p->M = M;
-    p->avx2 = avx2;
-    vx_rmsnorm_panel_kernel<<<M, 256, 0, vxh_hs(s)>>>(x, ldx, M, K, w, avx2, tail, ld_tail,
-                                                     (uint4 *)p->data, p->corr, p->rscale, xn_out,
-                                                     ld_xn);
-    VXH_LAUNCHED();
-    return VXH_OK;
+    int rc = vx_row_check(p, M, K, "rmsnorm_panel");
+    if (rc) return rc;
+    vx_row_args a = vx_row_base(p, M, K, avx2);
+    a.x = (float *)x;
+    a.ldx = ldx;
+    a.w = w;
+    a.tail = tail;
+    a.ld_tail = ld_tail;
+    a.tail_self = tail == x && ld_tail == ldx;
+    a.out = xn_out;
+    a.ld_out = ld_xn;
+    return vx_launch_row<VX_ROW_NORM>(a, s);
+}
+
+extern "C" int vxh_resid_rmsnorm_panel(float *x, int ldx, double *acc, int ld_acc, int M, int K,
+                                       const float *w, int avx2, int tail_self, vxh_panel *p,
+                                       float *xn_out, int ld_xn, vxh_stream s)
+{
+    int rc = vx_row_check(p, M, K, "resid_rmsnorm_panel");
+    if (rc) return rc;
+    vx_row_args a = vx_row_base(p, M, K, avx2);
+    a.x = x;
+    a.ldx = ldx;
+    a.acc = acc;
+    a.ld_acc = ld_acc;
+    a.w = w;
+    a.tail_self = tail_self;
+    a.out = xn_out;
+    a.ld_out = ld_xn;
+    return vx_launch_row<VX_ROW_RESID_NORM>(a, s);
+}
+
+extern "C" int vxh_swiglu_panel(double *acc, int ld_acc, int M, int F, float thr, int avx2,
+                                vxh_panel *p, float *h_out, int ldh, vxh_stream s)
+{
+    int rc = vx_row_check(p, M, F, "swiglu_panel");
+    if (rc) return rc;
+    vx_row_args a = vx_row_base(p, M, F, avx2);
+    a.acc = acc;
+    a.ld_acc = ld_acc;
+    a.thr = thr;
+    a.out = h_out;
+    a.ld_out = ldh;
+    return vx_launch_row<VX_ROW_SWIGLU>(a, s);
 }
 
 __global__ void vx_rmsnorm_kernel(const float *__restrict__ x, int ldx, int K,
@@ -295,27 +441,22 @@ extern "C" int vxh_rmsnorm(const float *x, int ldx, int M, int K, const float *w
 // ---------------------------------------------------------------------------
 // MFMA GEMM
 // ---------------------------------------------------------------------------
-struct vx_epi {
-    const float *rscale;
-    int kind;
-    float *y;
-    int ldy;
-    const float *r;
-    int ldr;
-    float thr;
-    float scale;
-    int n_out;
+// Q4_0 dword (8 nibbles in the repacked slot order) -> 8 fp16 values s - 8:
+// 1024 + s (low nibble) and 1024 + 16 s (high nibble) by exponent magic,
+// then one packed add / fma per pair.  The masks and the magic word arrive
+// as kernel arguments (SGPRs), so each (q & mask) | magic is one
+// v_and_or_b32 (gfx9 VOP3 encodings cannot carry a literal).
+struct vx_consts {
+    uint32_t lo4, hi4, lo8, magic;
 };
 
-// Q4_0 dword (8 nibbles in the repacked slot order) -> 8 fp16 values s - 8.
-__device__ __forceinline__ vx_half8 vx_unpack_q4(uint32_t q)
+__device__ __forceinline__ vx_half8 vx_unpack_q4(uint32_t q, const vx_consts &k)
 {
-    const uint32_t lo = 0x000F000Fu, hi = 0x00F000F0u, magic = 0x64006400u;
-    uint32_t q8 = q >> 8;
-    vx_half2 a = __builtin_bit_cast(vx_half2, (q & lo) | magic);
-    vx_half2 b = __builtin_bit_cast(vx_half2, (q & hi) | magic);
-    vx_half2 c = __builtin_bit_cast(vx_half2, (q8 & lo) | magic);
-    vx_half2 d = __builtin_bit_cast(vx_half2, (q8 & hi) | magic);
+    const uint32_t q8 = q >> 8;
+    vx_half2 a = __builtin_bit_cast(vx_half2, (q & k.lo4) | k.magic);
+    vx_half2 b = __builtin_bit_cast(vx_half2, (q & k.hi4) | k.magic);
+    vx_half2 c = __builtin_bit_cast(vx_half2, (q8 & k.lo4) | k.magic);
+    vx_half2 d = __builtin_bit_cast(vx_half2, (q8 & k.hi4) | k.magic);
     const vx_half2 off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
     const vx_half2 sc = {(_Float16)0.0625f, (_Float16)0.0625f};
     const vx_half2 off16 = {(_Float16)-72.0f, (_Float16)-72.0f};
@@ -327,15 +468,15 @@ __device__ __forceinline__ vx_half8 vx_unpack_q4(uint32_t q)
     return r;
 }
 
-// Two Q8_0 dwords (4 int8 each, bytes in the repacked order) -> 8 fp16.
-__device__ __forceinline__ vx_half8 vx_unpack_q8(uint32_t qa, uint32_t qb)
+// Two Q8_0 dwords (4 int8 each, bytes in the repacked order) -> 8 fp16:
+// (q ^ 0x80) = q + 128 as an unsigned byte, 1024 + that by exponent magic.
+__device__ __forceinline__ vx_half8 vx_unpack_q8(uint32_t qa, uint32_t qb, const vx_consts &k)
 {
-    const uint32_t m = 0x00FF00FFu, magic = 0x64006400u;
-    uint32_t ua = qa ^ 0x80808080u, ub = qb ^ 0x80808080u;
-    vx_half2 a0 = __builtin_bit_cast(vx_half2, (ua & m) | magic);
-    vx_half2 a1 = __builtin_bit_cast(vx_half2, ((ua >> 8) & m) | magic);
-    vx_half2 b0 = __builtin_bit_cast(vx_half2, (ub & m) | magic);
-    vx_half2 b1 = __builtin_bit_cast(vx_half2, ((ub >> 8) & m) | magic);
+    const uint32_t ua = qa ^ 0x80808080u, ub = qb ^ 0x80808080u;
+    vx_half2 a0 = __builtin_bit_cast(vx_half2, (ua & k.lo8) | k.magic);
+    vx_half2 a1 = __builtin_bit_cast(vx_half2, ((ua >> 8) & k.lo8) | k.magic);
+    vx_half2 b0 = __builtin_bit_cast(vx_half2, (ub & k.lo8) | k.magic);
+    vx_half2 b1 = __builtin_bit_cast(vx_half2, ((ub >> 8) & k.lo8) | k.magic);
     const vx_half2 off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
     a0 = a0 + off;
     a1 = a1 + off;
@@ -353,261 +494,311 @@ struct vx_mcfg {
     static constexpr int R1 = M <= 4 ? M : (M <= 8 ? 4 : (4 + (M - 8 < 4 ? M - 8 : 4)));
 };
 
-__device__ __forceinline__ float vx_silu(float g) { return g / (1.0f + expf(-g)); }
+// Block pairs per K slice: 16 keeps ~1-3k wavefronts on the big verify
+// shapes; small M and the largest M (LDS) use 8.
+template <int QT, int M>
+struct vx_ppw {
+    static constexpr int value = QT == 8 ? 8 : ((M <= 4 || M > 12) ? 8 : 16);
+};
 
-__device__ __forceinline__ void vx_store_epi(const vx_epi &ep, int m, int n, float v)
-{
-    if (n >= ep.n_out) return;
-    float y = v * ep.rscale[m] * ep.scale;
-    if (ep.kind == VXH_EPI_RESID) y = ep.r[(size_t)m * ep.ldr + n] + y;
-    else if (ep.kind == VXH_EPI_GATE) y = fabsf(ep.r[(size_t)m * ep.ldr + n]) < ep.thr ? 0.0f : y;
-    ep.y[(size_t)m * ep.ldy + n] = y;
-}
+struct vx_gemm_args {
+    const uint4 *wq;
+    const uint32_t *wd;
+    const uint4 *panel;
+    const float *corr;
+    const float *rscale;
+    int n_tiles, n_pairs, n_splits;
+    double *acc;
+    int ld_acc;
+    int n_out;
+    float scale;
+    const float *gate;
+    int ld_gate;
+    float thr;
+    vx_consts k;
+};
 
-// QT: 2 = Q4_0, 8 = Q8_0.  PF: weight loads kept in flight per wave.
-template <int QT, int M, bool AVX2, int PF>
-__global__ __launch_bounds__(256) void vx_gemm_mfma_kernel(
-    const uint4 *__restrict__ wq, const uint32_t *__restrict__ wd, const uint4 *__restrict__ panel,
-    const float *__restrict__ corr, int n_tiles, int n_pairs, int pps, int n_splits,
-    float *__restrict__ part, unsigned *__restrict__ counters, vx_epi ep)
+#define VX_RING 4
+
+// QT: 2 = Q4_0, 8 = Q8_0.
+template <int QT, int M, bool AVX2>
+__global__ __launch_bounds__(256) void vx_gemm_kernel(vx_gemm_args a)
 {
+    constexpr int PPW = vx_ppw<QT, M>::value;
     constexpr int NS = vx_mcfg<M>::NS;
     constexpr int R1 = vx_mcfg<M>::R1;
     constexpr int WPP = QT == 2 ? 1 : 2;   // 16-byte weight loads per lane per block pair
-    extern __shared__ uint4 lds[];
-    __shared__ int s_last;
+    constexpr int UNITS = PPW * 8 * NS;    // panel units of a full slice
+    constexpr int UPT = (UNITS + 255) / 256;
+    __shared__ uint4 lds[UPT * 256];
+    __shared__ float lcorr[AVX2 ? PPW * 2 * M : 1];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int grp = blockIdx.x / n_splits, split = blockIdx.x % n_splits;
+    const int grp = blockIdx.x / a.n_splits, split = blockIdx.x % a.n_splits;
     const int T = grp * 4 + wave;
-    const bool tile_ok = T < n_tiles;
-    const int p0 = split * pps;
-    const int p1 = min(p0 + pps, n_pairs);
-    const int np = p1 - p0;
+    const bool tile_ok = T < a.n_tiles;
+    const int Tc = tile_ok ? T : 0;
+    const int p0 = split * PPW;
+    const int np = min(PPW, a.n_pairs - p0);
+    const int units = np * 8 * NS;
     const int c = lane & 31, h = lane >> 5;
 
-    // ---- weight stream prefetch (issued before the LDS staging) ----
-    const uint4 *wp = wq + ((size_t)(tile_ok ? T : 0) * n_pairs * WPP + (size_t)p0 * WPP) * 64 + lane;
-    const uint32_t *sp = wd + ((size_t)(tile_ok ? T : 0) * n_pairs + p0) * 32 + c;
-    uint4 wbuf[PF][WPP];
-    uint32_t sbuf[PF];
+    // 1. the panel slice (issued first so its wait does not cover the weights)
+    const uint4 *psrc = a.panel + (size_t)p0 * 8 * NS;
+    uint4 pv[UPT];
 #pragma unroll
-    for (int i = 0; i < PF; i++) {
-        if (tile_ok && i < np) {
-#pragma unroll
-            for (int q = 0; q < WPP; q++) wbuf[i][q] = wp[((size_t)i * WPP + q) * 64];
-            sbuf[i] = sp[(size_t)i * 32];
-        }
-    }
-
-    // ---- stage the panel slice (and corrections) for blocks [2p0, 2p1) ----
-    const int units = np * 2 * 4 * NS;
-    const uint4 *psrc = panel + (size_t)p0 * 2 * 4 * NS;
-    for (int i = threadIdx.x; i < units; i += 256) lds[i] = psrc[i];
-    float *lcorr = (float *)(lds + units);
+    for (int j = 0; j < UPT; j++) pv[j] = psrc[min(j * 256 + (int)threadIdx.x, units - 1)];
+    // AVX2 corrections of the slice: at most PPW*2*M <= 512 floats, two per thread
+    float cv0 = 0.0f, cv1 = 0.0f;
     if (AVX2) {
-        const float *csrc = corr + (size_t)p0 * 2 * M;
-        for (int i = threadIdx.x; i < np * 2 * M; i += 256) lcorr[i] = csrc[i];
+        const int cnt = np * 2 * M;
+        const float *cs = a.corr + (size_t)p0 * 2 * M;
+        cv0 = cs[min((int)threadIdx.x, cnt - 1)];
+        cv1 = cs[min((int)threadIdx.x + 256, cnt - 1)];
+    }
+    // 2. the first RING pairs of this wavefront's weights and scales
+    const uint4 *wp = a.wq + ((size_t)Tc * a.n_pairs + p0) * WPP * 64 + lane;
+    const uint32_t *sp = a.wd + ((size_t)Tc * a.n_pairs + p0) * 32 + c;
+    uint4 w[VX_RING][WPP];
+    uint32_t sc[VX_RING];
+#pragma unroll
+    for (int i = 0; i < VX_RING; i++) {
+        const int pi = min(i, np - 1);
+#pragma unroll
+        for (int q = 0; q < WPP; q++) w[i][q] = wp[((size_t)pi * WPP + q) * 64];
+        sc[i] = sp[(size_t)pi * 32];
+    }
+#pragma unroll
+    for (int j = 0; j < UPT; j++) lds[j * 256 + threadIdx.x] = pv[j];
+    if (AVX2) {
+        if ((int)threadIdx.x < PPW * 2 * M) lcorr[threadIdx.x] = cv0;
+        if ((int)threadIdx.x + 256 < PPW * 2 * M) lcorr[threadIdx.x + 256] = cv1;
     }
     __syncthreads();
 
-    const bool a_ok = c < 16 ? (c < M) : (c - 16 < M);
-    const int slot = c < 16 ? c : M + (c - 16);
+    // idle A lanes read a valid slot; their output rows are never used
+    const int slot = c < 16 ? min(c, M - 1) : M + min(c - 16, M - 1);
     float acc[16];
 #pragma unroll
     for (int r = 0; r < 16; r++) acc[r] = 0.0f;
     const vx_f32x16 zero16 = {};
-    const vx_half8 zero8 = {};
-
-    if (tile_ok) {
-        for (int pb = 0; pb < np; pb += PF) {
 #pragma unroll
-            for (int i = 0; i < PF; i++) {
-                const int pl = pb + i;
-                if (pl < np) {
-                    uint4 w[WPP];
+    for (int i = 0; i < PPW; i++) {
+        uint4 wv[WPP];
 #pragma unroll
-                    for (int q = 0; q < WPP; q++) w[q] = wbuf[i][q];
-                    const uint32_t sc = sbuf[i];
-                    if (pl + PF < np) {
+        for (int q = 0; q < WPP; q++) wv[q] = w[i % VX_RING][q];
+        const uint32_t sv = sc[i % VX_RING];
+        if (i + VX_RING < PPW) {
+            const int pi = min(i + VX_RING, np - 1);
 #pragma unroll
-                        for (int q = 0; q < WPP; q++) wbuf[i][q] = wp[((size_t)(pl + PF) * WPP + q) * 64];
-                        sbuf[i] = sp[(size_t)(pl + PF) * 32];
+            for (int q = 0; q < WPP; q++) w[i % VX_RING][q] = wp[((size_t)pi * WPP + q) * 64];
+            sc[i % VX_RING] = sp[(size_t)pi * 32];
+        }
+        if (i < np) {
+#pragma unroll
+            for (int blk = 0; blk < 2; blk++) {
+                const int bl = 2 * i + blk;
+                vx_half8 b0, b1;
+                if (QT == 2) {
+                    b0 = vx_unpack_q4(blk ? wv[0].z : wv[0].x, a.k);
+                    b1 = vx_unpack_q4(blk ? wv[0].w : wv[0].y, a.k);
+                } else {
+                    b0 = vx_unpack_q8(wv[blk].x, wv[blk].y, a.k);
+                    b1 = vx_unpack_q8(wv[blk].z, wv[blk].w, a.k);
+                }
+                const vx_half8 a0 = __builtin_bit_cast(vx_half8, lds[((bl * 2 + 0) * 2 + h) * NS + slot]);
+                const vx_half8 a1 = __builtin_bit_cast(vx_half8, lds[((bl * 2 + 1) * 2 + h) * NS + slot]);
+                vx_f32x16 D = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b0, zero16, 0, 0, 0);
+                D = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b1, D, 0, 0, 0);
+                const float d = vx_half_bits_to_float((sv >> (16 * blk)) & 0xFFFFu);
+#pragma unroll
+                for (int r = 0; r < R1; r++) {
+                    float dh = D[r];
+                    if (AVX2) {
+                        const int m = 8 * (r / 4) + 4 * h + (r % 4);
+                        dh = fmaf(-8.0f, m < M ? lcorr[bl * M + m] : 0.0f, dh);
                     }
-#pragma unroll
-                    for (int blk = 0; blk < 2; blk++) {
-                        const int bl = 2 * pl + blk;
-                        vx_half8 b0, b1;
-                        if (QT == 2) {
-                            b0 = vx_unpack_q4(blk ? w[0].z : w[0].x);
-                            b1 = vx_unpack_q4(blk ? w[0].w : w[0].y);
-                        } else {
-                            b0 = vx_unpack_q8(w[blk].x, w[blk].y);
-                            b1 = vx_unpack_q8(w[blk].z, w[blk].w);
-                        }
-                        vx_half8 a0 = zero8, a1 = zero8;
-                        if (a_ok) {
-                            a0 = __builtin_bit_cast(vx_half8, lds[((bl * 2 + 0) * 2 + h) * NS + slot]);
-                            a1 = __builtin_bit_cast(vx_half8, lds[((bl * 2 + 1) * 2 + h) * NS + slot]);
-                        }
-                        vx_f32x16 D = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b0, zero16, 0, 0, 0);
-                        D = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b1, D, 0, 0, 0);
-                        const float d = vx_half_bits_to_float((sc >> (16 * blk)) & 0xFFFFu);
-#pragma unroll
-                        for (int r = 0; r < R1; r++) {
-                            float dh = D[r];
-                            if (AVX2) {
-                                const int m = 8 * (r / 4) + 4 * h + (r % 4);
-                                dh = fmaf(-8.0f, m < M ? lcorr[bl * M + m] : 0.0f, dh);
-                            }
-                            acc[r] = fmaf(d, dh, acc[r]);
-                            acc[r + 8] = fmaf(d, D[r + 8], acc[r + 8]);
-                        }
-                    }
+                    acc[r] = fmaf(d, dh, acc[r]);
+                    acc[r + 8] = fmaf(d, D[r + 8], acc[r + 8]);
                 }
             }
         }
     }
 
-    // ---- partial sums: hi + lo per (m, n) ----
-    const int n_phys = n_tiles * 32;
-    if (tile_ok) {
+    // 3. this slice's contribution, added in fp64
+    const int n = T * 32 + c;
+    if (!tile_ok || n >= a.n_out) return;
 #pragma unroll
-        for (int r = 0; r < R1; r++) {
-            const int m = 8 * (r / 4) + 4 * h + (r % 4);
-            if (m < M) part[((size_t)split * M + m) * n_phys + T * 32 + c] = acc[r] + acc[r + 8];
-        }
+    for (int r = 0; r < R1; r++) {
+        const int m = 8 * (r / 4) + 4 * h + (r % 4);
+        if (m >= M) continue;
+        if (a.gate && fabsf(a.gate[(size_t)m * a.ld_gate + n]) < a.thr) continue;
+        const float v = (acc[r] + acc[r + 8]) * a.rscale[m] * a.scale;
+        __hip_atomic_fetch_add(&a.acc[(size_t)m * a.ld_acc + n], (double)v, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
     }
-
-    // ---- last workgroup of this tile group reduces and applies the epilogue ----
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        unsigned prev = __hip_atomic_fetch_add(&counters[grp], 1u, __ATOMIC_ACQ_REL,
-                                               __HIP_MEMORY_SCOPE_AGENT);
-        s_last = prev == (unsigned)(n_splits - 1);
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    const int n0 = grp * 128;
-    if (ep.kind == VXH_EPI_SWIGLU) {
-        // tile t holds gate rows 16t..16t+15 (j < 16) and up rows (j >= 16)
-        for (int i = threadIdx.x; i < M * 64; i += 256) {
-            const int m = i / 64, jj = i % 64, tl = jj / 16, j = jj % 16;
-            const int tg = grp * 4 + tl;
-            if (tg >= n_tiles) continue;
-            float g = 0.0f, u = 0.0f;
-            for (int sp2 = 0; sp2 < n_splits; sp2++) {
-                const float *pr = part + ((size_t)sp2 * M + m) * n_phys + tg * 32;
-                g += pr[j];
-                u += pr[16 + j];
-            }
-            g *= ep.rscale[m] * ep.scale;
-            u *= ep.rscale[m] * ep.scale;
-            const int n = tg * 16 + j;
-            if (n < ep.n_out) {
-                const float sg = vx_silu(g);
-                ep.y[(size_t)m * ep.ldy + n] = fabsf(sg) < ep.thr ? 0.0f : sg * u;
-            }
-        }
-    } else {
-        for (int i = threadIdx.x; i < M * 128; i += 256) {
-            const int m = i / 128, n = n0 + i % 128;
-            if (n >= n_phys) continue;
-            float v = 0.0f;
-            for (int sp2 = 0; sp2 < n_splits; sp2++) v += part[((size_t)sp2 * M + m) * n_phys + n];
-            vx_store_epi(ep, m, n, v);
-        }
-    }
-    if (threadIdx.x == 0) counters[grp] = 0u;
 }
-
-// Splits the K range so that the launch has enough workgroups to cover the
-// 256 CUs while the LDS slice stays <= 40 KiB.
-static void vx_gemm_plan(int n_tiles, int n_pairs, int M, int *pps, int *n_splits)
-{
-    int groups = (n_tiles + 3) / 4;
-    int per_pair_lds = 128 * 2 * M + 8 * M;          // panel units + corrections
-    int max_pps = 40960 / per_pair_lds;
-    if (max_pps < 1) max_pps = 1;
-    int want_splits = (1024 + groups - 1) / groups;
-    int p = (n_pairs + want_splits - 1) / want_splits;
-    if (p < 4) p = 4;
-    if (p > max_pps) p = max_pps;
-    if (p > n_pairs) p = n_pairs;
-    *pps = p;
-    *n_splits = (n_pairs + p - 1) / p;
-}
-
-extern "C" size_t vxh_gemm_workspace_floats(int n_rows, int n_cols, int M)
-{
-    int n_tiles = (n_rows + 31) / 32, n_pairs = (n_cols / 32 + 1) / 2, pps, ns;
-    vx_gemm_plan(n_tiles, n_pairs, M, &pps, &ns);
-    return (size_t)ns * M * n_tiles * 32;
-}
-
-extern "C" int vxh_gemm_workspace_counters(int n_rows) { return ((n_rows + 31) / 32 + 3) / 4; }
 
 template <int QT, int M, bool AVX2>
-static int vx_launch_mfma(const vxh_qmat *W, const vxh_panel *X, const vx_epi &ep,
-                          vxh_workspace *ws, hipStream_t st)
+static int vx_launch_gemm(const vxh_qmat *W, vx_gemm_args &a, hipStream_t st)
 {
-    int n_tiles = W->n_rows / 32;
-    int pps, n_splits;
-    vx_gemm_plan(n_tiles, W->n_pairs, M, &pps, &n_splits);
-    int groups = (n_tiles + 3) / 4;
-    size_t need = (size_t)n_splits * M * W->n_rows;
-    if (need > ws->part_floats || groups > ws->n_counters)
-        return vxh_fail(VXH_ERR_PARAM, "gemm workspace too small: need %zu floats / %d counters",
-                        need, groups);
-    size_t lds = (size_t)pps * 2 * 4 * 2 * M * 16 + (AVX2 ? (size_t)pps * 2 * M * 4 : 0);
-    vx_gemm_mfma_kernel<QT, M, AVX2, 4><<<groups * n_splits, 256, lds, st>>>(
-        (const uint4 *)W->qs, (const uint32_t *)W->d, (const uint4 *)X->data, X->corr, n_tiles,
-        W->n_pairs, pps, n_splits, ws->part, ws->counters, ep);
+    constexpr int PPW = vx_ppw<QT, M>::value;
+    a.n_tiles = W->n_rows / 32;
+    a.n_pairs = W->n_pairs;
+    a.n_splits = (W->n_pairs + PPW - 1) / PPW;
+    const int groups = (a.n_tiles + 3) / 4;
+    vx_gemm_kernel<QT, M, AVX2><<<groups * a.n_splits, 256, 0, st>>>(a);
     VXH_LAUNCHED();
     return VXH_OK;
 }
 
 template <int M>
-static int vx_dispatch_m(const vxh_qmat *W, const vxh_panel *X, const vx_epi &ep,
-                         vxh_workspace *ws, hipStream_t st)
+static int vx_dispatch_m(const vxh_qmat *W, int avx2, vx_gemm_args &a, hipStream_t st)
 {
     if (W->type == 2) {
-        if (X->avx2) return vx_launch_mfma<2, M, true>(W, X, ep, ws, st);
-        return vx_launch_mfma<2, M, false>(W, X, ep, ws, st);
+        if (avx2) return vx_launch_gemm<2, M, true>(W, a, st);
+        return vx_launch_gemm<2, M, false>(W, a, st);
     }
-    if (X->avx2) return vxh_fail(VXH_ERR_UNSUPPORTED, "AVX2-lane panels apply to Q4_0 only");
-    return vx_launch_mfma<8, M, false>(W, X, ep, ws, st);
+    if (avx2) return vxh_fail(VXH_ERR_UNSUPPORTED, "AVX2-lane panels apply to Q4_0 only");
+    return vx_launch_gemm<8, M, false>(W, a, st);
 }
 
-extern "C" int vxh_gemm(const vxh_qmat *W, const vxh_panel *X, int M, const vxh_epilogue *e,
-                        vxh_workspace *ws, int path, vxh_stream s)
+extern "C" int vxh_gemm_acc(const vxh_qmat *W, const vxh_panel *X, int M, double *acc, int ld_acc,
+                            int n_out, float scale, const float *gate, int ld_gate, float thr,
+                            int path, vxh_stream s)
 {
     if (M != X->M || M < 1 || M > 16)
         return vxh_fail(VXH_ERR_PARAM, "gemm: M %d (panel M %d)", M, X->M);
     if (W->n_cols != X->K)
         return vxh_fail(VXH_ERR_PARAM, "gemm: W has K %d, panel %d", W->n_cols, X->K);
+    if (n_out < 0 || n_out > W->n_rows || (n_out > ld_acc && M > 1))
+        return vxh_fail(VXH_ERR_PARAM, "gemm: n_out %d (rows %d, ld %d)", n_out, W->n_rows, ld_acc);
     if (path == VXH_PATH_DOT)
         return vxh_fail(VXH_ERR_UNSUPPORTED, "dot-product path not built for this shape");
-    vx_epi ep{X->rscale, e->kind, e->y, e->ldy, e->r, e->ldr, e->thr, e->scale, e->n_out};
+    if (n_out == 0) return VXH_OK;
+    vx_gemm_args a;
+    memset(&a, 0, sizeof(a));
+    a.wq = (const uint4 *)W->qs;
+    a.wd = (const uint32_t *)W->d;
+    a.panel = (const uint4 *)X->data;
+    a.corr = X->corr;
+    a.rscale = X->rscale;
+    a.acc = acc;
+    a.ld_acc = ld_acc;
+    a.n_out = n_out;
+    a.scale = scale;
+    a.gate = gate;
+    a.ld_gate = ld_gate;
+    a.thr = thr;
+    a.k.lo4 = 0x000F000Fu;
+    a.k.hi4 = 0x00F000F0u;
+    a.k.lo8 = 0x00FF00FFu;
+    a.k.magic = 0x64006400u;
     hipStream_t st = vxh_hs(s);
     switch (M) {
-    case 1: return vx_dispatch_m<1>(W, X, ep, ws, st);
-    case 2: return vx_dispatch_m<2>(W, X, ep, ws, st);
-    case 3: return vx_dispatch_m<3>(W, X, ep, ws, st);
-    case 4: return vx_dispatch_m<4>(W, X, ep, ws, st);
-    case 5: return vx_dispatch_m<5>(W, X, ep, ws, st);
-    case 6: return vx_dispatch_m<6>(W, X, ep, ws, st);
-    case 7: return vx_dispatch_m<7>(W, X, ep, ws, st);
-    case 8: return vx_dispatch_m<8>(W, X, ep, ws, st);
-    case 9: return vx_dispatch_m<9>(W, X, ep, ws, st);
-    case 10: return vx_dispatch_m<10>(W, X, ep, ws, st);
-    case 11: return vx_dispatch_m<11>(W, X, ep, ws, st);
-    case 12: return vx_dispatch_m<12>(W, X, ep, ws, st);
-    case 13: return vx_dispatch_m<13>(W, X, ep, ws, st);
-    case 14: return vx_dispatch_m<14>(W, X, ep, ws, st);
-    case 15: return vx_dispatch_m<15>(W, X, ep, ws, st);
-    default: return vx_dispatch_m<16>(W, X, ep, ws, st);
+    case 1: return vx_dispatch_m<1>(W, X->avx2, a, st);
+    case 2: return vx_dispatch_m<2>(W, X->avx2, a, st);
+    case 3: return vx_dispatch_m<3>(W, X->avx2, a, st);
+    case 4: return vx_dispatch_m<4>(W, X->avx2, a, st);
+    case 5: return vx_dispatch_m<5>(W, X->avx2, a, st);
+    case 6: return vx_dispatch_m<6>(W, X->avx2, a, st);
+    case 7: return vx_dispatch_m<7>(W, X->avx2, a, st);
+    case 8: return vx_dispatch_m<8>(W, X->avx2, a, st);
+    case 9: return vx_dispatch_m<9>(W, X->avx2, a, st);
+    case 10: return vx_dispatch_m<10>(W, X->avx2, a, st);
+    case 11: return vx_dispatch_m<11>(W, X->avx2, a, st);
+    case 12: return vx_dispatch_m<12>(W, X->avx2, a, st);
+    case 13: return vx_dispatch_m<13>(W, X->avx2, a, st);
+    case 14: return vx_dispatch_m<14>(W, X->avx2, a, st);
+    case 15: return vx_dispatch_m<15>(W, X->avx2, a, st);
+    default: return vx_dispatch_m<16>(W, X->avx2, a, st);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// accumulator consumers
+// ---------------------------------------------------------------------------
+// y may alias r (x += acc in place)
+__global__ void vx_acc_store_kernel(double *__restrict__ acc, int ld_acc, int n, float *y, int ldy,
+                                    const float *r, int ldr)
+{
+    const int m = blockIdx.y;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        double *p = acc + (size_t)m * ld_acc + i;
+        const float v = (float)*p;
+        *p = 0.0;
+        y[(size_t)m * ldy + i] = r ? r[(size_t)m * ldr + i] + v : v;
+    }
+}
+
+extern "C" int vxh_acc_store(double *acc, int ld_acc, int M, int n, float *y, int ldy,
+                             const float *r, int ldr, vxh_stream s)
+{
+    if (M <= 0 || n <= 0) return VXH_OK;
+    int gx = (n + 255) / 256;
+    if (gx > 256) gx = 256;
+    vx_acc_store_kernel<<<dim3(gx, M), 256, 0, vxh_hs(s)>>>(acc, ld_acc, n, y, ldy, r, ldr);
+    VXH_LAUNCHED();
+    return VXH_OK;
+}
+
+__global__ void vx_acc_swiglu_kernel(double *__restrict__ acc, int ld_acc, int F, float thr,
+                                     float *__restrict__ h, int ldh)
+{
+    const int m = blockIdx.y;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < F; i += gridDim.x * blockDim.x) {
+        double *pg = acc + (size_t)m * ld_acc + 32 * (i / 16) + i % 16;
+        const float g = vx_silu((float)pg[0]), u = (float)pg[16];
+        pg[0] = 0.0;
+        pg[16] = 0.0;
+        h[(size_t)m * ldh + i] = fabsf(g) < thr ? 0.0f : g * u;
+    }
+}
+
+extern "C" int vxh_acc_swiglu(double *acc, int ld_acc, int M, int F, float thr, float *h, int ldh,
+                              vxh_stream s)
+{
+    if (M <= 0 || F <= 0) return VXH_OK;
+    int gx = (F + 255) / 256;
+    if (gx > 256) gx = 256;
+    vx_acc_swiglu_kernel<<<dim3(gx, M), 256, 0, vxh_hs(s)>>>(acc, ld_acc, F, thr, h, ldh);
+    VXH_LAUNCHED();
+    return VXH_OK;
+}
+
+extern "C" size_t vxh_gemm_workspace_elems(int n_rows, int M)
+{
+    return (size_t)M * (size_t)((n_rows + 31) / 32 * 32);
+}
+
+extern "C" int vxh_gemm(const vxh_qmat *W, const vxh_panel *X, int M, const vxh_epilogue *e,
+                        vxh_workspace *ws, int path, vxh_stream s)
+{
+    const int ld = W->n_rows;
+    if (!ws->acc || ws->acc_elems < vxh_gemm_workspace_elems(W->n_rows, M))
+        return vxh_fail(VXH_ERR_PARAM, "gemm workspace too small: need %zu elements",
+                        vxh_gemm_workspace_elems(W->n_rows, M));
+    int rc;
+    switch (e->kind) {
+    case VXH_EPI_STORE:
+    case VXH_EPI_RESID:
+        rc = vxh_gemm_acc(W, X, M, ws->acc, ld, e->n_out, e->scale, NULL, 0, 0.0f, path, s);
+        if (rc) return rc;
+        return vxh_acc_store(ws->acc, ld, M, e->n_out, e->y, e->ldy,
+                             e->kind == VXH_EPI_RESID ? e->r : NULL, e->ldr, s);
+    case VXH_EPI_GATE:
+        rc = vxh_gemm_acc(W, X, M, ws->acc, ld, e->n_out, e->scale, e->r, e->ldr, e->thr, path, s);
+        if (rc) return rc;
+        return vxh_acc_store(ws->acc, ld, M, e->n_out, e->y, e->ldy, NULL, 0, s);
+    case VXH_EPI_SWIGLU: {
+        const int phys = (e->n_out + 15) / 16 * 32;
+        if (phys > W->n_rows)
+            return vxh_fail(VXH_ERR_PARAM, "swiglu: F %d needs %d rows", e->n_out, phys);
+        rc = vxh_gemm_acc(W, X, M, ws->acc, ld, phys, e->scale, NULL, 0, 0.0f, path, s);
+        if (rc) return rc;
+        return vxh_acc_swiglu(ws->acc, ld, M, e->n_out, e->thr, e->y, e->ldy, s);
+    }
+    default:
+        return vxh_fail(VXH_ERR_PARAM, "gemm: epilogue kind %d", e->kind);
     }
 }

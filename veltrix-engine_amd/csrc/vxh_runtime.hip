@@ -207,25 +207,25 @@ extern "C" int vxh_graph_destroy(vxh_graph g)
     return VXH_OK;
 }
 
-extern "C" int vxh_workspace_alloc(vxh_workspace *w, size_t part_floats, int n_counters)
+extern "C" int vxh_workspace_alloc(vxh_workspace *w, size_t acc_elems, size_t part_floats)
 {
     memset(w, 0, sizeof(*w));
-    int rc = vxh_malloc((void **)&w->part, part_floats * sizeof(float));
+    int rc = vxh_malloc((void **)&w->acc, acc_elems * sizeof(double));
     if (rc) return rc;
-    rc = vxh_malloc((void **)&w->counters, (size_t)n_counters * sizeof(unsigned));
-    if (rc) { vxh_free(w->part); w->part = nullptr; return rc; }
-    // counters start at zero; every user resets the counter it used
-    VXH_CHECK(hipMemset(w->counters, 0, (size_t)n_counters * sizeof(unsigned)));
+    rc = vxh_malloc((void **)&w->part, part_floats * sizeof(float));
+    if (rc) { vxh_free(w->acc); w->acc = nullptr; return rc; }
+    // the accumulator starts zeroed; every consumer clears what it reads
+    VXH_CHECK(hipMemset(w->acc, 0, acc_elems * sizeof(double)));
     VXH_CHECK(hipDeviceSynchronize());
+    w->acc_elems = acc_elems;
     w->part_floats = part_floats;
-    w->n_counters = n_counters;
     return VXH_OK;
 }
 
 extern "C" int vxh_workspace_free(vxh_workspace *w)
 {
+    vxh_free(w->acc);
     vxh_free(w->part);
-    vxh_free(w->counters);
     memset(w, 0, sizeof(*w));
     return VXH_OK;
 }

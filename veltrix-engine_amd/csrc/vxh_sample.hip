@@ -59,6 +59,10 @@ __device__ __forceinline__ uint64_t vx_wg_sum_u64(uint64_t v, uint64_t *red)
 }
 
 // First index of the maximum (strict '>' scan order, src/speculative.c:93-98).
+// Lanes start from (-inf, 0x7fffffff); a row with no value above -inf (all
+// NaN or all -inf) keeps that sentinel, which maps to index 0 -- the
+// reference's scan also stays on its first element -- so callers can always
+// index the row with the result.
 __device__ __forceinline__ int vx_wg_argmax(float v, int idx, float *redv, int *redi)
 {
     for (int o = 32; o > 0; o >>= 1) {
@@ -73,7 +77,7 @@ __device__ __forceinline__ int vx_wg_argmax(float v, int idx, float *redv, int *
     for (int i = 1; i < SB / 64; i++)
         if (redv[i] > bv || (redv[i] == bv && redi[i] < bi)) { bv = redv[i]; bi = redi[i]; }
     __syncthreads();
-    return bi;
+    return bi == 0x7fffffff ? 0 : bi;
 }
 
 // Thread t owns the contiguous index range [t*chunk, min((t+1)*chunk, n)).

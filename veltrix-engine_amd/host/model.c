@@ -154,6 +154,7 @@ static vx_tensor *add_tensor(vx_model *m, int cap, const char *name, int type, i
 /* device state                                                                 */
 /* --------------------------------------------------------------------------- */
 static int gu_rows(int F) { return (F + 15) / 16 * 32; }
+static int round32(int n) { return (n + 31) / 32 * 32; }
 static void prof_free(vx_dev *d);
 
 static void dev_free(vx_dev *d)
@@ -172,8 +173,9 @@ static void dev_free(vx_dev *d)
     vxh_qmat_free(&d->out);
     vxh_free(d->out_norm);
     vxh_free(d->rope_cos); vxh_free(d->rope_sin);
-    vxh_free(d->tok); vxh_free(d->x); vxh_free(d->xn); vxh_free(d->xtail); vxh_free(d->qkv);
-    vxh_free(d->q); vxh_free(d->att); vxh_free(d->h); vxh_free(d->logits);
+    vxh_free(d->tok); vxh_free(d->x); vxh_free(d->xn); vxh_free(d->xtail);
+    vxh_free(d->q); vxh_free(d->att); vxh_free(d->logits);
+    vxh_free(d->acc_qkv); vxh_free(d->acc_x); vxh_free(d->acc_gu); vxh_free(d->acc_lg);
     vxh_free(d->stats); vxh_free(d->acc_out); vxh_free(d->pos_dev);
     vxh_panel_free(&d->pan_d);
     vxh_panel_free(&d->pan_f);
@@ -220,11 +222,17 @@ static vx_error dev_alloc_common(vx_model *m)
     TRY(vxh_malloc((void **)&d->xn, sizeof(float) * B * d->d));
     TRY(vxh_malloc((void **)&d->xtail, sizeof(float) * B * 4));
     TRY(vxh_fill_f32(d->xtail, 0.0f, B * 4, d->stream));
-    TRY(vxh_malloc((void **)&d->qkv, sizeof(float) * B * (d->d + 2 * d->kvd)));
     TRY(vxh_malloc((void **)&d->q, sizeof(float) * B * d->d));
     TRY(vxh_malloc((void **)&d->att, sizeof(float) * B * d->d));
-    TRY(vxh_malloc((void **)&d->h, sizeof(float) * B * d->F));
     TRY(vxh_malloc((void **)&d->logits, sizeof(float) * B * (size_t)d->V));
+    d->ld_qkv = round32(d->d + 2 * d->kvd);
+    d->ld_gu = gu_rows(d->F);
+    d->ld_lg = round32(d->V);
+    TRY(vxh_malloc((void **)&d->acc_qkv, sizeof(double) * B * (size_t)d->ld_qkv));
+    TRY(vxh_malloc((void **)&d->acc_x, sizeof(double) * B * (size_t)d->d));
+    TRY(vxh_malloc((void **)&d->acc_gu, sizeof(double) * B * (size_t)d->ld_gu));
+    TRY(vxh_malloc((void **)&d->acc_lg, sizeof(double) * B * (size_t)d->ld_lg));
+    d->acc_dirty = 1;                  /* zeroed before the first forward */
     TRY(vxh_malloc((void **)&d->stats, sizeof(float) * (B + 1) * 3));
     TRY(vxh_malloc((void **)&d->acc_out, sizeof(int) * (B + 4)));
     TRY(vxh_malloc((void **)&d->pos_dev, sizeof(int) * 4));
@@ -248,31 +256,15 @@ static vx_error upload_f32(vx_dev *d, float **dst, const void *src, int n)
     return VX_OK;
 }
 
-/* Workspace large enough for every GEMM of the model at M = 16 and for the
- * attention at n_ctx. */
+/* Workspace of the attention partials at n_ctx (the model's GEMMs use its
+ * own accumulators, so the workspace accumulator is a token). */
 static vx_error dev_alloc_workspace(vx_dev *d, int n_ctx, int cap)
 {
     const int B = VX_MAX_BATCH;
-    size_t need = 0;
-    int counters = d->n_kv + 1;
-#define NEED(rows, cols)                                                       \
-    do {                                                                       \
-        size_t f_ = vxh_gemm_workspace_floats((rows), (cols), B);              \
-        if (f_ > need) need = f_;                                              \
-        int c_ = vxh_gemm_workspace_counters(rows);                            \
-        if (c_ > counters) counters = c_;                                      \
-    } while (0)
-    NEED(d->d + 2 * d->kvd, d->d);
-    NEED(d->d, d->d);
-    NEED(gu_rows(d->F), d->d);
-    NEED(d->d, d->F);
-    NEED(d->V, d->d);
-#undef NEED
     size_t an = vxh_attention_workspace_floats(B, n_ctx, cap, d->n_heads, d->n_kv, d->hd);
-    if (an > need) need = an;
-    if (d->ws.part && d->ws.part_floats >= need && d->ws.n_counters >= counters) return VX_OK;
+    if (d->ws.part && d->ws.part_floats >= an) return VX_OK;
     vxh_workspace_free(&d->ws);
-    TRY(vxh_workspace_alloc(&d->ws, need, counters));
+    TRY(vxh_workspace_alloc(&d->ws, 32, an));
     return VX_OK;
 }
 
@@ -713,8 +705,9 @@ vx_error vx_model_get_profile(vx_model *m, vx_gemm_profile prof[VX_PROF_N])
     return e;
 }
 
-static vx_error gemm(vx_dev *d, const vxh_qmat *W, vxh_panel *P, int M, int kind, float *y, int ldy,
-                     const float *r, int ldr, int n_out, int cls, int rows_logical)
+/* acc[m][n] += scale * (W x_m)[n] for n < n_out (fp64 accumulator). */
+static vx_error gemm(vx_dev *d, const vxh_qmat *W, vxh_panel *P, int M, double *acc, int ld_acc,
+                     int n_out, int cls, int rows_logical)
 {
     int slot = -1;
     if (d->prof_on) {
@@ -729,30 +722,40 @@ static vx_error gemm(vx_dev *d, const vxh_qmat *W, vxh_panel *P, int M, int kind
         d->prof_flops[slot] = 2.0 * M * (double)rows_logical * W->n_cols;
         TRY(vxh_event_record(d->prof_ev[2 * slot], d->stream));
     }
-    vxh_epilogue ep;
-    ep.kind = kind;
-    ep.y = y;
-    ep.ldy = ldy;
-    ep.r = r;
-    ep.ldr = ldr;
-    ep.thr = d->opt.ffn_gate_threshold;
-    ep.scale = scale_for(d, W->type);
-    ep.n_out = n_out;
-    TRY(vxh_gemm(W, P, M, &ep, &d->ws, VXH_PATH_AUTO, d->stream));
+    TRY(vxh_gemm_acc(W, P, M, acc, ld_acc, n_out, scale_for(d, W->type), NULL, 0, 0.0f,
+                     VXH_PATH_AUTO, d->stream));
     if (slot >= 0) TRY(vxh_event_record(d->prof_ev[2 * slot + 1], d->stream));
     return VX_OK;
 }
 
+static vx_error zero_acc(vx_dev *d)
+{
+    const int B = VX_MAX_BATCH;
+    vxh_stream s = d->stream;
+    TRY(vxh_fill_f32((float *)d->acc_qkv, 0.0f, 2 * (size_t)B * d->ld_qkv, s));
+    TRY(vxh_fill_f32((float *)d->acc_x, 0.0f, 2 * (size_t)B * d->d, s));
+    TRY(vxh_fill_f32((float *)d->acc_gu, 0.0f, 2 * (size_t)B * d->ld_gu, s));
+    TRY(vxh_fill_f32((float *)d->acc_lg, 0.0f, 2 * (size_t)B * d->ld_lg, s));
+    d->acc_dirty = 0;
+    return VX_OK;
+}
+
+/* One batched forward.  Every GEMM adds into an fp64 accumulator that the
+ * next kernel consumes (and clears): q|k|v -> RoPE/KV write, attention
+ * output projection and down projection -> the residual + RMSNorm panel of
+ * the next block, gate/up -> the SwiGLU panel, logits -> a store. */
 vx_error vx_dev_forward(vx_model *m, int M, int n_past, int logits_mode)
 {
     vx_dev *d = vx_dev_of(m);
     if (M < 1 || M > VX_MAX_BATCH) return VX_ERR_PARAM;
     const int dd = d->d, kvd = d->kvd, F = d->F, V = d->V, n_ctx = d->n_ctx_alloc;
     const int avx2 = d->opt.q4_kernel == VX_Q4_AVX2_LANES;
-    const int ldqkv = dd + 2 * kvd;
+    const float thr = d->opt.ffn_gate_threshold;
     vxh_stream s = d->stream;
     vx_error e;
 
+    if (d->acc_dirty && (e = zero_acc(d)) != VX_OK) return e;
+    d->acc_dirty = 1;
     if (d->has_embd) TRY(vxh_qmat_gather_rows(&d->embd, d->tok, M, vx_get_synthetic_weight_scale(), d->x, dd, s));
     else TRY(vxh_fill_f32(d->x, 0.0f, (size_t)M * dd, s));
 
@@ -760,32 +763,36 @@ vx_error vx_dev_forward(vx_model *m, int M, int n_past, int logits_mode)
         vx_dev_layer *Ld = &d->layers[l];
         float *kc = m->k_cache + (size_t)l * n_ctx * kvd;
         float *vc = m->v_cache + (size_t)l * n_ctx * kvd;
-        TRY(vxh_rmsnorm_panel(d->x, dd, M, dd, Ld->attn_norm, avx2, d->x, dd, &d->pan_d,
-                              (avx2 && Ld->has_o) ? d->xn : NULL, dd, s));
-        if ((e = gemm(d, &Ld->wqkv, &d->pan_d, M, VXH_EPI_STORE, d->qkv, ldqkv, NULL, 0, ldqkv,
-                      VX_PROF_QKV, ldqkv)))
+        /* x += previous down projection; attention RMSNorm; QKV tail = x[0..3] */
+        TRY(vxh_resid_rmsnorm_panel(d->x, dd, d->acc_x, dd, M, dd, Ld->attn_norm, avx2, 1, &d->pan_d,
+                                    (avx2 && Ld->has_o) ? d->xn : NULL, dd, s));
+        if ((e = gemm(d, &Ld->wqkv, &d->pan_d, M, d->acc_qkv, d->ld_qkv, dd + 2 * kvd, VX_PROF_QKV,
+                      dd + 2 * kvd)))
             return e;
-        TRY(vxh_rope_kv(d->qkv, ldqkv, M, n_past, n_ctx, d->n_heads, d->n_kv, d->hd, Ld->bq, Ld->bk,
-                        Ld->bv, d->rope_cos, d->rope_sin, d->n_pos, d->q, kc, vc, s));
+        TRY(vxh_rope_kv(d->acc_qkv, d->ld_qkv, M, n_past, n_ctx, d->n_heads, d->n_kv, d->hd, Ld->bq,
+                        Ld->bk, Ld->bv, d->rope_cos, d->rope_sin, d->n_pos, d->q, kc, vc, s));
         TRY(vxh_attention(d->q, M, n_past, n_ctx, d->n_heads, d->n_kv, d->hd, d->opt.attn_cap, kc, vc,
                           d->att, dd, &d->ws, s));
         if (Ld->has_o) {
+            /* attn_o's x86-build tail is the normed x (src/model.c:426, :544) */
             TRY(vxh_prep_panel(&d->pan_d, d->att, dd, M, dd, avx2, d->xn, dd, s));
-            if ((e = gemm(d, &Ld->wo, &d->pan_d, M, VXH_EPI_RESID, d->x, dd, d->x, dd, dd, VX_PROF_O, dd)))
-                return e;
+            if ((e = gemm(d, &Ld->wo, &d->pan_d, M, d->acc_x, dd, dd, VX_PROF_O, dd))) return e;
         } else {
             TRY(vxh_add_rows(d->x, dd, d->att, dd, M, dd, s));
         }
+        /* x += attention output; FFN RMSNorm; gate/up tail = x[0..3] */
+        TRY(vxh_resid_rmsnorm_panel(d->x, dd, d->acc_x, dd, M, dd, Ld->ffn_norm, avx2, 1, &d->pan_d,
+                                    NULL, 0, s));
         /* the logits' x86-build tail reads the last layer's post-attention
          * residual (src/model.c:426, :547) */
         if (avx2 && l == d->n_layers - 1) TRY(vxh_copy_rows(d->xtail, 4, d->x, dd, M, 4, s));
-        TRY(vxh_rmsnorm_panel(d->x, dd, M, dd, Ld->ffn_norm, avx2, d->x, dd, &d->pan_d, NULL, 0, s));
-        if ((e = gemm(d, &Ld->wgu, &d->pan_d, M, VXH_EPI_SWIGLU, d->h, F, NULL, 0, F, VX_PROF_GATEUP, 2 * F)))
+        if ((e = gemm(d, &Ld->wgu, &d->pan_d, M, d->acc_gu, d->ld_gu, d->ld_gu, VX_PROF_GATEUP, 2 * F)))
             return e;
-        TRY(vxh_prep_panel(&d->pan_f, d->h, F, M, F, avx2, NULL, 0, s));
-        if ((e = gemm(d, &Ld->wd, &d->pan_f, M, VXH_EPI_RESID, d->x, dd, d->x, dd, dd, VX_PROF_DOWN, dd)))
-            return e;
+        TRY(vxh_swiglu_panel(d->acc_gu, d->ld_gu, M, F, thr, avx2, &d->pan_f, NULL, 0, s));
+        if ((e = gemm(d, &Ld->wd, &d->pan_f, M, d->acc_x, dd, dd, VX_PROF_DOWN, dd))) return e;
     }
+    /* x += last down projection (clears the residual accumulator) */
+    TRY(vxh_acc_store(d->acc_x, dd, M, dd, d->x, dd, d->x, dd, s));
 
     if (logits_mode != VX_LOGITS_NONE) {
         int rows = logits_mode == VX_LOGITS_LAST ? 1 : M;
@@ -798,10 +805,13 @@ vx_error vx_dev_forward(vx_model *m, int M, int n_past, int logits_mode)
             TRY(vxh_prep_panel(&d->pan_d, src, dd, rows, dd, avx2, tail, 4, s));
         int orows = d->has_out ? d->out_rows : 0;
         if (orows < V) TRY(vxh_fill_rows(d->logits, V, rows, orows, V - orows, -1e30f, s));
-        if (d->has_out && (e = gemm(d, &d->out, &d->pan_d, rows, VXH_EPI_STORE, d->logits, V, NULL, 0, orows,
-                                    VX_PROF_OUTPUT, orows)))
-            return e;
+        if (d->has_out) {
+            if ((e = gemm(d, &d->out, &d->pan_d, rows, d->acc_lg, d->ld_lg, orows, VX_PROF_OUTPUT, orows)))
+                return e;
+            TRY(vxh_acc_store(d->acc_lg, d->ld_lg, rows, orows, d->logits, V, NULL, 0, s));
+        }
     }
+    d->acc_dirty = 0;
     return VX_OK;
 }
 

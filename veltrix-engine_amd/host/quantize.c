@@ -145,13 +145,12 @@ static int op_panel(int K)
     return rc;
 }
 
-static int op_workspace(int rows, int cols)
+static int op_workspace(int rows)
 {
-    size_t f = vxh_gemm_workspace_floats(rows, cols, VX_MAX_BATCH);
-    int c = vxh_gemm_workspace_counters(rows);
-    if (g_op.ws.part && g_op.ws.part_floats >= f && g_op.ws.n_counters >= c) return VXH_OK;
+    size_t n = vxh_gemm_workspace_elems(rows, VX_MAX_BATCH);
+    if (g_op.ws.acc && g_op.ws.acc_elems >= n) return VXH_OK;
     vxh_workspace_free(&g_op.ws);
-    return vxh_workspace_alloc(&g_op.ws, f, c);
+    return vxh_workspace_alloc(&g_op.ws, n, 32);
 }
 
 static void report(const char *what, int rc)
@@ -179,7 +178,7 @@ static int run_gemm(int type, const void *A, const float *X, int ldx, float *Y, 
     vxh_qmat W;
     if ((rc = vxh_qmat_alloc(&W, type, rows, K))) return rc;
     if ((rc = vxh_qmat_set_rows(&W, A, 0, rows, rows, 0, 0, g_op.s))) goto out;
-    if ((rc = op_panel(K)) || (rc = op_workspace(rows, K))) goto out;
+    if ((rc = op_panel(K)) || (rc = op_workspace(rows))) goto out;
     if ((rc = grow(&g_op.x, &g_op.x_cap, (size_t)VX_MAX_BATCH * K))) goto out;
     if ((rc = grow(&g_op.y, &g_op.y_cap, (size_t)VX_MAX_BATCH * rows))) goto out;
     if (gate) {
@@ -222,6 +221,11 @@ static int run_gemm(int type, const void *A, const float *X, int ldx, float *Y, 
     }
 out:
     vxh_stream_sync(g_op.s);
+    /* a failed call may leave part of a GEMM in the accumulator */
+    if (rc && g_op.ws.acc) {
+        vxh_fill_f32((float *)g_op.ws.acc, 0.0f, 2 * g_op.ws.acc_elems, g_op.s);
+        vxh_stream_sync(g_op.s);
+    }
     vxh_qmat_free(&W);
     return rc;
 }
@@ -292,6 +296,11 @@ static int run_dequant(int type, const void *x, float *y, int n)
     rc = vxh_download(y, g_op.x, sizeof(float) * (size_t)n, g_op.s);
 out:
     vxh_stream_sync(g_op.s);
+    /* a failed call may leave part of a GEMM in the accumulator */
+    if (rc && g_op.ws.acc) {
+        vxh_fill_f32((float *)g_op.ws.acc, 0.0f, 2 * g_op.ws.acc_elems, g_op.s);
+        vxh_stream_sync(g_op.s);
+    }
     vxh_qmat_free(&W);
     return rc;
 }

@@ -72,7 +72,12 @@ typedef struct vx_dev {
     int n_pos;
     /* activations, VX_MAX_BATCH rows */
     int *tok;                          /* [16]                                      */
-    float *x, *xn, *xtail, *qkv, *q, *att, *h, *logits;
+    float *x, *xn, *xtail, *q, *att, *logits;
+    /* fp64 GEMM accumulators (zero between uses; each consumer clears what
+     * it reads): q|k|v rows, residual-stream updates, gate/up, logits */
+    double *acc_qkv, *acc_x, *acc_gu, *acc_lg;
+    int ld_qkv, ld_gu, ld_lg;
+    int acc_dirty;                     /* a forward failed part-way: re-zero first */
     vxh_panel pan_d, pan_f;
     vxh_workspace ws;
     /* sampling buffers */
