@@ -172,30 +172,80 @@ __global__ __launch_bounds__(ATT_THREADS) void vx_attention_kernel(
     }
 }
 
-// One workgroup per (row m, head): rescale the chunks' partial results to
-// the global max and normalise by 1/(sum + 1e-10) (src/tensor.c:156-171).
-__global__ void vx_attention_combine_kernel(const float *__restrict__ part, int M, int n_heads,
-                                            int n_kv, int hd, int n_chunks, float *__restrict__ out,
-                                            int ld_out)
+// One workgroup per (row m, head): merge the chunks' partial results with
+// the online-softmax rescale and normalise by 1/(sum + 1e-10)
+// (src/tensor.c:156-171).  Thread t owns float4 lane d4 = t % (hd/4) of the
+// head and every S-th chunk starting at t / (hd/4) (S = 256/(hd/4) slices);
+// its running (max, sum, acc) is merged across the slices in LDS, so the
+// chunk walk is spread over the workgroup instead of serialised per thread.
+#define CMB_THREADS 256
+__global__ __launch_bounds__(CMB_THREADS) void vx_attention_combine_kernel(
+    const float *__restrict__ part, int M, int n_heads, int n_kv, int hd, int n_chunks,
+    float *__restrict__ out, int ld_out)
 {
+    __shared__ float4 s_acc[CMB_THREADS];
+    __shared__ float s_m[CMB_THREADS], s_l[CMB_THREADS];
     const int m = blockIdx.x % M, head = blockIdx.x / M;
     const int G = n_heads / n_kv, QM = G * M;
     const int g = head / G, hl = head % G;
     const int qi = hl * M + m;
-    const float *pg = part + (size_t)g * n_chunks * QM * (hd + 2);
-    float gm = -INFINITY;
-    for (int c2 = 0; c2 < n_chunks; c2++) gm = fmaxf(gm, pg[((size_t)c2 * QM + qi) * (hd + 2)]);
-    for (int d = threadIdx.x; d < hd; d += blockDim.x) {
-        float l = 0.0f, a = 0.0f;
-        for (int c2 = 0; c2 < n_chunks; c2++) {
-            const float *pc = pg + ((size_t)c2 * QM + qi) * (hd + 2);
-            float cm = pc[0];
-            if (cm == -INFINITY) continue;
-            float f = expf(cm - gm);
-            l = fmaf(f, pc[1], l);
-            a = fmaf(f, pc[2 + d], a);
+    const int L4 = hd / 4, S = CMB_THREADS / L4;
+    const int d4 = threadIdx.x % L4, sl = threadIdx.x / L4;
+    const size_t cstride = (size_t)QM * (hd + 2);
+    const float *pq = part + (size_t)g * n_chunks * cstride + (size_t)qi * (hd + 2);
+
+    float mx = -INFINITY, l = 0.0f;
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (sl < S) {
+        for (int c0 = sl; c0 < n_chunks; c0 += 4 * S) {
+            float cm[4], cl[4];
+            float4 ca[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int c = c0 + u * S;
+                const float *pc = pq + (size_t)min(c, n_chunks - 1) * cstride;
+                cm[u] = c < n_chunks ? pc[0] : -INFINITY;
+                cl[u] = pc[1];
+                ca[u] = *(const float4 *)(pc + 2 + 4 * d4);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                if (cm[u] == -INFINITY) continue;
+                const float nm = fmaxf(mx, cm[u]);
+                const float fo = mx == -INFINITY ? 0.0f : expf(mx - nm);
+                const float fn = expf(cm[u] - nm);
+                l = l * fo + cl[u] * fn;
+                a.x = a.x * fo + ca[u].x * fn;
+                a.y = a.y * fo + ca[u].y * fn;
+                a.z = a.z * fo + ca[u].z * fn;
+                a.w = a.w * fo + ca[u].w * fn;
+                mx = nm;
+            }
         }
-        out[(size_t)m * ld_out + (size_t)head * hd + d] = a * (1.0f / (l + 1e-10f));
+    }
+    s_m[threadIdx.x] = mx;
+    s_l[threadIdx.x] = l;
+    s_acc[threadIdx.x] = a;
+    __syncthreads();
+    if (sl == 0) {
+        float gm = -INFINITY;
+        for (int j = 0; j < S; j++) gm = fmaxf(gm, s_m[j * L4 + d4]);
+        float lt = 0.0f;
+        float4 at = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int j = 0; j < S; j++) {
+            const float cm = s_m[j * L4 + d4];
+            if (cm == -INFINITY) continue;
+            const float f = expf(cm - gm);
+            const float4 v = s_acc[j * L4 + d4];
+            lt = fmaf(f, s_l[j * L4 + d4], lt);
+            at.x = fmaf(f, v.x, at.x);
+            at.y = fmaf(f, v.y, at.y);
+            at.z = fmaf(f, v.z, at.z);
+            at.w = fmaf(f, v.w, at.w);
+        }
+        const float inv = 1.0f / (lt + 1e-10f);
+        *(float4 *)(out + (size_t)m * ld_out + (size_t)head * hd + 4 * d4) =
+            make_float4(at.x * inv, at.y * inv, at.z * inv, at.w * inv);
     }
 }
 
@@ -247,7 +297,7 @@ extern "C" int vxh_attention(const float *q, int M, int n_past, int n_ctx, int n
         q, M, n_past, n_ctx, n_heads, n_kv_heads, head_dim, cap, kc, vc, n_chunks, qpg, n_qg,
         ws->part);
     VXH_LAUNCHED();
-    vx_attention_combine_kernel<<<M * n_heads, head_dim < 64 ? 64 : head_dim, 0, vxh_hs(s)>>>(
+    vx_attention_combine_kernel<<<M * n_heads, CMB_THREADS, 0, vxh_hs(s)>>>(
         ws->part, M, n_heads, n_kv_heads, head_dim, n_chunks, out, ld_out);
     VXH_LAUNCHED();
     return VXH_OK;
