@@ -441,22 +441,26 @@ extern "C" int vxh_rmsnorm(const float *x, int ldx, int M, int K, const float *w
 // ---------------------------------------------------------------------------
 // MFMA GEMM
 // ---------------------------------------------------------------------------
+// (q & mask) | magic in one v_and_or_b32.  The compiler splits it into a
+// v_and / v_or pair (gfx9 VOP3 encodings take no literal), so it is written
+// out; the mask travels in an SGPR and the magic word in a VGPR.
+__device__ __forceinline__ uint32_t vx_and_or(uint32_t q, uint32_t mask, uint32_t magic)
+{
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(q), "s"(mask), "v"(magic));
+    return r;
+}
+
 // Q4_0 dword (8 nibbles in the repacked slot order) -> 8 fp16 values s - 8:
 // 1024 + s (low nibble) and 1024 + 16 s (high nibble) by exponent magic,
-// then one packed add / fma per pair.  The masks and the magic word arrive
-// as kernel arguments (SGPRs), so each (q & mask) | magic is one
-// v_and_or_b32 (gfx9 VOP3 encodings cannot carry a literal).
-struct vx_consts {
-    uint32_t lo4, hi4, lo8, magic;
-};
-
-__device__ __forceinline__ vx_half8 vx_unpack_q4(uint32_t q, const vx_consts &k)
+// then one packed add / fma per pair.
+__device__ __forceinline__ vx_half8 vx_unpack_q4(uint32_t q, uint32_t magic)
 {
     const uint32_t q8 = q >> 8;
-    vx_half2 a = __builtin_bit_cast(vx_half2, (q & k.lo4) | k.magic);
-    vx_half2 b = __builtin_bit_cast(vx_half2, (q & k.hi4) | k.magic);
-    vx_half2 c = __builtin_bit_cast(vx_half2, (q8 & k.lo4) | k.magic);
-    vx_half2 d = __builtin_bit_cast(vx_half2, (q8 & k.hi4) | k.magic);
+    vx_half2 a = __builtin_bit_cast(vx_half2, vx_and_or(q, 0x000F000Fu, magic));
+    vx_half2 b = __builtin_bit_cast(vx_half2, vx_and_or(q, 0x00F000F0u, magic));
+    vx_half2 c = __builtin_bit_cast(vx_half2, vx_and_or(q8, 0x000F000Fu, magic));
+    vx_half2 d = __builtin_bit_cast(vx_half2, vx_and_or(q8, 0x00F000F0u, magic));
     const vx_half2 off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
     const vx_half2 sc = {(_Float16)0.0625f, (_Float16)0.0625f};
     const vx_half2 off16 = {(_Float16)-72.0f, (_Float16)-72.0f};
@@ -470,13 +474,14 @@ __device__ __forceinline__ vx_half8 vx_unpack_q4(uint32_t q, const vx_consts &k)
 
 // Two Q8_0 dwords (4 int8 each, bytes in the repacked order) -> 8 fp16:
 // (q ^ 0x80) = q + 128 as an unsigned byte, 1024 + that by exponent magic.
-__device__ __forceinline__ vx_half8 vx_unpack_q8(uint32_t qa, uint32_t qb, const vx_consts &k)
+__device__ __forceinline__ vx_half8 vx_unpack_q8(uint32_t qa, uint32_t qb, uint32_t magic)
 {
+    const uint32_t m = 0x00FF00FFu;
     const uint32_t ua = qa ^ 0x80808080u, ub = qb ^ 0x80808080u;
-    vx_half2 a0 = __builtin_bit_cast(vx_half2, (ua & k.lo8) | k.magic);
-    vx_half2 a1 = __builtin_bit_cast(vx_half2, ((ua >> 8) & k.lo8) | k.magic);
-    vx_half2 b0 = __builtin_bit_cast(vx_half2, (ub & k.lo8) | k.magic);
-    vx_half2 b1 = __builtin_bit_cast(vx_half2, ((ub >> 8) & k.lo8) | k.magic);
+    vx_half2 a0 = __builtin_bit_cast(vx_half2, vx_and_or(ua, m, magic));
+    vx_half2 a1 = __builtin_bit_cast(vx_half2, vx_and_or(ua >> 8, m, magic));
+    vx_half2 b0 = __builtin_bit_cast(vx_half2, vx_and_or(ub, m, magic));
+    vx_half2 b1 = __builtin_bit_cast(vx_half2, vx_and_or(ub >> 8, m, magic));
     const vx_half2 off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
     a0 = a0 + off;
     a1 = a1 + off;
@@ -494,12 +499,19 @@ struct vx_mcfg {
     static constexpr int R1 = M <= 4 ? M : (M <= 8 ? 4 : (4 + (M - 8 < 4 ? M - 8 : 4)));
 };
 
-// Block pairs per K slice: 16 keeps ~1-3k wavefronts on the big verify
-// shapes; small M and the largest M (LDS) use 8.
+// Block pairs per K slice.  Each M has up to three slice lengths (in
+// ascending order); the launcher takes the shortest one whose launch stays
+// within VX_WG_TARGET workgroups, or the longest.  Short slices suit the small
+// draft matrices at M = 1, long ones the large verify matrices; M > 12 stays
+// short for LDS.
 template <int QT, int M>
-struct vx_ppw {
-    static constexpr int value = QT == 8 ? 8 : ((M <= 4 || M > 12) ? 8 : 16);
+struct vx_ppw_set {
+    static constexpr int n = QT == 8 ? (M <= 4 ? 2 : 1) : (M <= 4 ? 3 : 2);
+    static constexpr int v0 = QT == 8 ? (M <= 4 ? 2 : 8) : (M <= 4 ? 2 : (M <= 12 ? 8 : 4));
+    static constexpr int v1 = QT == 8 ? 8 : (M <= 4 ? 4 : (M <= 12 ? 16 : 8));
+    static constexpr int v2 = QT == 8 ? 8 : (M <= 4 ? 8 : (M <= 12 ? 16 : 8));
 };
+#define VX_WG_TARGET 1600
 
 struct vx_gemm_args {
     const uint4 *wq;
@@ -515,16 +527,14 @@ struct vx_gemm_args {
     const float *gate;
     int ld_gate;
     float thr;
-    vx_consts k;
 };
 
 #define VX_RING 4
 
 // QT: 2 = Q4_0, 8 = Q8_0.
-template <int QT, int M, bool AVX2>
+template <int QT, int M, bool AVX2, int PPW>
 __global__ __launch_bounds__(256) void vx_gemm_kernel(vx_gemm_args a)
 {
-    constexpr int PPW = vx_ppw<QT, M>::value;
     constexpr int NS = vx_mcfg<M>::NS;
     constexpr int R1 = vx_mcfg<M>::R1;
     constexpr int WPP = QT == 2 ? 1 : 2;   // 16-byte weight loads per lane per block pair
@@ -542,6 +552,7 @@ __global__ __launch_bounds__(256) void vx_gemm_kernel(vx_gemm_args a)
     const int np = min(PPW, a.n_pairs - p0);
     const int units = np * 8 * NS;
     const int c = lane & 31, h = lane >> 5;
+    const uint32_t magic = 0x64006400u;
 
     // 1. the panel slice (issued first so its wait does not cover the weights)
     const uint4 *psrc = a.panel + (size_t)p0 * 8 * NS;
@@ -600,11 +611,11 @@ __global__ __launch_bounds__(256) void vx_gemm_kernel(vx_gemm_args a)
                 const int bl = 2 * i + blk;
                 vx_half8 b0, b1;
                 if (QT == 2) {
-                    b0 = vx_unpack_q4(blk ? wv[0].z : wv[0].x, a.k);
-                    b1 = vx_unpack_q4(blk ? wv[0].w : wv[0].y, a.k);
+                    b0 = vx_unpack_q4(blk ? wv[0].z : wv[0].x, magic);
+                    b1 = vx_unpack_q4(blk ? wv[0].w : wv[0].y, magic);
                 } else {
-                    b0 = vx_unpack_q8(wv[blk].x, wv[blk].y, a.k);
-                    b1 = vx_unpack_q8(wv[blk].z, wv[blk].w, a.k);
+                    b0 = vx_unpack_q8(wv[blk].x, wv[blk].y, magic);
+                    b1 = vx_unpack_q8(wv[blk].z, wv[blk].w, magic);
                 }
                 const vx_half8 a0 = __builtin_bit_cast(vx_half8, lds[((bl * 2 + 0) * 2 + h) * NS + slot]);
                 const vx_half8 a1 = __builtin_bit_cast(vx_half8, lds[((bl * 2 + 1) * 2 + h) * NS + slot]);
@@ -639,17 +650,30 @@ __global__ __launch_bounds__(256) void vx_gemm_kernel(vx_gemm_args a)
     }
 }
 
-template <int QT, int M, bool AVX2>
-static int vx_launch_gemm(const vxh_qmat *W, vx_gemm_args &a, hipStream_t st)
+template <int QT, int M, bool AVX2, int PPW>
+static int vx_launch_ppw(const vxh_qmat *W, vx_gemm_args &a, hipStream_t st)
 {
-    constexpr int PPW = vx_ppw<QT, M>::value;
     a.n_tiles = W->n_rows / 32;
     a.n_pairs = W->n_pairs;
     a.n_splits = (W->n_pairs + PPW - 1) / PPW;
     const int groups = (a.n_tiles + 3) / 4;
-    vx_gemm_kernel<QT, M, AVX2><<<groups * a.n_splits, 256, 0, st>>>(a);
+    vx_gemm_kernel<QT, M, AVX2, PPW><<<groups * a.n_splits, 256, 0, st>>>(a);
     VXH_LAUNCHED();
     return VXH_OK;
+}
+
+template <int QT, int M, bool AVX2>
+static int vx_launch_gemm(const vxh_qmat *W, vx_gemm_args &a, hipStream_t st)
+{
+    typedef vx_ppw_set<QT, M> S;
+    const long groups = (W->n_rows / 32 + 3) / 4;
+    const int cand[3] = {S::v0, S::v1, S::v2};
+    int pick = S::n - 1;
+    for (int i = 0; i < S::n; i++)
+        if (groups * ((W->n_pairs + cand[i] - 1) / cand[i]) <= VX_WG_TARGET) { pick = i; break; }
+    if (pick == 0) return vx_launch_ppw<QT, M, AVX2, S::v0>(W, a, st);
+    if (pick == 1) return vx_launch_ppw<QT, M, AVX2, S::v1>(W, a, st);
+    return vx_launch_ppw<QT, M, AVX2, S::v2>(W, a, st);
 }
 
 template <int M>
@@ -690,10 +714,6 @@ extern "C" int vxh_gemm_acc(const vxh_qmat *W, const vxh_panel *X, int M, double
     a.gate = gate;
     a.ld_gate = ld_gate;
     a.thr = thr;
-    a.k.lo4 = 0x000F000Fu;
-    a.k.hi4 = 0x00F000F0u;
-    a.k.lo8 = 0x00FF00FFu;
-    a.k.magic = 0x64006400u;
     hipStream_t st = vxh_hs(s);
     switch (M) {
     case 1: return vx_dispatch_m<1>(W, X->avx2, a, st);
