@@ -305,7 +305,7 @@ def run_spec(args):
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
             "traffic": read_traffic(),
-            "kernel": f"vx_gemm_mfma_kernel (Q4_0, M={args.k + 1}), all verify GEMM launches",
+            "kernel": f"vx_gemm_kernel (Q4_0, M={args.k + 1}), all verify GEMM launches (kernel-execution events)",
             "launches": launches,
             "avg_launch_us": round(1e3 * ms / max(launches, 1), 3),
             "bytes_per_launch": round(byt / max(launches, 1)),
@@ -344,6 +344,17 @@ def run_gemm(args):
 
     M = args.k + 1
     results = []
+    # calibration for rocprofv3 byte counters: a device-to-device copy of a
+    # known size (FETCH_SIZE and WRITE_SIZE of that copy should read 256 MiB)
+    cal_bytes = 256 << 20
+    ca, cb = N.DevBuf(L, nbytes=cal_bytes), N.DevBuf(L, nbytes=cal_bytes)
+    L.vxh_copy.argtypes = [vp, vp, CC.c_size_t, vp]
+    for _ in range(3):
+        assert L.vxh_copy(cb.ptr, ca.ptr, cal_bytes, None) == 0
+    L.vxh_device_sync()
+    log(json.dumps({"calibration_copy_bytes": cal_bytes, "copies": 3}))
+    ca.free()
+    cb.free()
     for rows, cols, qt in ((4096, 4096, 2), (12288, 4096, 2), (4096, 11008, 2), (22016, 4096, 2),
                            (32000, 4096, 2), (11008, 4096, 8), (4096, 11008, 8)):
         bpw = 18 if qt == 2 else 34

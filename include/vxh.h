@@ -179,6 +179,12 @@ enum { VXH_PATH_AUTO = 0, VXH_PATH_MFMA = 1, VXH_PATH_DOT = 2 };
 int vxh_gemm_acc(const vxh_qmat *W, const vxh_panel *X, int M, double *acc, int ld_acc,
                  int n_out, float scale, const float *gate, int ld_gate, float thr, int path,
                  vxh_stream s);
+/* vxh_gemm_acc with the kernel's execution bracketed by two events that the
+ * dispatch itself records (start and end of the kernel, no extra packets):
+ * vxh_event_elapsed_ms(start, stop) is the kernel's own duration. */
+int vxh_gemm_acc_timed(const vxh_qmat *W, const vxh_panel *X, int M, double *acc, int ld_acc,
+                       int n_out, float scale, const float *gate, int ld_gate, float thr, int path,
+                       vxh_event start, vxh_event stop, vxh_stream s);
 /* y[m][i] = (r ? r[m][i] : 0) + (float)acc[m][i] for i < n; acc cleared. */
 int vxh_acc_store(double *acc, int ld_acc, int M, int n, float *y, int ldy, const float *r,
                   int ldr, vxh_stream s);

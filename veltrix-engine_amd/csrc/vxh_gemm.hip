@@ -22,6 +22,8 @@
 // before the next GEMM that targets it.
 #include <string.h>
 
+#include <hip/hip_ext.h>
+
 #include "vxh_internal.h"
 
 // ---------------------------------------------------------------------------
@@ -651,19 +653,25 @@ __global__ __launch_bounds__(256) void vx_gemm_kernel(vx_gemm_args a)
 }
 
 template <int QT, int M, bool AVX2, int PPW>
-static int vx_launch_ppw(const vxh_qmat *W, vx_gemm_args &a, hipStream_t st)
+static int vx_launch_ppw(const vxh_qmat *W, vx_gemm_args &a, hipStream_t st, hipEvent_t e0,
+                         hipEvent_t e1)
 {
     a.n_tiles = W->n_rows / 32;
     a.n_pairs = W->n_pairs;
     a.n_splits = (W->n_pairs + PPW - 1) / PPW;
     const int groups = (a.n_tiles + 3) / 4;
-    vx_gemm_kernel<QT, M, AVX2, PPW><<<groups * a.n_splits, 256, 0, st>>>(a);
+    if (e0 || e1)   // events recorded by the dispatch itself around the kernel
+        hipExtLaunchKernelGGL(vx_gemm_kernel<QT, M, AVX2, PPW>, dim3(groups * a.n_splits), dim3(256), 0,
+                              st, e0, e1, 0, a);
+    else
+        vx_gemm_kernel<QT, M, AVX2, PPW><<<groups * a.n_splits, 256, 0, st>>>(a);
     VXH_LAUNCHED();
     return VXH_OK;
 }
 
 template <int QT, int M, bool AVX2>
-static int vx_launch_gemm(const vxh_qmat *W, vx_gemm_args &a, hipStream_t st)
+static int vx_launch_gemm(const vxh_qmat *W, vx_gemm_args &a, hipStream_t st, hipEvent_t e0,
+                          hipEvent_t e1)
 {
     typedef vx_ppw_set<QT, M> S;
     const long groups = (W->n_rows / 32 + 3) / 4;
@@ -671,25 +679,26 @@ static int vx_launch_gemm(const vxh_qmat *W, vx_gemm_args &a, hipStream_t st)
     int pick = S::n - 1;
     for (int i = 0; i < S::n; i++)
         if (groups * ((W->n_pairs + cand[i] - 1) / cand[i]) <= VX_WG_TARGET) { pick = i; break; }
-    if (pick == 0) return vx_launch_ppw<QT, M, AVX2, S::v0>(W, a, st);
-    if (pick == 1) return vx_launch_ppw<QT, M, AVX2, S::v1>(W, a, st);
-    return vx_launch_ppw<QT, M, AVX2, S::v2>(W, a, st);
+    if (pick == 0) return vx_launch_ppw<QT, M, AVX2, S::v0>(W, a, st, e0, e1);
+    if (pick == 1) return vx_launch_ppw<QT, M, AVX2, S::v1>(W, a, st, e0, e1);
+    return vx_launch_ppw<QT, M, AVX2, S::v2>(W, a, st, e0, e1);
 }
 
 template <int M>
-static int vx_dispatch_m(const vxh_qmat *W, int avx2, vx_gemm_args &a, hipStream_t st)
+static int vx_dispatch_m(const vxh_qmat *W, int avx2, vx_gemm_args &a, hipStream_t st, hipEvent_t e0,
+                         hipEvent_t e1)
 {
     if (W->type == 2) {
-        if (avx2) return vx_launch_gemm<2, M, true>(W, a, st);
-        return vx_launch_gemm<2, M, false>(W, a, st);
+        if (avx2) return vx_launch_gemm<2, M, true>(W, a, st, e0, e1);
+        return vx_launch_gemm<2, M, false>(W, a, st, e0, e1);
     }
     if (avx2) return vxh_fail(VXH_ERR_UNSUPPORTED, "AVX2-lane panels apply to Q4_0 only");
-    return vx_launch_gemm<8, M, false>(W, a, st);
+    return vx_launch_gemm<8, M, false>(W, a, st, e0, e1);
 }
 
-extern "C" int vxh_gemm_acc(const vxh_qmat *W, const vxh_panel *X, int M, double *acc, int ld_acc,
-                            int n_out, float scale, const float *gate, int ld_gate, float thr,
-                            int path, vxh_stream s)
+extern "C" int vxh_gemm_acc_timed(const vxh_qmat *W, const vxh_panel *X, int M, double *acc,
+                                  int ld_acc, int n_out, float scale, const float *gate, int ld_gate,
+                                  float thr, int path, vxh_event start, vxh_event stop, vxh_stream s)
 {
     if (M != X->M || M < 1 || M > 16)
         return vxh_fail(VXH_ERR_PARAM, "gemm: M %d (panel M %d)", M, X->M);
@@ -715,24 +724,33 @@ extern "C" int vxh_gemm_acc(const vxh_qmat *W, const vxh_panel *X, int M, double
     a.ld_gate = ld_gate;
     a.thr = thr;
     hipStream_t st = vxh_hs(s);
+    hipEvent_t e0 = (hipEvent_t)start, e1 = (hipEvent_t)stop;
     switch (M) {
-    case 1: return vx_dispatch_m<1>(W, X->avx2, a, st);
-    case 2: return vx_dispatch_m<2>(W, X->avx2, a, st);
-    case 3: return vx_dispatch_m<3>(W, X->avx2, a, st);
-    case 4: return vx_dispatch_m<4>(W, X->avx2, a, st);
-    case 5: return vx_dispatch_m<5>(W, X->avx2, a, st);
-    case 6: return vx_dispatch_m<6>(W, X->avx2, a, st);
-    case 7: return vx_dispatch_m<7>(W, X->avx2, a, st);
-    case 8: return vx_dispatch_m<8>(W, X->avx2, a, st);
-    case 9: return vx_dispatch_m<9>(W, X->avx2, a, st);
-    case 10: return vx_dispatch_m<10>(W, X->avx2, a, st);
-    case 11: return vx_dispatch_m<11>(W, X->avx2, a, st);
-    case 12: return vx_dispatch_m<12>(W, X->avx2, a, st);
-    case 13: return vx_dispatch_m<13>(W, X->avx2, a, st);
-    case 14: return vx_dispatch_m<14>(W, X->avx2, a, st);
-    case 15: return vx_dispatch_m<15>(W, X->avx2, a, st);
-    default: return vx_dispatch_m<16>(W, X->avx2, a, st);
+    case 1: return vx_dispatch_m<1>(W, X->avx2, a, st, e0, e1);
+    case 2: return vx_dispatch_m<2>(W, X->avx2, a, st, e0, e1);
+    case 3: return vx_dispatch_m<3>(W, X->avx2, a, st, e0, e1);
+    case 4: return vx_dispatch_m<4>(W, X->avx2, a, st, e0, e1);
+    case 5: return vx_dispatch_m<5>(W, X->avx2, a, st, e0, e1);
+    case 6: return vx_dispatch_m<6>(W, X->avx2, a, st, e0, e1);
+    case 7: return vx_dispatch_m<7>(W, X->avx2, a, st, e0, e1);
+    case 8: return vx_dispatch_m<8>(W, X->avx2, a, st, e0, e1);
+    case 9: return vx_dispatch_m<9>(W, X->avx2, a, st, e0, e1);
+    case 10: return vx_dispatch_m<10>(W, X->avx2, a, st, e0, e1);
+    case 11: return vx_dispatch_m<11>(W, X->avx2, a, st, e0, e1);
+    case 12: return vx_dispatch_m<12>(W, X->avx2, a, st, e0, e1);
+    case 13: return vx_dispatch_m<13>(W, X->avx2, a, st, e0, e1);
+    case 14: return vx_dispatch_m<14>(W, X->avx2, a, st, e0, e1);
+    case 15: return vx_dispatch_m<15>(W, X->avx2, a, st, e0, e1);
+    default: return vx_dispatch_m<16>(W, X->avx2, a, st, e0, e1);
     }
+}
+
+extern "C" int vxh_gemm_acc(const vxh_qmat *W, const vxh_panel *X, int M, double *acc, int ld_acc,
+                            int n_out, float scale, const float *gate, int ld_gate, float thr,
+                            int path, vxh_stream s)
+{
+    return vxh_gemm_acc_timed(W, X, M, acc, ld_acc, n_out, scale, gate, ld_gate, thr, path, nullptr,
+                              nullptr, s);
 }
 
 // ---------------------------------------------------------------------------

@@ -720,11 +720,10 @@ static vx_error gemm(vx_dev *d, const vxh_qmat *W, vxh_panel *P, int M, double *
         double wb = (double)rows_logical * W->n_cols / 32.0 * (W->type == VX_TYPE_Q4_0 ? 18.0 : 34.0);
         d->prof_bytes[slot] = wb + 4.0 * M * W->n_cols + 4.0 * M * n_out;
         d->prof_flops[slot] = 2.0 * M * (double)rows_logical * W->n_cols;
-        TRY(vxh_event_record(d->prof_ev[2 * slot], d->stream));
     }
-    TRY(vxh_gemm_acc(W, P, M, acc, ld_acc, n_out, scale_for(d, W->type), NULL, 0, 0.0f,
-                     VXH_PATH_AUTO, d->stream));
-    if (slot >= 0) TRY(vxh_event_record(d->prof_ev[2 * slot + 1], d->stream));
+    TRY(vxh_gemm_acc_timed(W, P, M, acc, ld_acc, n_out, scale_for(d, W->type), NULL, 0, 0.0f,
+                           VXH_PATH_AUTO, slot >= 0 ? d->prof_ev[2 * slot] : NULL,
+                           slot >= 0 ? d->prof_ev[2 * slot + 1] : NULL, d->stream));
     return VX_OK;
 }
 
