@@ -71,19 +71,23 @@ extern "C" int vxh_rope_kv(double *qkv, int ld_qkv, int M, int n_past, int n_ctx
 // of ACH positions, query group).  The G = n_heads/n_kv query heads of the
 // kv head times the M rows form QM query vectors; the chunk's K and V rows
 // are loaded once (all loads issued before the first use) into LDS and used
-// by all of them.  Each workgroup writes (max, sum, acc[hd]) per query; a
-// second kernel combines the chunks with the online-softmax rescale.
+// by all of them.  Scores: one thread per (query, position), float4 LDS
+// reads; softmax of a query across its 32 lanes with shuffles; P.V: one
+// thread per (query, 4 channels).  Each workgroup writes (max, sum, acc[hd])
+// per query at a stride of hd + 4 floats (acc 16-byte aligned at offset 4);
+// a second kernel combines the chunks with the online-softmax rescale.
 // ---------------------------------------------------------------------------
 #define ACH 32
 #define ATT_THREADS 256
 #define ATT_MAX_HD 128
+#define PART_STRIDE(hd) ((hd) + 4)
 
 __global__ __launch_bounds__(ATT_THREADS) void vx_attention_kernel(
     const float *__restrict__ q, int M, int n_past, int n_ctx, int n_heads, int n_kv, int hd,
     int cap, const float *__restrict__ kc, const float *__restrict__ vc, int n_chunks, int qpg,
     int n_qg, float *__restrict__ part)
 {
-    extern __shared__ float sm[];
+    extern __shared__ float4 sm4[];
     const int per_g = n_chunks * n_qg;
     const int g = blockIdx.x / per_g;
     const int ch = (blockIdx.x % per_g) / n_qg, qg = blockIdx.x % n_qg;
@@ -93,17 +97,16 @@ __global__ __launch_bounds__(ATT_THREADS) void vx_attention_kernel(
     const int nq = min(qpg, QM - q0);       // queries of this workgroup: [q0, q0 + nq)
     const int kvd = n_kv * hd;
     const int t0 = ch * ACH;
-    const int hdp = hd + 1;
-    float *sq = sm;                       // [nq][hd]
-    float *sk = sq + nq * hd;             // [ACH][hd+1]
-    float *sv = sk + ACH * hdp;           // [ACH][hd]
-    float *ss = sv + ACH * hd;            // [nq][ACH]
+    const int hd4 = hd / 4, kp4 = hd4 + 1;  // K rows padded by one float4
+    float4 *sq4 = sm4;                      // [nq][hd4]
+    float4 *sk4 = sq4 + nq * hd4;           // [ACH][kp4]
+    float4 *sv4 = sk4 + ACH * kp4;          // [ACH][hd4]
+    float *sp = (float *)(sv4 + ACH * hd4); // [nq][ACH]
     const float scale = 1.0f / sqrtf((float)hd);
 
     // K/V chunk: ACH*hd/4 float4 each, at most 4 per thread; rows past the
     // cache end read as zeros (their scores are masked below)
     constexpr int KV4 = ACH * ATT_MAX_HD / 4 / ATT_THREADS;
-    const int hd4 = hd / 4;
     float4 kr[KV4], vr[KV4];
 #pragma unroll
     for (int j = 0; j < KV4; j++) {
@@ -117,58 +120,69 @@ __global__ __launch_bounds__(ATT_THREADS) void vx_attention_kernel(
     for (int i = threadIdx.x; i < nq * hd4; i += ATT_THREADS) {
         const int ql = i / hd4, d4 = i % hd4;
         const int qi = q0 + ql, hl = qi / M, m = qi % M;
-        const float4 v = *(const float4 *)(q + (size_t)m * n_heads * hd + (size_t)(g * G + hl) * hd + 4 * d4);
-        *(float4 *)(sq + ql * hd + 4 * d4) = v;
+        sq4[ql * hd4 + d4] = *(const float4 *)(q + (size_t)m * n_heads * hd + (size_t)(g * G + hl) * hd + 4 * d4);
     }
 #pragma unroll
     for (int j = 0; j < KV4; j++) {
         const int i = j * ATT_THREADS + threadIdx.x;
         const int t = i / hd4, d4 = i % hd4;
         if (t < ACH) {
-            float *k = sk + t * hdp + 4 * d4;
-            k[0] = kr[j].x; k[1] = kr[j].y; k[2] = kr[j].z; k[3] = kr[j].w;
-            *(float4 *)(sv + t * hd + 4 * d4) = vr[j];
+            sk4[t * kp4 + d4] = kr[j];
+            sv4[t * hd4 + d4] = vr[j];
         }
     }
     __syncthreads();
 
+    // scores and the chunk's softmax statistics; a query's 32 positions are
+    // the 32 lanes of one half-wave (ATT_THREADS and ACH are multiples of 32)
+    const size_t ps = PART_STRIDE(hd);
+    float *pstat = part + ((size_t)g * n_chunks + ch) * QM * ps;
     for (int i = threadIdx.x; i < nq * ACH; i += ATT_THREADS) {
-        int ql = i / ACH, t = i % ACH;
-        int m = (q0 + ql) % M;
-        int pos = n_past + m < n_ctx ? n_past + m : n_ctx - 1;
+        const int ql = i / ACH, t = i % ACH;
+        const int m = (q0 + ql) % M;
+        const int pos = n_past + m < n_ctx ? n_past + m : n_ctx - 1;
         int cs = pos + 1;
         if (cap > 0 && cs > cap) cs = cap;
         float sc = -INFINITY;
         if (t0 + t < cs) {
-            float a = 0.0f;
-            const float *qv = sq + ql * hd;
-            const float *kv = sk + t * hdp;
-            for (int d = 0; d < hd; d++) a = fmaf(qv[d], kv[d], a);
-            sc = a * scale;
+            const float4 *qv = sq4 + ql * hd4;
+            const float4 *kv = sk4 + t * kp4;
+            float a0 = 0.0f, a1 = 0.0f;
+            for (int d4 = 0; d4 < hd4; d4++) {
+                const float4 x = qv[d4], y = kv[d4];
+                a0 = fmaf(x.x, y.x, a0);
+                a1 = fmaf(x.y, y.y, a1);
+                a0 = fmaf(x.z, y.z, a0);
+                a1 = fmaf(x.w, y.w, a1);
+            }
+            sc = (a0 + a1) * scale;
         }
-        ss[i] = sc;
+        float mx = sc;
+        for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 32));
+        const float e = mx == -INFINITY ? 0.0f : expf(sc - mx);
+        float l = e;
+        for (int o = 16; o > 0; o >>= 1) l += __shfl_xor(l, o, 32);
+        sp[ql * ACH + t] = e;
+        if (t == 0) {
+            pstat[(size_t)(q0 + ql) * ps + 0] = mx;
+            pstat[(size_t)(q0 + ql) * ps + 1] = l;
+        }
     }
     __syncthreads();
-
-    float *pstat = part + ((size_t)g * n_chunks + ch) * QM * (hd + 2);
-    for (int ql = threadIdx.x; ql < nq; ql += ATT_THREADS) {
-        float mx = -INFINITY;
-        for (int t = 0; t < ACH; t++) mx = fmaxf(mx, ss[ql * ACH + t]);
-        float l = 0.0f;
+    for (int i = threadIdx.x; i < nq * hd4; i += ATT_THREADS) {
+        const int ql = i / hd4, d4 = i % hd4;
+        const float *pr = sp + ql * ACH;
+        float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 8
         for (int t = 0; t < ACH; t++) {
-            float e = mx == -INFINITY ? 0.0f : expf(ss[ql * ACH + t] - mx);
-            ss[ql * ACH + t] = e;
-            l += e;
+            const float p = pr[t];
+            const float4 v = sv4[t * hd4 + d4];
+            a.x = fmaf(p, v.x, a.x);
+            a.y = fmaf(p, v.y, a.y);
+            a.z = fmaf(p, v.z, a.z);
+            a.w = fmaf(p, v.w, a.w);
         }
-        pstat[(size_t)(q0 + ql) * (hd + 2) + 0] = mx;
-        pstat[(size_t)(q0 + ql) * (hd + 2) + 1] = l;
-    }
-    __syncthreads();
-    for (int i = threadIdx.x; i < nq * hd; i += ATT_THREADS) {
-        int ql = i / hd, d = i % hd;
-        float a = 0.0f;
-        for (int t = 0; t < ACH; t++) a = fmaf(ss[ql * ACH + t], sv[t * hd + d], a);
-        pstat[(size_t)(q0 + ql) * (hd + 2) + 2 + d] = a;
+        *(float4 *)(pstat + (size_t)(q0 + ql) * ps + 4 + 4 * d4) = a;
     }
 }
 
@@ -191,8 +205,8 @@ __global__ __launch_bounds__(CMB_THREADS) void vx_attention_combine_kernel(
     const int qi = hl * M + m;
     const int L4 = hd / 4, S = CMB_THREADS / L4;
     const int d4 = threadIdx.x % L4, sl = threadIdx.x / L4;
-    const size_t cstride = (size_t)QM * (hd + 2);
-    const float *pq = part + (size_t)g * n_chunks * cstride + (size_t)qi * (hd + 2);
+    const size_t cstride = (size_t)QM * PART_STRIDE(hd);
+    const float *pq = part + (size_t)g * n_chunks * cstride + (size_t)qi * PART_STRIDE(hd);
 
     float mx = -INFINITY, l = 0.0f;
     float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -206,7 +220,7 @@ __global__ __launch_bounds__(CMB_THREADS) void vx_attention_combine_kernel(
                 const float *pc = pq + (size_t)min(c, n_chunks - 1) * cstride;
                 cm[u] = c < n_chunks ? pc[0] : -INFINITY;
                 cl[u] = pc[1];
-                ca[u] = *(const float4 *)(pc + 2 + 4 * d4);
+                ca[u] = *(const float4 *)(pc + 4 + 4 * d4);
             }
 #pragma unroll
             for (int u = 0; u < 4; u++) {
@@ -252,12 +266,12 @@ __global__ __launch_bounds__(CMB_THREADS) void vx_attention_combine_kernel(
 // LDS of a workgroup holding nq queries; the query split keeps it <= 64 KiB.
 static size_t vx_attn_lds(int nq, int hd)
 {
-    return sizeof(float) * ((size_t)nq * hd + (size_t)ACH * (hd + 1) + (size_t)ACH * hd + (size_t)nq * ACH);
+    return sizeof(float) * ((size_t)nq * hd + (size_t)ACH * (hd + 4) + (size_t)ACH * hd + (size_t)nq * ACH);
 }
 
 static int vx_attn_qpg(int hd)
 {
-    long room = 65536 / 4 - (long)ACH * (2 * hd + 1);
+    long room = 65536 / 4 - (long)ACH * (2 * hd + 4);
     return room > 0 ? (int)(room / (hd + ACH)) : 0;
 }
 
@@ -267,7 +281,7 @@ extern "C" size_t vxh_attention_workspace_floats(int M, int n_ctx, int cap, int 
     int ctx = n_ctx;
     if (cap > 0 && ctx > cap) ctx = cap;
     int n_chunks = (ctx + ACH - 1) / ACH;
-    return (size_t)n_kv_heads * n_chunks * (n_heads / n_kv_heads) * M * (head_dim + 2);
+    return (size_t)n_kv_heads * n_chunks * (n_heads / n_kv_heads) * M * PART_STRIDE(head_dim);
 }
 
 extern "C" int vxh_attention(const float *q, int M, int n_past, int n_ctx, int n_heads,
@@ -289,7 +303,7 @@ extern "C" int vxh_attention(const float *q, int M, int n_past, int n_ctx, int n
     int qpg = vx_attn_qpg(head_dim);
     if (qpg > QM) qpg = QM;
     int n_qg = (QM + qpg - 1) / qpg;
-    size_t need = (size_t)n_kv_heads * n_chunks * QM * (head_dim + 2);
+    size_t need = (size_t)n_kv_heads * n_chunks * QM * PART_STRIDE(head_dim);
     if (need > ws->part_floats)
         return vxh_fail(VXH_ERR_PARAM, "attention workspace too small (%zu floats needed)", need);
     size_t lds = vx_attn_lds(qpg, head_dim);
