@@ -182,7 +182,7 @@ __global__ __launch_bounds__(VX_ROW_THREADS) void vx_row_panel_kernel(vx_row_arg
     // ---- load (and, for the accumulator modes, consume) ----
 #pragma unroll
     for (int j = 0; j < G; j++) {
-        const int g = threadIdx.x + j * VX_ROW_THREADS;
+        const int g = threadIdx.x + j * blockDim.x;
 #pragma unroll
         for (int kk = 0; kk < 8; kk++) v[j][kk] = 0.0f;
         if (g >= ng) continue;
@@ -245,7 +245,7 @@ __global__ __launch_bounds__(VX_ROW_THREADS) void vx_row_panel_kernel(vx_row_arg
         const float inv = vx_rms_inv(ss, K);
 #pragma unroll
         for (int j = 0; j < G; j++) {
-            const int g = threadIdx.x + j * VX_ROW_THREADS;
+            const int g = threadIdx.x + j * blockDim.x;
             if (g >= ng) continue;
             float wv[8];
             if (a.w) {
@@ -263,7 +263,7 @@ __global__ __launch_bounds__(VX_ROW_THREADS) void vx_row_panel_kernel(vx_row_arg
     if (a.out) {
 #pragma unroll
         for (int j = 0; j < G; j++) {
-            const int g = threadIdx.x + j * VX_ROW_THREADS;
+            const int g = threadIdx.x + j * blockDim.x;
             if (g >= ng) continue;
             float *o = a.out + (size_t)m * a.ld_out + 8 * g;
             *(float4 *)o = make_float4(v[j][0], v[j][1], v[j][2], v[j][3]);
@@ -283,7 +283,7 @@ __global__ __launch_bounds__(VX_ROW_THREADS) void vx_row_panel_kernel(vx_row_arg
     if (threadIdx.x == 0) a.rscale[m] = rs;
 #pragma unroll
     for (int j = 0; j < G; j++) {
-        const int g = threadIdx.x + j * VX_ROW_THREADS;
+        const int g = threadIdx.x + j * blockDim.x;
         if (g >= ngp) continue;   // groups of the padding block are zeros
         float u[8];
 #pragma unroll
@@ -319,13 +319,17 @@ __global__ __launch_bounds__(VX_ROW_THREADS) void vx_row_panel_kernel(vx_row_arg
 template <int MODE>
 static int vx_launch_row(const vx_row_args &a, vxh_stream s)
 {
-    const int ng = a.K / 8;
-    if (ng <= VX_ROW_THREADS)
-        vx_row_panel_kernel<MODE, 1><<<a.M, VX_ROW_THREADS, 0, vxh_hs(s)>>>(a);
-    else if (ng <= 2 * VX_ROW_THREADS)
-        vx_row_panel_kernel<MODE, 2><<<a.M, VX_ROW_THREADS, 0, vxh_hs(s)>>>(a);
-    else if (ng <= 3 * VX_ROW_THREADS)
-        vx_row_panel_kernel<MODE, 3><<<a.M, VX_ROW_THREADS, 0, vxh_hs(s)>>>(a);
+    // G groups of 8 per thread, the workgroup just large enough for the row
+    // (padding block included): short rows sync fewer wavefronts
+    const int ngp = (a.K / 32 + 1) / 2 * 2 * 4;
+    const int G = (ngp + VX_ROW_THREADS - 1) / VX_ROW_THREADS;
+    const int threads = ((ngp + G - 1) / G + 63) / 64 * 64;
+    if (G == 1)
+        vx_row_panel_kernel<MODE, 1><<<a.M, threads, 0, vxh_hs(s)>>>(a);
+    else if (G == 2)
+        vx_row_panel_kernel<MODE, 2><<<a.M, threads, 0, vxh_hs(s)>>>(a);
+    else if (G == 3)
+        vx_row_panel_kernel<MODE, 3><<<a.M, threads, 0, vxh_hs(s)>>>(a);
     else
         return vxh_fail(VXH_ERR_PARAM, "row length %d above %d", a.K, VXH_MAX_K);
     VXH_LAUNCHED();
