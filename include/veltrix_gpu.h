@@ -48,7 +48,11 @@ typedef struct {
     int attn_cap;              /* attend to at most the first attn_cap positions;
                                   4096 as the reference (src/model.c:304-305), 0 = none */
     float ffn_gate_threshold;  /* up rows with |silu(gate)| below it are zero; 0.01    */
-    int use_graphs;            /* replay captured HIP graphs for repeated batch shapes */
+    int fused;                 /* 1: GEMMs run the follow-up row work in their last
+                                  workgroups (6 launches per layer); 0 (default):
+                                  separate row kernels, faster on MI355X because the
+                                  last-arriver tail costs ~5 dependent memory round
+                                  trips.  AVX2-lane mode always uses separate kernels. */
 } vx_model_options;
 
 void vx_model_get_options(const vx_model *model, vx_model_options *opt);

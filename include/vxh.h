@@ -227,6 +227,66 @@ size_t vxh_gemm_workspace_elems(int n_rows, int M);
 int vxh_gemm(const vxh_qmat *W, const vxh_panel *X, int M, const vxh_epilogue *ep,
              vxh_workspace *ws, int path, vxh_stream s);
 
+/* ---- fused forward path ---------------------------------------------------------
+ * The same GEMM with the follow-up elementwise work of the reference's
+ * forward (src/model.c:514-594) run inside it: the last workgroup to finish
+ * each group of VXH_CHUNK output columns reads the final sums, writes the
+ * results, clears the accumulator and resets its counter.
+ *
+ * Inputs are "x-panels": panel units as vxh_panel (M rows) whose K columns
+ * are split in chunks of VXH_CHUNK, each chunk scaled by its own power of two;
+ * rs[m * rs_ld + c] is the output scale of chunk c of row m (rs_ld = 1: one
+ * scale per row).  RMSNorm is applied after the product: a panel holding
+ * w .* x with ss[m] = sum x^2 gives W (w .* x) / sqrt(ss[m]/K + 1e-5), equal
+ * to the GEMM of the reference's normalised row w .* (x / rms)
+ * (src/tensor.c:128-142) up to rounding.  ss = NULL: no normalisation. */
+#define VXH_CHUNK 1024
+typedef struct {
+    void *data;        /* device, vxh_panel_bytes(M, K); padding reads as zeros */
+    float *rs;         /* device, [16][rs_ld]                                   */
+    int rs_ld;         /* chunks per row, (K + VXH_CHUNK - 1) / VXH_CHUNK        */
+    double *ss;        /* device [M] sum of squares (producers add into it) or NULL */
+    int M, K;
+} vxh_xpanel;
+
+int vxh_xpanel_alloc(vxh_xpanel *p, int max_M, int K);
+int vxh_xpanel_free(vxh_xpanel *p);
+/* Panel of w .* x[m] (norm_w NULL = ones) with per-chunk scales; adds
+ * sum x[m]^2 into p->ss[m] when p->ss != NULL. */
+int vxh_rows_xpanel(const float *x, int ldx, int M, int K, const float *norm_w, vxh_xpanel *p,
+                    vxh_stream s);
+
+enum {
+    VXH_FEPI_STORE = 1,   /* y[m][n] = out (last_row_only: row M-1 only, as row 0)      */
+    VXH_FEPI_RESID = 2,   /* x[m][n] += out, then out_panel = w .* x, out_panel->ss += x^2 */
+    VXH_FEPI_SWIGLU = 3,  /* h = SwiGLU of the 16-row interleaved gate/up output
+                             (src/model.c:582-585, gate-skip threshold thr) -> out_panel  */
+    VXH_FEPI_ROPE = 4,    /* q | k | v output -> RoPE, q_out and the KV cache (as vxh_rope_kv) */
+};
+typedef struct {
+    int kind;
+    unsigned *counters;   /* device, n_counters words, zero before the call and after it:
+                             64 words (one 256-byte line) per super-group of VXH_CHUNK
+                             output columns (2 VXH_CHUNK for SWIGLU) and per 128 rows   */
+    int n_counters;
+    vxh_xpanel *out_panel;/* RESID, SWIGLU: the next GEMM's input (K = n_out or n_h)     */
+    const float *norm_w;  /* RESID: weight of the next RMSNorm (NULL = ones)             */
+    float *x; int ldx;    /* RESID: residual rows                                        */
+    float *y; int ldy;    /* STORE: output rows                                          */
+    int last_row_only;    /* STORE                                                       */
+    float *h; int ldh;    /* SWIGLU: h rows [M][ldh == n_h] (written; the panel's source) */
+    int n_h;              /* SWIGLU: F                                                   */
+    float thr;            /* SWIGLU: gate-skip threshold                                 */
+    int n_past, n_ctx, n_pos, n_heads, n_kv_heads, head_dim;   /* ROPE, as vxh_rope_kv   */
+    const float *bq, *bk, *bv, *cos_tab, *sin_tab;
+    float *q_out, *k_cache, *v_cache;
+} vxh_fepi;
+/* acc[M][ld_acc] must be zero (it is again on return); ld_acc >= n_out rounded up
+ * to 32; n_out % 32 == 0 except for STORE. */
+int vxh_gemm_fused(const vxh_qmat *W, const vxh_xpanel *X, int M, double *acc, int ld_acc,
+                   int n_out, float scale, const vxh_fepi *e, vxh_event start, vxh_event stop,
+                   vxh_stream s);
+
 /* ---- attention block ---------------------------------------------------------
  * RoPE + KV write (src/tensor.c:173-271 portable branch, src/model.c:291-296):
  * qkv[m] = [q | k | v] (+ optional F32 biases), read from the fp64 GEMM
@@ -248,6 +308,16 @@ int vxh_attention(const float *q, int M, int n_past, int n_ctx, int n_heads, int
                   int head_dim, int cap, const float *k_cache_layer,
                   const float *v_cache_layer, float *out, int ld_out,
                   vxh_workspace *ws, vxh_stream s);
+
+/* vxh_attention whose second launch also builds the output projection's
+ * x-panel p (K = n_heads * head_dim, one scale per row): the last head of
+ * each row to finish reads the row back and writes its panel.  row_counters:
+ * 64 * M device words (one counter per 256-byte line), zero before the call
+ * and after it. */
+int vxh_attention_xpanel(const float *q, int M, int n_past, int n_ctx, int n_heads, int n_kv_heads,
+                         int head_dim, int cap, const float *k_cache_layer,
+                         const float *v_cache_layer, float *out, int ld_out, vxh_workspace *ws,
+                         unsigned *row_counters, vxh_xpanel *p, vxh_stream s);
 
 size_t vxh_attention_workspace_floats(int M, int n_ctx, int cap, int n_heads, int n_kv_heads,
                                       int head_dim);

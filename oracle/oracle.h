@@ -93,7 +93,8 @@ int or_forward(or_model *m, const int *tokens, int n, float *logits);
  * n calls of the reference forward with n_tokens = 1. */
 int or_forward_all(or_model *m, const int *tokens, int n, float *logits_all);
 
-/* ---- acceptance (build-defined semantics, see DESIGN) ------------------ */
+/* ---- acceptance: textbook speculative sampling on softmax probabilities
+ * (the reference compares raw logits, src/speculative.c:167, :205) ------ */
 int  or_argmax(const float *x, int n);
 /* p = softmax(l / T) with the reference's sample_top_p arithmetic
  * (src/speculative.c:44-53).  T must be > 0. */

@@ -193,9 +193,58 @@ __global__ __launch_bounds__(ATT_THREADS) void vx_attention_kernel(
 // its running (max, sum, acc) is merged across the slices in LDS, so the
 // chunk walk is spread over the workgroup instead of serialised per thread.
 #define CMB_THREADS 256
+
+// Panel of row m of att (XP variant): the last head of the row to finish
+// reads the row back (after an agent-scope acquire) and writes its fp16 hi/lo
+// panel with one power-of-two scale (every chunk entry of the row).
+__device__ void vx_att_row_panel(const float *att, int d, int M, int m, uint4 *pan, float *rs,
+                                 int rs_ld)
+{
+    __shared__ float red[CMB_THREADS / 64];
+    __shared__ float s_in;
+    float am = 0.0f;
+    for (int c = 8 * threadIdx.x; c < d; c += 8 * CMB_THREADS)
+        for (int k = 0; k < 8; k++)
+            am = fmaxf(am, fabsf(att[c + k]));
+    for (int o = 32; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = am;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float a = red[0];
+        for (int i = 1; i < CMB_THREADS / 64; i++) a = fmaxf(a, red[i]);
+        float si = 1.0f, so = 1.0f;
+        if (a > 0.0f && isfinite(a)) {
+            int ex;
+            frexpf(a, &ex);
+            si = ldexpf(1.0f, 14 - ex);
+            so = ldexpf(1.0f, ex - 14);
+        }
+        for (int c = 0; c < rs_ld; c++) rs[m * rs_ld + c] = so;
+        s_in = si;
+    }
+    __syncthreads();
+    const float sc = s_in;
+    for (int c = 8 * threadIdx.x; c < d; c += 8 * CMB_THREADS) {
+        float v[8];
+        for (int k = 0; k < 8; k++)
+            v[k] = att[c + k] * sc;
+        vx_half8 hi, lo;
+        for (int k = 0; k < 8; k++) {
+            _Float16 a = (_Float16)v[k];
+            hi[k] = a;
+            lo[k] = (_Float16)(v[k] - (float)a);
+        }
+        const int g = c / 8, b = g >> 2, h = (g >> 1) & 1, s = g & 1;
+        const size_t base = ((size_t)(b * 2 + s) * 2 + h) * (2 * M);
+        pan[base + m] = __builtin_bit_cast(uint4, hi);
+        pan[base + M + m] = __builtin_bit_cast(uint4, lo);
+    }
+}
+
+template <bool XP>
 __global__ __launch_bounds__(CMB_THREADS) void vx_attention_combine_kernel(
     const float *__restrict__ part, int M, int n_heads, int n_kv, int hd, int n_chunks,
-    float *__restrict__ out, int ld_out)
+    float *__restrict__ out, int ld_out, unsigned *cnt, uint4 *pan, float *rs, int rs_ld)
 {
     __shared__ float4 s_acc[CMB_THREADS];
     __shared__ float s_m[CMB_THREADS], s_l[CMB_THREADS];
@@ -258,8 +307,34 @@ __global__ __launch_bounds__(CMB_THREADS) void vx_attention_combine_kernel(
             at.w = fmaf(f, v.w, at.w);
         }
         const float inv = 1.0f / (lt + 1e-10f);
-        *(float4 *)(out + (size_t)m * ld_out + (size_t)head * hd + 4 * d4) =
-            make_float4(at.x * inv, at.y * inv, at.z * inv, at.w * inv);
+        float *o = out + (size_t)m * ld_out + (size_t)head * hd + 4 * d4;
+        if (XP) {
+            // written through to device scope: the row's last head reads it
+            __hip_atomic_store(o + 0, at.x * inv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(o + 1, at.y * inv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(o + 2, at.z * inv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(o + 3, at.w * inv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            *(float4 *)o = make_float4(at.x * inv, at.y * inv, at.z * inv, at.w * inv);
+        }
+    }
+    if constexpr (XP) {
+        __shared__ int s_last;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            // one counter per 256-byte line
+            unsigned *c = cnt + (size_t)m * 64;
+            const unsigned old = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s_last = old + 1 == (unsigned)n_heads;
+            if (s_last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (s_last) {
+            // drop stale cached lines: the other heads wrote through to device scope
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            vx_att_row_panel(out + (size_t)m * ld_out, n_heads * hd, M, m, pan, rs, rs_ld);
+        }
     }
 }
 
@@ -284,10 +359,10 @@ extern "C" size_t vxh_attention_workspace_floats(int M, int n_ctx, int cap, int 
     return (size_t)n_kv_heads * n_chunks * (n_heads / n_kv_heads) * M * PART_STRIDE(head_dim);
 }
 
-extern "C" int vxh_attention(const float *q, int M, int n_past, int n_ctx, int n_heads,
-                             int n_kv_heads, int head_dim, int cap, const float *kc,
-                             const float *vc, float *out, int ld_out, vxh_workspace *ws,
-                             vxh_stream s)
+static int vx_attention_run(const float *q, int M, int n_past, int n_ctx, int n_heads,
+                            int n_kv_heads, int head_dim, int cap, const float *kc, const float *vc,
+                            float *out, int ld_out, vxh_workspace *ws, unsigned *row_counters,
+                            vxh_xpanel *xp, vxh_stream s)
 {
     if (M < 1 || n_kv_heads < 1 || n_heads % n_kv_heads)
         return vxh_fail(VXH_ERR_PARAM, "attention: M %d heads %d kv %d", M, n_heads, n_kv_heads);
@@ -311,10 +386,38 @@ extern "C" int vxh_attention(const float *q, int M, int n_past, int n_ctx, int n
         q, M, n_past, n_ctx, n_heads, n_kv_heads, head_dim, cap, kc, vc, n_chunks, qpg, n_qg,
         ws->part);
     VXH_LAUNCHED();
-    vx_attention_combine_kernel<<<M * n_heads, CMB_THREADS, 0, vxh_hs(s)>>>(
-        ws->part, M, n_heads, n_kv_heads, head_dim, n_chunks, out, ld_out);
+    if (xp)
+        vx_attention_combine_kernel<true><<<M * n_heads, CMB_THREADS, 0, vxh_hs(s)>>>(
+            ws->part, M, n_heads, n_kv_heads, head_dim, n_chunks, out, ld_out, row_counters,
+            (uint4 *)xp->data, xp->rs, xp->rs_ld);
+    else
+        vx_attention_combine_kernel<false><<<M * n_heads, CMB_THREADS, 0, vxh_hs(s)>>>(
+            ws->part, M, n_heads, n_kv_heads, head_dim, n_chunks, out, ld_out, nullptr, nullptr,
+            nullptr, 0);
     VXH_LAUNCHED();
     return VXH_OK;
+}
+
+extern "C" int vxh_attention(const float *q, int M, int n_past, int n_ctx, int n_heads,
+                             int n_kv_heads, int head_dim, int cap, const float *kc,
+                             const float *vc, float *out, int ld_out, vxh_workspace *ws,
+                             vxh_stream s)
+{
+    return vx_attention_run(q, M, n_past, n_ctx, n_heads, n_kv_heads, head_dim, cap, kc, vc, out,
+                            ld_out, ws, nullptr, nullptr, s);
+}
+
+extern "C" int vxh_attention_xpanel(const float *q, int M, int n_past, int n_ctx, int n_heads,
+                                    int n_kv_heads, int head_dim, int cap, const float *kc,
+                                    const float *vc, float *out, int ld_out, vxh_workspace *ws,
+                                    unsigned *row_counters, vxh_xpanel *p, vxh_stream s)
+{
+    if (!p || !row_counters || p->K != n_heads * head_dim)
+        return vxh_fail(VXH_ERR_PARAM, "attention_xpanel: panel K %d, need %d", p ? p->K : -1,
+                        n_heads * head_dim);
+    p->M = M;
+    return vx_attention_run(q, M, n_past, n_ctx, n_heads, n_kv_heads, head_dim, cap, kc, vc, out,
+                            ld_out, ws, row_counters, p, s);
 }
 
 __global__ void vx_add_rows_kernel(float *__restrict__ y, int ldy, const float *__restrict__ x,

@@ -20,11 +20,7 @@
 // no workgroup waits for another.  Consumers read the accumulator and clear
 // it (vxh_acc_*, the residual/SwiGLU panels, RoPE), so it is all zeros again
 // before the next GEMM that targets it.
-#include <string.h>
-
-#include <hip/hip_ext.h>
-
-#include "vxh_internal.h"
+#include "vxh_gemm_core.h"
 
 // ---------------------------------------------------------------------------
 // panels
@@ -126,45 +122,6 @@ __device__ __forceinline__ float vx_block_max(float v, float *red)
     for (int i = 1; i < nw; i++) r = fmaxf(r, red[i]);
     __syncthreads();
     return r;
-}
-
-// inv = 1/sqrt(ss/K + 1e-5) as in the reference (src/tensor.c:134-139);
-// returns 0 when the rms is below 1e-10 (the reference then writes zeros).
-__device__ __forceinline__ float vx_rms_inv(float ss, int K)
-{
-    float rms = sqrtf(ss / (float)K + 1e-5f);
-    return rms < 1e-10f ? 0.0f : 1.0f / rms;
-}
-
-// Power-of-two row scale: s = 2^-e with amax = f * 2^e, f in [0.5, 1), so
-// that every scaled value has magnitude < 1 (fp16 hi/lo keep 22 bits).
-__device__ __forceinline__ float vx_row_scale(float amax, float *rs_out)
-{
-    if (!(amax > 0.0f) || !isfinite(amax)) { *rs_out = 1.0f; return 1.0f; }
-    int e;
-    frexpf(amax, &e);
-    *rs_out = ldexpf(1.0f, e);
-    return ldexpf(1.0f, -e);
-}
-
-__device__ __forceinline__ float vx_silu(float g) { return g / (1.0f + expf(-g)); }
-
-// Panel unit of group g (elements 8g..8g+7): block b = g/4, lane half h =
-// (g/2)%2, MFMA half s = g%2; hi at slot m, lo at slot M+m.
-__device__ __forceinline__ void vx_panel_store(uint4 *__restrict__ panel, int M, int g, int m,
-                                               const float v[8])
-{
-    vx_half8 hi, lo;
-#pragma unroll
-    for (int kk = 0; kk < 8; kk++) {
-        _Float16 a = (_Float16)v[kk];
-        hi[kk] = a;
-        lo[kk] = (_Float16)(v[kk] - (float)a);
-    }
-    const int b = g >> 2, h = (g >> 1) & 1, s = g & 1;
-    const size_t base = ((size_t)(b * 2 + s) * 2 + h) * (2 * M);
-    panel[base + m] = __builtin_bit_cast(uint4, hi);
-    panel[base + M + m] = __builtin_bit_cast(uint4, lo);
 }
 
 // G = groups of 8 elements per thread (K <= 8192 * G <= VXH_MAX_K).
@@ -444,262 +401,6 @@ extern "C" int vxh_rmsnorm(const float *x, int ldx, int M, int K, const float *w
     return VXH_OK;
 }
 
-// ---------------------------------------------------------------------------
-// MFMA GEMM
-// ---------------------------------------------------------------------------
-// (q & mask) | magic in one v_and_or_b32.  The compiler splits it into a
-// v_and / v_or pair (gfx9 VOP3 encodings take no literal), so it is written
-// out; the mask travels in an SGPR and the magic word in a VGPR.
-__device__ __forceinline__ uint32_t vx_and_or(uint32_t q, uint32_t mask, uint32_t magic)
-{
-    uint32_t r;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(q), "s"(mask), "v"(magic));
-    return r;
-}
-
-// Q4_0 dword (8 nibbles in the repacked slot order) -> 8 fp16 values s - 8:
-// 1024 + s (low nibble) and 1024 + 16 s (high nibble) by exponent magic,
-// then one packed add / fma per pair.
-__device__ __forceinline__ vx_half8 vx_unpack_q4(uint32_t q, uint32_t magic)
-{
-    const uint32_t q8 = q >> 8;
-    vx_half2 a = __builtin_bit_cast(vx_half2, vx_and_or(q, 0x000F000Fu, magic));
-    vx_half2 b = __builtin_bit_cast(vx_half2, vx_and_or(q, 0x00F000F0u, magic));
-    vx_half2 c = __builtin_bit_cast(vx_half2, vx_and_or(q8, 0x000F000Fu, magic));
-    vx_half2 d = __builtin_bit_cast(vx_half2, vx_and_or(q8, 0x00F000F0u, magic));
-    const vx_half2 off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
-    const vx_half2 sc = {(_Float16)0.0625f, (_Float16)0.0625f};
-    const vx_half2 off16 = {(_Float16)-72.0f, (_Float16)-72.0f};
-    a = a + off;
-    b = b * sc + off16;
-    c = c + off;
-    d = d * sc + off16;
-    vx_half8 r = {a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
-    return r;
-}
-
-// Two Q8_0 dwords (4 int8 each, bytes in the repacked order) -> 8 fp16:
-// (q ^ 0x80) = q + 128 as an unsigned byte, 1024 + that by exponent magic.
-__device__ __forceinline__ vx_half8 vx_unpack_q8(uint32_t qa, uint32_t qb, uint32_t magic)
-{
-    const uint32_t m = 0x00FF00FFu;
-    const uint32_t ua = qa ^ 0x80808080u, ub = qb ^ 0x80808080u;
-    vx_half2 a0 = __builtin_bit_cast(vx_half2, vx_and_or(ua, m, magic));
-    vx_half2 a1 = __builtin_bit_cast(vx_half2, vx_and_or(ua >> 8, m, magic));
-    vx_half2 b0 = __builtin_bit_cast(vx_half2, vx_and_or(ub, m, magic));
-    vx_half2 b1 = __builtin_bit_cast(vx_half2, vx_and_or(ub >> 8, m, magic));
-    const vx_half2 off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
-    a0 = a0 + off;
-    a1 = a1 + off;
-    b0 = b0 + off;
-    b1 = b1 + off;
-    vx_half8 r = {a0.x, a0.y, a1.x, a1.y, b0.x, b0.y, b1.x, b1.y};
-    return r;
-}
-
-template <int M>
-struct vx_mcfg {
-    static constexpr int NS = 2 * M;
-    // hi accumulator registers in use: register r < R1 holds column
-    // c = 8(r/4) + 4h + r%4 (h = lane/32); lo is register r + 8.
-    static constexpr int R1 = M <= 4 ? M : (M <= 8 ? 4 : (4 + (M - 8 < 4 ? M - 8 : 4)));
-};
-
-// Block pairs per K slice.  Each M has up to three slice lengths (in
-// ascending order); the launcher takes the shortest one whose launch stays
-// within VX_WG_TARGET workgroups, or the longest.  Short slices suit the small
-// draft matrices at M = 1, long ones the large verify matrices; M > 12 stays
-// short for LDS.
-template <int QT, int M>
-struct vx_ppw_set {
-    static constexpr int n = QT == 8 ? (M <= 4 ? 2 : 1) : (M <= 4 ? 3 : 2);
-    static constexpr int v0 = QT == 8 ? (M <= 4 ? 2 : 8) : (M <= 4 ? 2 : (M <= 12 ? 8 : 4));
-    static constexpr int v1 = QT == 8 ? 8 : (M <= 4 ? 4 : (M <= 12 ? 16 : 8));
-    static constexpr int v2 = QT == 8 ? 8 : (M <= 4 ? 8 : (M <= 12 ? 16 : 8));
-};
-#define VX_WG_TARGET 1600
-
-struct vx_gemm_args {
-    const uint4 *wq;
-    const uint32_t *wd;
-    const uint4 *panel;
-    const float *corr;
-    const float *rscale;
-    int n_tiles, n_pairs, n_splits;
-    double *acc;
-    int ld_acc;
-    int n_out;
-    float scale;
-    const float *gate;
-    int ld_gate;
-    float thr;
-};
-
-#define VX_RING 4
-
-// QT: 2 = Q4_0, 8 = Q8_0.
-template <int QT, int M, bool AVX2, int PPW>
-__global__ __launch_bounds__(256) void vx_gemm_kernel(vx_gemm_args a)
-{
-    constexpr int NS = vx_mcfg<M>::NS;
-    constexpr int R1 = vx_mcfg<M>::R1;
-    constexpr int WPP = QT == 2 ? 1 : 2;   // 16-byte weight loads per lane per block pair
-    constexpr int UNITS = PPW * 8 * NS;    // panel units of a full slice
-    constexpr int UPT = (UNITS + 255) / 256;
-    __shared__ uint4 lds[UPT * 256];
-    __shared__ float lcorr[AVX2 ? PPW * 2 * M : 1];
-
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int grp = blockIdx.x / a.n_splits, split = blockIdx.x % a.n_splits;
-    const int T = grp * 4 + wave;
-    const bool tile_ok = T < a.n_tiles;
-    const int Tc = tile_ok ? T : 0;
-    const int p0 = split * PPW;
-    const int np = min(PPW, a.n_pairs - p0);
-    const int units = np * 8 * NS;
-    const int c = lane & 31, h = lane >> 5;
-    const uint32_t magic = 0x64006400u;
-
-    // 1. the panel slice (issued first so its wait does not cover the weights)
-    const uint4 *psrc = a.panel + (size_t)p0 * 8 * NS;
-    uint4 pv[UPT];
-#pragma unroll
-    for (int j = 0; j < UPT; j++) pv[j] = psrc[min(j * 256 + (int)threadIdx.x, units - 1)];
-    // AVX2 corrections of the slice: at most PPW*2*M <= 512 floats, two per thread
-    float cv0 = 0.0f, cv1 = 0.0f;
-    if (AVX2) {
-        const int cnt = np * 2 * M;
-        const float *cs = a.corr + (size_t)p0 * 2 * M;
-        cv0 = cs[min((int)threadIdx.x, cnt - 1)];
-        cv1 = cs[min((int)threadIdx.x + 256, cnt - 1)];
-    }
-    // 2. the first RING pairs of this wavefront's weights and scales
-    const uint4 *wp = a.wq + ((size_t)Tc * a.n_pairs + p0) * WPP * 64 + lane;
-    const uint32_t *sp = a.wd + ((size_t)Tc * a.n_pairs + p0) * 32 + c;
-    uint4 w[VX_RING][WPP];
-    uint32_t sc[VX_RING];
-#pragma unroll
-    for (int i = 0; i < VX_RING; i++) {
-        const int pi = min(i, np - 1);
-#pragma unroll
-        for (int q = 0; q < WPP; q++) w[i][q] = wp[((size_t)pi * WPP + q) * 64];
-        sc[i] = sp[(size_t)pi * 32];
-    }
-#pragma unroll
-    for (int j = 0; j < UPT; j++) lds[j * 256 + threadIdx.x] = pv[j];
-    if (AVX2) {
-        if ((int)threadIdx.x < PPW * 2 * M) lcorr[threadIdx.x] = cv0;
-        if ((int)threadIdx.x + 256 < PPW * 2 * M) lcorr[threadIdx.x + 256] = cv1;
-    }
-    __syncthreads();
-
-    // idle A lanes read a valid slot; their output rows are never used
-    const int slot = c < 16 ? min(c, M - 1) : M + min(c - 16, M - 1);
-    float acc[16];
-#pragma unroll
-    for (int r = 0; r < 16; r++) acc[r] = 0.0f;
-    const vx_f32x16 zero16 = {};
-#pragma unroll
-    for (int i = 0; i < PPW; i++) {
-        uint4 wv[WPP];
-#pragma unroll
-        for (int q = 0; q < WPP; q++) wv[q] = w[i % VX_RING][q];
-        const uint32_t sv = sc[i % VX_RING];
-        if (i + VX_RING < PPW) {
-            const int pi = min(i + VX_RING, np - 1);
-#pragma unroll
-            for (int q = 0; q < WPP; q++) w[i % VX_RING][q] = wp[((size_t)pi * WPP + q) * 64];
-            sc[i % VX_RING] = sp[(size_t)pi * 32];
-        }
-        if (i < np) {
-#pragma unroll
-            for (int blk = 0; blk < 2; blk++) {
-                const int bl = 2 * i + blk;
-                vx_half8 b0, b1;
-                if (QT == 2) {
-                    b0 = vx_unpack_q4(blk ? wv[0].z : wv[0].x, magic);
-                    b1 = vx_unpack_q4(blk ? wv[0].w : wv[0].y, magic);
-                } else {
-                    b0 = vx_unpack_q8(wv[blk].x, wv[blk].y, magic);
-                    b1 = vx_unpack_q8(wv[blk].z, wv[blk].w, magic);
-                }
-                const vx_half8 a0 = __builtin_bit_cast(vx_half8, lds[((bl * 2 + 0) * 2 + h) * NS + slot]);
-                const vx_half8 a1 = __builtin_bit_cast(vx_half8, lds[((bl * 2 + 1) * 2 + h) * NS + slot]);
-                vx_f32x16 D = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b0, zero16, 0, 0, 0);
-                D = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b1, D, 0, 0, 0);
-                const float d = vx_half_bits_to_float((sv >> (16 * blk)) & 0xFFFFu);
-#pragma unroll
-                for (int r = 0; r < R1; r++) {
-                    float dh = D[r];
-                    if (AVX2) {
-                        const int m = 8 * (r / 4) + 4 * h + (r % 4);
-                        dh = fmaf(-8.0f, m < M ? lcorr[bl * M + m] : 0.0f, dh);
-                    }
-                    acc[r] = fmaf(d, dh, acc[r]);
-                    acc[r + 8] = fmaf(d, D[r + 8], acc[r + 8]);
-                }
-            }
-        }
-    }
-
-    // 3. this slice's contribution, added in fp64
-    const int n = T * 32 + c;
-    if (!tile_ok || n >= a.n_out) return;
-#pragma unroll
-    for (int r = 0; r < R1; r++) {
-        const int m = 8 * (r / 4) + 4 * h + (r % 4);
-        if (m >= M) continue;
-        if (a.gate && fabsf(a.gate[(size_t)m * a.ld_gate + n]) < a.thr) continue;
-        const float v = (acc[r] + acc[r + 8]) * a.rscale[m] * a.scale;
-        __hip_atomic_fetch_add(&a.acc[(size_t)m * a.ld_acc + n], (double)v, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-    }
-}
-
-template <int QT, int M, bool AVX2, int PPW>
-static int vx_launch_ppw(const vxh_qmat *W, vx_gemm_args &a, hipStream_t st, hipEvent_t e0,
-                         hipEvent_t e1)
-{
-    a.n_tiles = W->n_rows / 32;
-    a.n_pairs = W->n_pairs;
-    a.n_splits = (W->n_pairs + PPW - 1) / PPW;
-    const int groups = (a.n_tiles + 3) / 4;
-    if (e0 || e1)   // events recorded by the dispatch itself around the kernel
-        hipExtLaunchKernelGGL(vx_gemm_kernel<QT, M, AVX2, PPW>, dim3(groups * a.n_splits), dim3(256), 0,
-                              st, e0, e1, 0, a);
-    else
-        vx_gemm_kernel<QT, M, AVX2, PPW><<<groups * a.n_splits, 256, 0, st>>>(a);
-    VXH_LAUNCHED();
-    return VXH_OK;
-}
-
-template <int QT, int M, bool AVX2>
-static int vx_launch_gemm(const vxh_qmat *W, vx_gemm_args &a, hipStream_t st, hipEvent_t e0,
-                          hipEvent_t e1)
-{
-    typedef vx_ppw_set<QT, M> S;
-    const long groups = (W->n_rows / 32 + 3) / 4;
-    const int cand[3] = {S::v0, S::v1, S::v2};
-    int pick = S::n - 1;
-    for (int i = 0; i < S::n; i++)
-        if (groups * ((W->n_pairs + cand[i] - 1) / cand[i]) <= VX_WG_TARGET) { pick = i; break; }
-    if (pick == 0) return vx_launch_ppw<QT, M, AVX2, S::v0>(W, a, st, e0, e1);
-    if (pick == 1) return vx_launch_ppw<QT, M, AVX2, S::v1>(W, a, st, e0, e1);
-    return vx_launch_ppw<QT, M, AVX2, S::v2>(W, a, st, e0, e1);
-}
-
-template <int M>
-static int vx_dispatch_m(const vxh_qmat *W, int avx2, vx_gemm_args &a, hipStream_t st, hipEvent_t e0,
-                         hipEvent_t e1)
-{
-    if (W->type == 2) {
-        if (avx2) return vx_launch_gemm<2, M, true>(W, a, st, e0, e1);
-        return vx_launch_gemm<2, M, false>(W, a, st, e0, e1);
-    }
-    if (avx2) return vxh_fail(VXH_ERR_UNSUPPORTED, "AVX2-lane panels apply to Q4_0 only");
-    return vx_launch_gemm<8, M, false>(W, a, st, e0, e1);
-}
-
 extern "C" int vxh_gemm_acc_timed(const vxh_qmat *W, const vxh_panel *X, int M, double *acc,
                                   int ld_acc, int n_out, float scale, const float *gate, int ld_gate,
                                   float thr, int path, vxh_event start, vxh_event stop, vxh_stream s)
@@ -720,6 +421,8 @@ extern "C" int vxh_gemm_acc_timed(const vxh_qmat *W, const vxh_panel *X, int M, 
     a.panel = (const uint4 *)X->data;
     a.corr = X->corr;
     a.rscale = X->rscale;
+    a.rs_ld = 1;
+    a.rs_chunk = 1 << 30;
     a.acc = acc;
     a.ld_acc = ld_acc;
     a.n_out = n_out;
@@ -727,26 +430,7 @@ extern "C" int vxh_gemm_acc_timed(const vxh_qmat *W, const vxh_panel *X, int M, 
     a.gate = gate;
     a.ld_gate = ld_gate;
     a.thr = thr;
-    hipStream_t st = vxh_hs(s);
-    hipEvent_t e0 = (hipEvent_t)start, e1 = (hipEvent_t)stop;
-    switch (M) {
-    case 1: return vx_dispatch_m<1>(W, X->avx2, a, st, e0, e1);
-    case 2: return vx_dispatch_m<2>(W, X->avx2, a, st, e0, e1);
-    case 3: return vx_dispatch_m<3>(W, X->avx2, a, st, e0, e1);
-    case 4: return vx_dispatch_m<4>(W, X->avx2, a, st, e0, e1);
-    case 5: return vx_dispatch_m<5>(W, X->avx2, a, st, e0, e1);
-    case 6: return vx_dispatch_m<6>(W, X->avx2, a, st, e0, e1);
-    case 7: return vx_dispatch_m<7>(W, X->avx2, a, st, e0, e1);
-    case 8: return vx_dispatch_m<8>(W, X->avx2, a, st, e0, e1);
-    case 9: return vx_dispatch_m<9>(W, X->avx2, a, st, e0, e1);
-    case 10: return vx_dispatch_m<10>(W, X->avx2, a, st, e0, e1);
-    case 11: return vx_dispatch_m<11>(W, X->avx2, a, st, e0, e1);
-    case 12: return vx_dispatch_m<12>(W, X->avx2, a, st, e0, e1);
-    case 13: return vx_dispatch_m<13>(W, X->avx2, a, st, e0, e1);
-    case 14: return vx_dispatch_m<14>(W, X->avx2, a, st, e0, e1);
-    case 15: return vx_dispatch_m<15>(W, X->avx2, a, st, e0, e1);
-    default: return vx_dispatch_m<16>(W, X->avx2, a, st, e0, e1);
-    }
+    return vx_dispatch<VX_EPI_NONE>(W, M, X->avx2, a, vxh_hs(s), (hipEvent_t)start, (hipEvent_t)stop);
 }
 
 extern "C" int vxh_gemm_acc(const vxh_qmat *W, const vxh_panel *X, int M, double *acc, int ld_acc,

@@ -14,6 +14,7 @@
 #include "vxh.h"
 
 #define VX_MAX_BATCH 16
+#define VX_N_COUNTERS (64 * 2048)  /* GEMM arrival counters, 64 words apart */
 
 /* ---- errors ----------------------------------------------------------------- */
 void vx_set_error(const char *fmt, ...);
@@ -85,10 +86,15 @@ typedef struct vx_dev {
     int *acc_out;                      /* [2 + 16]                                  */
     /* options */
     vx_model_options opt;
-    /* graphs per batch shape: [M][logit mode] */
-    vxh_graph graphs[VX_MAX_BATCH + 1][3];
-    int graph_pos[VX_MAX_BATCH + 1][3];
-    int *pos_dev;                      /* n_past for graph replays                  */
+    /* fused path: GEMM inputs as x-panels (the attention output, the normed
+     * residual stream, h), per-layer RMSNorm sums of squares
+     * ss[(l * 2 + j) * 16 + m] (j = 0 attention norm, 1 FFN norm; l = L is
+     * the output norm) and the last-arriver counters (zero between uses) */
+    vxh_xpanel xp_att, xp_x, xp_h;
+    double *ss;
+    float *hrows;                      /* [16][F] SwiGLU output of the fused path    */
+    unsigned *cnt;                     /* [VX_N_COUNTERS] GEMM arrival counters      */
+    unsigned *cnt_row;                 /* [16 * 64] attention rows, 64 words apart   */
     /* GEMM profiling (vx_model_set_profiling) */
     int prof_on;
     int prof_n, prof_cap;
