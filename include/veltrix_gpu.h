@@ -48,12 +48,16 @@ typedef struct {
     int attn_cap;              /* attend to at most the first attn_cap positions;
                                   4096 as the reference (src/model.c:304-305), 0 = none */
     float ffn_gate_threshold;  /* up rows with |silu(gate)| below it are zero; 0.01    */
-    int fused;                 /* 1: GEMMs run the follow-up row work in their last
-                                  workgroups (6 launches per layer); 0 (default):
-                                  separate row kernels, faster on MI355X because the
-                                  last-arriver tail costs ~5 dependent memory round
-                                  trips.  AVX2-lane mode always uses separate kernels. */
+    int fused;                 /* VX_FUSED_*: how the row work between GEMMs runs
+                                  (AVX2-lane mode always uses separate kernels)       */
+    int pro_max_rows;          /* VX_FUSED_PROLOGUE: forwards of more rows use the
+                                  separate row kernels                                 */
 } vx_model_options;
+
+#define VX_FUSED_NONE 0        /* separate row kernels (11 launches per layer)          */
+#define VX_FUSED_EPILOGUE 1    /* in the last workgroups of the producing GEMM (6)      */
+#define VX_FUSED_PROLOGUE 2    /* in the consuming GEMM, which builds its own input
+                                  panel slice; RMSNorm applied to the product (7)      */
 
 void vx_model_get_options(const vx_model *model, vx_model_options *opt);
 vx_error vx_model_set_options(vx_model *model, const vx_model_options *opt);

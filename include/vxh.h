@@ -227,6 +227,45 @@ size_t vxh_gemm_workspace_elems(int n_rows, int M);
 int vxh_gemm(const vxh_qmat *W, const vxh_panel *X, int M, const vxh_epilogue *ep,
              vxh_workspace *ws, int path, vxh_stream s);
 
+/* ---- GEMM that builds its own panel ------------------------------------------
+ * vxh_gemm_acc_timed whose workgroups build their K slice of the panel from
+ * the source rows, so that no row kernel runs between two GEMMs of the
+ * forward (src/model.c:514-594).  K = W's columns.
+ *   VXH_PRO_ROWS    a = w .* x                          (w NULL: a = x)
+ *   VXH_PRO_RESID   t = x + (float)src, a = w .* t; t is stored to x_out
+ *                   (the residual add, src/model.c:546, :589)
+ *   VXH_PRO_SWIGLU  a = |silu(g)| < thr ? 0 : silu(g) * u (src/model.c:582-585),
+ *                   g, u the fp32 roundings of the tile-interleaved gate/up
+ *                   sums in src (layout as vxh_swiglu_panel) times
+ *                   1/sqrt(ss_in[m]/ss_K + 1e-5) (ss_in NULL: times 1)
+ * ROWS and RESID add sum x^2 (resp. t^2) of each row into ss[m] when ss is
+ * not NULL, so that the RMSNorm (src/tensor.c:128-142) is applied to the
+ * product instead of the input: W (w .* t) / sqrt(ss/K + 1e-5), by the
+ * product's consumer (vxh_rope_kv_norm, vxh_acc_store_norm, a SWIGLU
+ * prologue).  src is read, not cleared.  The n_clear doubles at clear (an
+ * accumulator that this launch neither reads nor writes) are zeroed.
+ * x, src, w, x_out: 16-byte aligned, ldx and ld_xout multiples of 4, ld_src
+ * even; x_out must not overlap x; acc must not overlap src or clear. */
+enum { VXH_PRO_ROWS = 1, VXH_PRO_RESID = 2, VXH_PRO_SWIGLU = 3 };
+typedef struct {
+    int kind;
+    const float *x; int ldx;        /* ROWS, RESID: input rows [M][ldx]                 */
+    const double *src; int ld_src;  /* RESID: pending GEMM sums; SWIGLU: gate/up sums    */
+    const float *w;                 /* ROWS, RESID: RMSNorm weight [K] or NULL           */
+    float *x_out; int ld_xout;      /* RESID: updated residual rows or NULL              */
+    double *ss;                     /* ROWS, RESID: [M] sums of squares are added, or NULL */
+    const double *ss_in; int ss_K;  /* SWIGLU: deferred RMSNorm of the gate/up product   */
+    float thr;                      /* SWIGLU: gate-skip threshold                       */
+    double *clear; size_t n_clear;  /* zeroed by the launch                              */
+} vxh_pro;
+int vxh_gemm_pro(const vxh_qmat *W, int M, const vxh_pro *p, double *acc, int ld_acc, int n_out,
+                 float scale, vxh_event start, vxh_event stop, vxh_stream s);
+/* y[m][i] = (float)acc[m][i] * 1/sqrt(ss[m]/ss_K + 1e-5) for i < n (the
+ * RMSNorm of a VXH_PRO_ROWS/RESID product, 0 where the rms is below 1e-10 as
+ * src/tensor.c:134-139); acc cleared. */
+int vxh_acc_store_norm(double *acc, int ld_acc, int M, int n, float *y, int ldy, const double *ss,
+                       int ss_K, vxh_stream s);
+
 /* ---- fused forward path ---------------------------------------------------------
  * The same GEMM with the follow-up elementwise work of the reference's
  * forward (src/model.c:514-594) run inside it: the last workgroup to finish
@@ -299,6 +338,13 @@ int vxh_rope_kv(double *qkv, int ld_qkv, int M, int n_past, int n_ctx, int n_hea
                 int n_kv_heads, int head_dim, const float *bq, const float *bk, const float *bv,
                 const float *cos_tab, const float *sin_tab, int n_pos,
                 float *q_out, float *k_cache_layer, float *v_cache_layer, vxh_stream s);
+/* vxh_rope_kv of a VXH_PRO_RESID/ROWS product: q, k, v are the accumulator's
+ * fp32 roundings times 1/sqrt(ss[m]/ss_K + 1e-5) before the biases. */
+int vxh_rope_kv_norm(double *qkv, int ld_qkv, int M, int n_past, int n_ctx, int n_heads,
+                     int n_kv_heads, int head_dim, const float *bq, const float *bk,
+                     const float *bv, const float *cos_tab, const float *sin_tab, int n_pos,
+                     const double *ss, int ss_K, float *q_out, float *k_cache_layer,
+                     float *v_cache_layer, vxh_stream s);
 /* Causal attention of M rows against the layer's KV cache
  * (src/model.c:300-338): row m reads positions [0, min(pos_m + 1, cap)),
  * head h uses kv head h*n_kv/n_heads, softmax with 1/(sum + 1e-10).  Two

@@ -1,0 +1,347 @@
+"""GPU parity of the GEMM that builds its own panel slice (vxh_gemm_pro), of
+its consumers (vxh_acc_store_norm; vxh_rope_kv_norm through the model) and of
+the prologue forward path, against the oracle and the separate-kernel path.
+
+Direct entry-point cases compose the reference's arithmetic on the host:
+the residual add in fp32 (src/model.c:546, :589), RMSNorm (src/tensor.c:
+128-142), SwiGLU with the gate-skip (src/model.c:582-585) via the oracle's
+SiLU, then the oracle's GEMV (src/quantize.c exact Q4_0 path, or Q8_0
+dequantised + f32 GEMV).  Bars: the stored residual rows are bit-exact (one
+fp32 add of the same operands); sums of squares within 1e-6 relative of the
+fp64 sum; products within 1e-4 + 1e-3*|oracle| or closer to the fp64 exact
+value than the oracle is (the `parity` helper); cleared ranges all zero.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import _native as N
+from _native import close, max_violation
+from _oracle_model import OracleModel
+from test_gpu_model import GpuModel, make
+
+pytestmark = pytest.mark.gpu
+O = N.oracle()
+vp = C.c_void_p
+
+PRO_ROWS, PRO_RESID, PRO_SWIGLU = 1, 2, 3
+
+
+class Qmat(C.Structure):
+    _fields_ = [("type", C.c_int), ("n_rows", C.c_int), ("n_cols", C.c_int), ("n_pairs", C.c_int),
+                ("qs", vp), ("d", vp)]
+
+
+class Pro(C.Structure):
+    _fields_ = [("kind", C.c_int), ("x", vp), ("ldx", C.c_int), ("src", vp), ("ld_src", C.c_int),
+                ("w", vp), ("x_out", vp), ("ld_xout", C.c_int), ("ss", vp), ("ss_in", vp),
+                ("ss_K", C.c_int), ("thr", C.c_float), ("clear", vp), ("n_clear", C.c_size_t)]
+
+
+@pytest.fixture(scope="module")
+def P():
+    if not N.product_available():
+        pytest.fail("product library not built")
+    L = N.bind_vxh(N.product())
+    assert L.vxh_init() == 0, L.vxh_last_error()
+    L.vxh_qmat_alloc.argtypes = [C.POINTER(Qmat), C.c_int, C.c_int, C.c_int]
+    L.vxh_qmat_free.argtypes = [C.POINTER(Qmat)]
+    L.vxh_qmat_set_rows.argtypes = [C.POINTER(Qmat), vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, vp]
+    L.vxh_gemm_pro.argtypes = [C.POINTER(Qmat), C.c_int, C.POINTER(Pro), vp, C.c_int, C.c_int, C.c_float,
+                               vp, vp, vp]
+    L.vxh_acc_store_norm.argtypes = [vp, C.c_int, C.c_int, C.c_int, vp, C.c_int, vp, C.c_int, vp]
+    return L
+
+
+def qmat(P, W, typ):
+    rows, nb = W.shape
+    q = Qmat()
+    assert P.vxh_qmat_alloc(C.byref(q), typ, rows, nb * 32) == 0, P.vxh_last_error()
+    assert P.vxh_qmat_set_rows(C.byref(q), W.ctypes.data_as(vp), 0, rows, rows, 0, 0, None) == 0
+    return q
+
+
+def oracle_gemv(W, typ, X):
+    """Reference GEMV of every row of X (fp32), and the fp64 exact product."""
+    rows, nb = W.shape
+    cols = nb * 32
+    out = np.zeros((X.shape[0], rows), np.float32)
+    if typ == 2:
+        for m in range(X.shape[0]):
+            O.or_gemv_q4_0(N._ptr(W), np.ascontiguousarray(X[m]), out[m], rows, cols)
+        vals = N.q4_values(W)
+    else:
+        A = np.zeros(rows * cols, np.float32)
+        O.or_dequantize_row_q8_0(N._ptr(W), A, rows * cols, 1.0)
+        A = A.reshape(rows, cols)
+        for m in range(X.shape[0]):
+            O.or_gemv_f32(out[m], A, np.ascontiguousarray(X[m]), rows, cols)
+        vals = N.q8_values(W)
+    return out, X.astype(np.float64) @ vals.T
+
+
+def rand_w(rng, typ, rows, cols):
+    return N.rand_q4_0(rng, rows, cols) if typ == 2 else N.rand_q8_0(rng, rows, cols)
+
+
+def run_pro(P, q, M, pro, n_out, ld_acc, scale=1.0):
+    acc = N.DevBuf(P, np.zeros(M * ld_acc, np.float64))
+    rc = P.vxh_gemm_pro(C.byref(q), M, C.byref(pro), acc.ptr, ld_acc, n_out, scale, None, None, None)
+    assert rc == 0, P.vxh_last_error()
+    assert P.vxh_stream_sync(None) == 0
+    return acc
+
+
+# (rows, K, M, type): draft- and verify-shaped, a ragged output count, an odd
+# block count (padding block in the last pair), Q8_0
+CASES = [(2560, 2048, 1, 2), (5632 * 2, 2048, 1, 2), (4096, 4096, 9, 2), (100, 96, 5, 2),
+         (300, 2048, 16, 2), (512, 1024, 3, 8), (1000, 4096, 9, 8)]
+
+
+@pytest.mark.parametrize("rows,K,M,typ", CASES)
+def test_pro_resid(P, rows, K, M, typ):
+    """t = x + src stored, sum t^2 added, product of w .* t, clear range zeroed,
+    then the deferred norm through vxh_acc_store_norm."""
+    print(f"gemm_pro resid rows={rows} K={K} M={M} type={typ}", flush=True)
+    rng = np.random.default_rng(rows + K + M + typ)
+    W = rand_w(rng, typ, rows, K)
+    q = qmat(P, W, typ)
+    x = rng.normal(0, 1, (M, K)).astype(np.float32)
+    src = rng.normal(0, 0.5, (M, K))                      # fp64 sums
+    w = rng.normal(1, 0.2, K).astype(np.float32)
+    dx, dsrc, dw = N.DevBuf(P, x), N.DevBuf(P, src), N.DevBuf(P, w)
+    dxo = N.DevBuf(P, nbytes=4 * M * K)
+    dss = N.DevBuf(P, np.zeros(16, np.float64))
+    n_clr = 3 * K + 5
+    dclr = N.DevBuf(P, np.ones(n_clr, np.float64))
+    pro = Pro(kind=PRO_RESID, x=dx.ptr, ldx=K, src=dsrc.ptr, ld_src=K, w=dw.ptr, x_out=dxo.ptr,
+              ld_xout=K, ss=dss.ptr, clear=dclr.ptr, n_clear=n_clr)
+    ld = (rows + 31) // 32 * 32
+    acc = run_pro(P, q, M, pro, rows, ld)
+    t = x + src.astype(np.float32)
+    assert np.array_equal(dxo.get(np.float32, M * K).reshape(M, K), t)
+    ss = dss.get(np.float64, M)
+    ss_ref = (t.astype(np.float64) ** 2).sum(1)
+    assert np.allclose(ss, ss_ref, rtol=1e-6, atol=0), (ss, ss_ref)
+    assert not np.any(dclr.get(np.float64, n_clr))
+    got = acc.get(np.float64, M * ld).reshape(M, ld)[:, :rows]
+    ref, exact = oracle_gemv(W, typ, (w * t).astype(np.float32))
+    ok, nfb = N.parity(got, ref, exact)
+    assert ok, max_violation(got, ref)
+    # deferred RMSNorm: y = acc / rms(t) against the reference's normalise-then-GEMV
+    dy = N.DevBuf(P, nbytes=4 * M * rows)
+    assert P.vxh_acc_store_norm(acc.ptr, ld, M, rows, dy.ptr, rows, dss.ptr, K, None) == 0
+    y = dy.get(np.float32, M * rows).reshape(M, rows)
+    xn = np.zeros((M, K), np.float32)
+    for m in range(M):
+        O.or_rms_norm(xn[m], np.ascontiguousarray(t[m]), w, K)
+    ref, exact = oracle_gemv(W, typ, xn)
+    ok, nfb2 = N.parity(y, ref, exact)
+    assert ok, max_violation(y, ref)
+    assert not np.any(acc.get(np.float64, M * ld)), "acc_store_norm clears the accumulator"
+    print(f"elements on the exact-value fallback: {nfb} (product), {nfb2} (normed)")
+    for b in (dx, dsrc, dw, dxo, dss, dclr, acc, dy):
+        b.free()
+    P.vxh_qmat_free(C.byref(q))
+
+
+@pytest.mark.parametrize("rows,K,M,typ", CASES[2:6])
+@pytest.mark.parametrize("with_w", [False, True])
+def test_pro_rows(P, rows, K, M, typ, with_w):
+    print(f"gemm_pro rows rows={rows} K={K} M={M} type={typ} w={with_w}", flush=True)
+    rng = np.random.default_rng(rows * 3 + K + M + typ + with_w)
+    W = rand_w(rng, typ, rows, K)
+    q = qmat(P, W, typ)
+    ldx = K + 4                                            # a row stride above K
+    x = (rng.normal(0, 1, (M, ldx)) * np.exp(rng.normal(0, 3, (M, 1)))).astype(np.float32)
+    w = rng.normal(1, 0.2, K).astype(np.float32) if with_w else None
+    dx = N.DevBuf(P, x)
+    dw = N.DevBuf(P, w) if with_w else None
+    dss = N.DevBuf(P, np.zeros(16, np.float64))
+    pro = Pro(kind=PRO_ROWS, x=dx.ptr, ldx=ldx, w=dw.ptr if dw else None, ss=dss.ptr)
+    ld = (rows + 31) // 32 * 32
+    acc = run_pro(P, q, M, pro, rows, ld, scale=0.5)
+    got = acc.get(np.float64, M * ld).reshape(M, ld)[:, :rows]
+    a = x[:, :K] * w if with_w else x[:, :K]
+    ref, exact = oracle_gemv(W, typ, a.astype(np.float32))
+    ok, _ = N.parity(got, 0.5 * ref, 0.5 * exact)
+    assert ok, max_violation(got, 0.5 * ref)
+    ss = dss.get(np.float64, M)
+    assert np.allclose(ss, (x[:, :K].astype(np.float64) ** 2).sum(1), rtol=1e-6, atol=0)
+    for b in (dx, dw, dss, acc):
+        if b:
+            b.free()
+    P.vxh_qmat_free(C.byref(q))
+
+
+def swiglu_ref(gate, up, thr):
+    """h = |silu(g)| < thr ? 0 : silu(g) * u with the oracle's SiLU (fp32)."""
+    s = np.ascontiguousarray(gate, np.float32).copy()
+    for m in range(s.shape[0]):
+        O.or_silu(s[m], s.shape[1])
+    return np.where(np.abs(s) < thr, np.float32(0), s * up).astype(np.float32), s
+
+
+@pytest.mark.parametrize("rows,F,M,typ", [(2048, 5632, 1, 2), (4096, 11008, 9, 2), (64, 96, 4, 2),
+                                          (512, 1408, 16, 8)])
+def test_pro_swiglu(P, rows, F, M, typ):
+    """Down projection reading the tile-interleaved gate/up sums directly,
+    with the deferred FFN RMSNorm applied to g and u."""
+    print(f"gemm_pro swiglu rows={rows} F={F} M={M} type={typ}", flush=True)
+    rng = np.random.default_rng(rows + F + M + typ + 7)
+    W = rand_w(rng, typ, rows, F)
+    q = qmat(P, W, typ)
+    thr = 0.01
+    ld_src = (F + 15) // 16 * 32
+    gate = rng.normal(0, 2.0, (M, F))
+    up = rng.normal(0, 2.0, (M, F))
+    ss_in = rng.uniform(100.0, 5000.0, M)
+    K_norm = 2048
+    r = np.array([1.0 / np.sqrt(np.float32(s) / np.float32(K_norm) + np.float32(1e-5))
+                  for s in ss_in], np.float32)
+    g32 = gate.astype(np.float32) * r[:, None]
+    # keep every gate decision at least 1e-4 away from the threshold, where
+    # the last ulp of expf could flip it
+    _, s = swiglu_ref(g32, np.zeros_like(g32), thr)
+    near = np.abs(np.abs(s) - thr) < 1e-4
+    gate[near] = 1.0
+    g32 = gate.astype(np.float32) * r[:, None]
+    u32 = up.astype(np.float32) * r[:, None]
+    src = np.zeros((M, ld_src))
+    for i in range(F):
+        src[:, 32 * (i // 16) + i % 16] = gate[:, i]
+        src[:, 32 * (i // 16) + i % 16 + 16] = up[:, i]
+    dsrc = N.DevBuf(P, src)
+    dssi = N.DevBuf(P, ss_in)
+    pro = Pro(kind=PRO_SWIGLU, src=dsrc.ptr, ld_src=ld_src, ss_in=dssi.ptr, ss_K=K_norm, thr=thr)
+    ld = (rows + 31) // 32 * 32
+    acc = run_pro(P, q, M, pro, rows, ld)
+    got = acc.get(np.float64, M * ld).reshape(M, ld)[:, :rows]
+    h, _ = swiglu_ref(g32, u32, thr)
+    ref, exact = oracle_gemv(W, typ, h)
+    ok, _ = N.parity(got, ref, exact)
+    assert ok, max_violation(got, ref)
+    assert np.array_equal(dsrc.get(np.float64, M * ld_src).reshape(M, ld_src), src), "src is read only"
+    for b in (dsrc, dssi, acc):
+        b.free()
+    P.vxh_qmat_free(C.byref(q))
+
+
+def test_pro_rejects_bad_arguments(P):
+    rng = np.random.default_rng(5)
+    W = N.rand_q4_0(rng, 64, 128)
+    q = qmat(P, W, 2)
+    dx = N.DevBuf(P, np.zeros((2, 128), np.float32))
+    acc = N.DevBuf(P, np.zeros(2 * 64, np.float64))
+    bad = [Pro(kind=9, x=dx.ptr, ldx=128),
+           Pro(kind=PRO_ROWS, x=dx.ptr, ldx=126),                      # ldx below K
+           Pro(kind=PRO_ROWS, x=vp(dx.ptr.value + 4), ldx=128),          # misaligned rows
+           Pro(kind=PRO_RESID, x=dx.ptr, ldx=128),                     # no sums
+           Pro(kind=PRO_RESID, x=dx.ptr, ldx=128, src=acc.ptr, ld_src=128),   # acc overlaps src
+           Pro(kind=PRO_RESID, x=dx.ptr, ldx=128, src=dx.ptr, ld_src=64, x_out=dx.ptr, ld_xout=128),
+           Pro(kind=PRO_SWIGLU, src=dx.ptr, ld_src=100),               # gate/up rows too short
+           Pro(kind=PRO_ROWS, x=dx.ptr, ldx=128, n_clear=4)]           # clear count, no pointer
+    for i, pro in enumerate(bad):
+        rc = P.vxh_gemm_pro(C.byref(q), 2, C.byref(pro), acc.ptr, 64, 64, 1.0, None, None, None)
+        assert rc != 0, i
+    good = Pro(kind=PRO_ROWS, x=dx.ptr, ldx=128)
+    assert P.vxh_gemm_pro(C.byref(q), 17, C.byref(good), acc.ptr, 64, 64, 1.0, None, None, None) != 0
+    for b in (dx, acc):
+        b.free()
+    P.vxh_qmat_free(C.byref(q))
+
+
+# ---------------------------------------------------------------------------
+# model level
+# ---------------------------------------------------------------------------
+def set_mode(g, fused, thr, max_rows=16):
+    opt = N.VxModelOptions()
+    g.P.vx_model_get_options(g.mp, C.byref(opt))
+    opt.fused = fused
+    opt.pro_max_rows = max_rows
+    opt.ffn_gate_threshold = thr
+    assert g.P.vx_model_set_options(g.mp, C.byref(opt)) == 0
+
+
+@pytest.mark.parametrize("shape,thr", [("small", 0.01), ("d2048", 0.0)])
+def test_pro_forward_matches_separate_and_oracle(P, tmp_path, shape, thr):
+    """Verify batches of 9, 16 and 1 rows after a prefix, on the prologue path
+    (fused = 2) and the separate-kernel path (fused = 0).  The d=2048 model
+    runs with the gate-skip threshold at 0: its ~10^5 gate decisions per
+    verify include a few within 1e-7 of 0.01, where any re-association of
+    the sums flips them; the default threshold is covered by the small model."""
+    if shape == "small":
+        dims = dict(L=2, d=128, h=4, kv=2, ff=256, V=300)
+    else:
+        dims = dict(L=2, d=2048, h=16, kv=4, ff=5632, V=1000)
+    print(f"prologue forward {shape} thr {thr}", flush=True)
+    path, raw, (L, d, h, kv, ff, V) = make(tmp_path, 71, **dims)
+    rng = np.random.default_rng(17)
+    prefix = rng.integers(0, V, 20).astype(np.int32)
+    b9 = rng.integers(0, V, 9).astype(np.int32)
+    b16 = rng.integers(0, V, 16).astype(np.int32)
+    got = {}
+    for mode in (2, 0):
+        g = GpuModel(P, path)
+        set_mode(g, mode, thr)
+        try:
+            g.forward(prefix)
+            got[mode] = (g.verify(b9), g.verify(b16), g.verify(b16[:1]))
+            assert g.cache_len == 20 + 9 + 16 + 1
+        finally:
+            g.close()
+    for which, f, s in zip(("M=9", "M=16", "M=1"), got[2], got[0]):
+        assert close(f, s), (which, "prologue vs separate", max_violation(f, s))
+    om = OracleModel(raw, L, d, h, kv, ff, V, n_ctx=4096, gate_thr=thr)
+    toks = np.concatenate([prefix, b9, b16, b16[:1]])
+    ref = np.zeros((len(toks), V), np.float32)
+    O.or_forward_all(om.ptr, toks, len(toks), ref)
+    refs = (ref[20:29], ref[29:45], ref[45:46])
+    for which, r, f in zip(("M=9", "M=16", "M=1"), refs, got[2]):
+        assert close(f, r), (which, "prologue vs oracle", max_violation(f, r))
+        for j in range(len(r)):
+            top = np.sort(r[j])[-2:]
+            if top[1] - top[0] > 1e-4:
+                assert f[j].argmax() == r[j].argmax(), (which, j)
+
+
+def test_pro_decode_steps_and_threshold_switch(P, tmp_path):
+    """Token-by-token forwards on the prologue path, then the same tokens with
+    pro_max_rows = 1 so batches above one row take the separate kernels
+    within one model (both paths leave every accumulator clear)."""
+    print("prologue decode steps d2048", flush=True)
+    path, raw, (L, d, h, kv, ff, V) = make(tmp_path, 72, L=1, d=2048, h=32, kv=4, ff=5632, V=512)
+    toks = np.random.default_rng(18).integers(0, V, 12).astype(np.int32)
+    g = GpuModel(P, path)
+    set_mode(g, 2, 0.0)
+    try:
+        steps = np.stack([g.forward(toks[i:i + 1]) for i in range(len(toks))])
+        P.vx_model_kv_truncate(g.mp, 0)
+        set_mode(g, 2, 0.0, max_rows=1)
+        mixed = np.concatenate([g.forward(toks[:1])[None], g.verify(toks[1:9]), g.verify(toks[9:10]),
+                                g.verify(toks[10:])])
+    finally:
+        g.close()
+    om = OracleModel(raw, L, d, h, kv, ff, V, n_ctx=4096, gate_thr=0.0)
+    ref = np.zeros((len(toks), V), np.float32)
+    O.or_forward_all(om.ptr, toks, len(toks), ref)
+    assert close(steps, ref), max_violation(steps, ref)
+    assert close(mixed, ref), max_violation(mixed, ref)
+
+
+def test_pro_path_repeats_bit_exactly(P, tmp_path):
+    """Sums of squares and products are fp64 additions of fp32 partials, so the
+    same verify run twice gives identical bits."""
+    print("prologue repeat d2048", flush=True)
+    path, raw, dims = make(tmp_path, 73, L=2, d=2048, h=16, kv=4, ff=5632, V=640)
+    toks = np.random.default_rng(19).integers(0, dims[5], 9).astype(np.int32)
+    g = GpuModel(P, path)
+    set_mode(g, 2, 0.01)
+    try:
+        a = g.verify(toks)
+        P.vx_model_kv_truncate(g.mp, 0)
+        b = g.verify(toks)
+        assert np.array_equal(a, b)
+    finally:
+        g.close()

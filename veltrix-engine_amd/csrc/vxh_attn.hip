@@ -11,8 +11,9 @@ __global__ void vx_rope_kv_kernel(double *__restrict__ qkv, int ld_qkv, int M, i
                                   int n_ctx, int n_heads, int n_kv_heads, int hd,
                                   const float *__restrict__ bq, const float *__restrict__ bk,
                                   const float *__restrict__ bv, const float *__restrict__ cs,
-                                  const float *__restrict__ sn, float *__restrict__ q_out,
-                                  float *__restrict__ kc, float *__restrict__ vc)
+                                  const float *__restrict__ sn, const double *__restrict__ ss,
+                                  int ss_K, float *__restrict__ q_out, float *__restrict__ kc,
+                                  float *__restrict__ vc)
 {
     const int qd = n_heads * hd, kvd = n_kv_heads * hd;
     const int half = hd / 2;
@@ -23,6 +24,7 @@ __global__ void vx_rope_kv_kernel(double *__restrict__ qkv, int ld_qkv, int M, i
     int rope_pos = n_past + m;
     int pos = rope_pos < n_ctx ? rope_pos : n_ctx - 1;
     double *row = qkv + (size_t)m * ld_qkv;
+    const float rin = ss ? vx_rms_inv((float)ss[m], ss_K) : 1.0f;   // deferred RMSNorm
     if (r < (qd + kvd) / 2) {
         int e = 2 * r;                       // element index within [q | k]
         bool isq = e < qd;
@@ -30,7 +32,7 @@ __global__ void vx_rope_kv_kernel(double *__restrict__ qkv, int ld_qkv, int M, i
         int i = (el % hd) / 2;               // pair index within the head
         double2 ab = *(const double2 *)(row + e);
         *(double2 *)(row + e) = make_double2(0.0, 0.0);
-        float a = (float)ab.x, b = (float)ab.y;
+        float a = (float)ab.x * rin, b = (float)ab.y * rin;
         const float *bias = isq ? bq : bk;
         if (bias) { a += bias[el]; b += bias[el + 1]; }
         float c = cs[(size_t)rope_pos * half + i], s = sn[(size_t)rope_pos * half + i];
@@ -43,11 +45,29 @@ __global__ void vx_rope_kv_kernel(double *__restrict__ qkv, int ld_qkv, int M, i
         }
     } else {
         int el = r - (qd + kvd) / 2;
-        float v = (float)row[qd + kvd + el];
+        float v = (float)row[qd + kvd + el] * rin;
         row[qd + kvd + el] = 0.0;
         if (bv) v += bv[el];
         vc[(size_t)pos * kvd + el] = v;
     }
+}
+
+extern "C" int vxh_rope_kv_norm(double *qkv, int ld_qkv, int M, int n_past, int n_ctx, int n_heads,
+                                int n_kv_heads, int head_dim, const float *bq, const float *bk,
+                                const float *bv, const float *cos_tab, const float *sin_tab, int n_pos,
+                                const double *ss, int ss_K, float *q_out, float *k_cache_layer,
+                                float *v_cache_layer, vxh_stream s)
+{
+    if (M < 1 || head_dim % 2 || ld_qkv % 2 || n_past < 0 || n_past + M - 1 >= n_pos)
+        return vxh_fail(VXH_ERR_PARAM, "rope_kv: M %d n_past %d n_pos %d", M, n_past, n_pos);
+    if (ss && ss_K < 1) return vxh_fail(VXH_ERR_PARAM, "rope_kv: norm length %d", ss_K);
+    int qd = n_heads * head_dim, kvd = n_kv_heads * head_dim;
+    int n = M * ((qd + kvd) / 2 + kvd);
+    vx_rope_kv_kernel<<<(n + 255) / 256, 256, 0, vxh_hs(s)>>>(
+        qkv, ld_qkv, M, n_past, n_ctx, n_heads, n_kv_heads, head_dim, bq, bk, bv, cos_tab, sin_tab,
+        ss, ss_K, q_out, k_cache_layer, v_cache_layer);
+    VXH_LAUNCHED();
+    return VXH_OK;
 }
 
 extern "C" int vxh_rope_kv(double *qkv, int ld_qkv, int M, int n_past, int n_ctx, int n_heads,
@@ -55,15 +75,8 @@ extern "C" int vxh_rope_kv(double *qkv, int ld_qkv, int M, int n_past, int n_ctx
                            const float *bv, const float *cos_tab, const float *sin_tab, int n_pos,
                            float *q_out, float *k_cache_layer, float *v_cache_layer, vxh_stream s)
 {
-    if (M < 1 || head_dim % 2 || ld_qkv % 2 || n_past < 0 || n_past + M - 1 >= n_pos)
-        return vxh_fail(VXH_ERR_PARAM, "rope_kv: M %d n_past %d n_pos %d", M, n_past, n_pos);
-    int qd = n_heads * head_dim, kvd = n_kv_heads * head_dim;
-    int n = M * ((qd + kvd) / 2 + kvd);
-    vx_rope_kv_kernel<<<(n + 255) / 256, 256, 0, vxh_hs(s)>>>(
-        qkv, ld_qkv, M, n_past, n_ctx, n_heads, n_kv_heads, head_dim, bq, bk, bv, cos_tab, sin_tab,
-        q_out, k_cache_layer, v_cache_layer);
-    VXH_LAUNCHED();
-    return VXH_OK;
+    return vxh_rope_kv_norm(qkv, ld_qkv, M, n_past, n_ctx, n_heads, n_kv_heads, head_dim, bq, bk, bv,
+                            cos_tab, sin_tab, n_pos, nullptr, 0, q_out, k_cache_layer, v_cache_layer, s);
 }
 
 // ---------------------------------------------------------------------------

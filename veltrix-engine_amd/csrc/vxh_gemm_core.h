@@ -1,7 +1,8 @@
 // Shared device code of the skinny-M dequant GEMM: operand unpacking, the
 // MFMA kernel template and its launchers, and the row helpers the panel
-// producers use.  Included by vxh_gemm.hip (plain GEMM) and vxh_fused.hip
-// (GEMM with a fused epilogue).
+// producers use.  Included by vxh_gemm.hip (plain GEMM), vxh_fused.hip
+// (GEMM with a fused epilogue) and vxh_pro_*.hip (GEMM that builds its own
+// panel slice).
 #pragma once
 
 #include <string.h>
@@ -9,14 +10,6 @@
 #include <hip/hip_ext.h>
 
 #include "vxh_internal.h"
-
-// inv = 1/sqrt(ss/K + 1e-5) as in the reference (src/tensor.c:134-139);
-// returns 0 when the rms is below 1e-10 (the reference then writes zeros).
-__device__ __forceinline__ float vx_rms_inv(float ss, int K)
-{
-    float rms = sqrtf(ss / (float)K + 1e-5f);
-    return rms < 1e-10f ? 0.0f : 1.0f / rms;
-}
 
 // Power-of-two row scale: s = 2^-e with amax = f * 2^e, f in [0.5, 1), so
 // that every scaled value has magnitude < 1 (fp16 hi/lo keep 22 bits).
@@ -153,6 +146,30 @@ struct vx_epi_args {
     float *q_out, *kc, *vc;
 };
 
+// Prologue kinds (vxh_pro*.hip): instead of reading a panel that a row kernel
+// wrote, the workgroup builds its own K slice of the panel from the rows the
+// panel is made of.  Every workgroup sharing a K slice builds the same slice;
+// the first tile group also stores the updated residual and adds the row's
+// sum of squares, so the consumer of the product can apply the RMSNorm.
+enum { VX_PRO_PANEL = 0, VX_PRO_ROWS = 1, VX_PRO_RESID = 2, VX_PRO_SWIGLU = 3 };
+
+struct vx_pro_args {
+    const float *x;         // ROWS, RESID: input rows
+    int ldx;
+    const double *src;      // RESID: pending sums added to x; SWIGLU: gate/up accumulator
+    int ld_src;
+    const float *w;         // ROWS, RESID: RMSNorm weight folded into the panel (NULL: none)
+    float *x_out;           // RESID: x + src, stored by the first tile group (NULL: not stored)
+    int ld_xout;
+    double *ss;             // ROWS, RESID: sum of squares of the rows, added by the first tile group
+    const double *ss_in;    // SWIGLU: gate/up sums are scaled by 1/rms(ss_in[m] / ss_K)
+    int ss_K;
+    float thr;              // SWIGLU gate threshold
+    int K;                  // row length
+    double *clr;            // n_clr doubles zeroed by the launch (an accumulator already consumed)
+    long n_clr;
+};
+
 struct vx_gemm_args {
     const uint4 *wq;
     const uint32_t *wd;
@@ -173,18 +190,112 @@ struct vx_gemm_args {
     int ld_gate;
     float thr;
     vx_epi_args e;
+    vx_pro_args p;
 };
 
 // Defined in vxh_fused.hip for EPI != VX_EPI_NONE.
 template <int EPI, int M>
 __device__ void vx_gemm_epilogue(const vx_gemm_args &a, int sg, uint4 *lds, int lds_units);
 
+// ---------------------------------------------------------------------------
+// prologue kinds: building the panel slice in the GEMM
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float vx_wave_max64(float v)
+{
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+__device__ __forceinline__ float vx_wave_sum64(float v)
+{
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// Source values of one 8-column group of a prologue row.
+struct vx_pro_raw {
+    float4 x0, x1, w0, w1;
+    double2 a[4], b[4];
+};
+
+template <int PRO>
+__device__ __forceinline__ void vx_pro_load(const vx_pro_args &p, int m, int e0, vx_pro_raw &r)
+{
+    if constexpr (PRO == VX_PRO_SWIGLU) {
+        // h column i -> tile i/16: gate at physical column 32(i/16) + i%16, up 16 further
+        const double *ar = p.src + (size_t)m * p.ld_src + 32 * (e0 / 16) + e0 % 16;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            r.a[q] = *(const double2 *)(ar + 2 * q);
+            r.b[q] = *(const double2 *)(ar + 16 + 2 * q);
+        }
+    } else {
+        const float *xr = p.x + (size_t)m * p.ldx + e0;
+        r.x0 = *(const float4 *)xr;
+        r.x1 = *(const float4 *)(xr + 4);
+        if (PRO == VX_PRO_RESID) {
+            const double *ar = p.src + (size_t)m * p.ld_src + e0;
+#pragma unroll
+            for (int q = 0; q < 4; q++) r.a[q] = *(const double2 *)(ar + 2 * q);
+        }
+        if (p.w) {
+            r.w0 = *(const float4 *)(p.w + e0);
+            r.w1 = *(const float4 *)(p.w + e0 + 4);
+        }
+    }
+}
+
+// Panel values of a loaded group.  ROWS, RESID: v = w .* t with t = x (+ src),
+// t^2 added to ss, t stored to xo when not NULL.  SWIGLU: v = silu(g) * u,
+// zero where |silu(g)| < thr (src/model.c:582-585), g and u the fp32
+// roundings of the sums times rin.
+template <int PRO>
+__device__ __forceinline__ void vx_pro_values(const vx_pro_args &p, const vx_pro_raw &r, float rin,
+                                              float *xo, float v[8], float &ss)
+{
+    if constexpr (PRO == VX_PRO_SWIGLU) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float g0 = vx_silu((float)r.a[q].x * rin), g1 = vx_silu((float)r.a[q].y * rin);
+            const float u0 = (float)r.b[q].x * rin, u1 = (float)r.b[q].y * rin;
+            v[2 * q] = fabsf(g0) < p.thr ? 0.0f : g0 * u0;
+            v[2 * q + 1] = fabsf(g1) < p.thr ? 0.0f : g1 * u1;
+        }
+    } else {
+        float t[8] = {r.x0.x, r.x0.y, r.x0.z, r.x0.w, r.x1.x, r.x1.y, r.x1.z, r.x1.w};
+        if (PRO == VX_PRO_RESID) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                t[2 * q] = t[2 * q] + (float)r.a[q].x;
+                t[2 * q + 1] = t[2 * q + 1] + (float)r.a[q].y;
+            }
+            if (xo) {
+                *(float4 *)xo = make_float4(t[0], t[1], t[2], t[3]);
+                *(float4 *)(xo + 4) = make_float4(t[4], t[5], t[6], t[7]);
+            }
+        }
+#pragma unroll
+        for (int kk = 0; kk < 8; kk++) ss += t[kk] * t[kk];
+        if (p.w) {
+            const float wv[8] = {r.w0.x, r.w0.y, r.w0.z, r.w0.w, r.w1.x, r.w1.y, r.w1.z, r.w1.w};
+#pragma unroll
+            for (int kk = 0; kk < 8; kk++) v[kk] = wv[kk] * t[kk];
+        } else {
+#pragma unroll
+            for (int kk = 0; kk < 8; kk++) v[kk] = t[kk];
+        }
+    }
+}
+
 #define VX_RING 4
 
 // QT: 2 = Q4_0, 8 = Q8_0.
-template <int QT, int M, bool AVX2, int PPW, int EPI = VX_EPI_NONE>
+template <int QT, int M, bool AVX2, int PPW, int EPI = VX_EPI_NONE, int PRO = VX_PRO_PANEL>
 __global__ __launch_bounds__(256) void vx_gemm_kernel(vx_gemm_args a)
 {
+    static_assert(EPI == VX_EPI_NONE || PRO == VX_PRO_PANEL, "fused epilogues read panels");
+    static_assert(!AVX2 || PRO == VX_PRO_PANEL, "AVX2-lane corrections come with panels");
+    constexpr bool PANEL = PRO == VX_PRO_PANEL;
     constexpr int NS = vx_mcfg<M>::NS;
     constexpr int R1 = vx_mcfg<M>::R1;
     constexpr int WPP = QT == 2 ? 1 : 2;   // 16-byte weight loads per lane per block pair
@@ -192,6 +303,7 @@ __global__ __launch_bounds__(256) void vx_gemm_kernel(vx_gemm_args a)
     constexpr int UPT = (UNITS + 255) / 256;
     __shared__ uint4 lds[UPT * 256];
     __shared__ float lcorr[AVX2 ? PPW * 2 * M : 1];
+    __shared__ float lrs[PANEL ? 1 : M];   // prologue kinds: output scale of each row's slice
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int grp = blockIdx.x / a.n_splits, split = blockIdx.x % a.n_splits;
@@ -204,11 +316,43 @@ __global__ __launch_bounds__(256) void vx_gemm_kernel(vx_gemm_args a)
     const int c = lane & 31, h = lane >> 5;
     const uint32_t magic = 0x64006400u;
 
+    // 0. prologue kinds: this workgroup's share of the accumulator to clear
+    if constexpr (!PANEL) {
+        if (a.p.clr) {
+            const long per = (a.p.n_clr + gridDim.x - 1) / gridDim.x;
+            const long b = (long)blockIdx.x * per, e = min(b + per, a.p.n_clr);
+            for (long i = b + threadIdx.x; i < e; i += 256) a.p.clr[i] = 0.0;
+        }
+    }
+
     // 1. the panel slice (issued first so its wait does not cover the weights)
-    const uint4 *psrc = a.panel + (size_t)p0 * 8 * NS;
-    uint4 pv[UPT];
+    constexpr int PU = PANEL ? UPT : 1;
+    uint4 pv[PU];
+    if constexpr (PANEL) {
+        const uint4 *psrc = a.panel + (size_t)p0 * 8 * NS;
 #pragma unroll
-    for (int j = 0; j < UPT; j++) pv[j] = psrc[min(j * 256 + (int)threadIdx.x, units - 1)];
+        for (int j = 0; j < UPT; j++) pv[j] = psrc[min(j * 256 + (int)threadIdx.x, units - 1)];
+    }
+    // prologue kinds: the slice's source rows; wavefront w builds rows
+    // m = w + 4r, lane l the 8-column groups l + 64j.  Small slices are loaded
+    // here, ahead of the weights; larger ones row by row after them.
+    constexpr int RW = PANEL ? 1 : (M + 3) / 4;
+    constexpr int GL = PANEL ? 1 : (PPW * 8 + 63) / 64;
+    constexpr bool PRELOAD = !PANEL && RW * GL <= 2;
+    const int ng = np * 8, k0 = p0 * 64;
+    vx_pro_raw raw[PRELOAD ? RW : 1][PRELOAD ? GL : 1];
+    if constexpr (PRELOAD) {
+#pragma unroll
+        for (int rr = 0; rr < RW; rr++) {
+            const int m = wave + 4 * rr;
+            if (m >= M) continue;
+#pragma unroll
+            for (int j = 0; j < GL; j++) {
+                const int g = lane + 64 * j;
+                if (g < ng && k0 + 8 * g < a.p.K) vx_pro_load<PRO>(a.p, m, k0 + 8 * g, raw[rr][j]);
+            }
+        }
+    }
     // AVX2 corrections of the slice: at most PPW*2*M <= 512 floats, two per thread
     float cv0 = 0.0f, cv1 = 0.0f;
     if (AVX2) {
@@ -229,8 +373,62 @@ __global__ __launch_bounds__(256) void vx_gemm_kernel(vx_gemm_args a)
         for (int q = 0; q < WPP; q++) w[i][q] = wp[((size_t)pi * WPP + q) * 64];
         sc[i] = sp[(size_t)pi * 32];
     }
+    if constexpr (PANEL) {
 #pragma unroll
-    for (int j = 0; j < UPT; j++) lds[j * 256 + threadIdx.x] = pv[j];
+        for (int j = 0; j < UPT; j++) lds[j * 256 + threadIdx.x] = pv[j];
+    } else {
+        const bool lead = grp == 0;
+#pragma unroll
+        for (int rr = 0; rr < RW; rr++) {
+            const int m = wave + 4 * rr;
+            if (m >= M) continue;
+            const float rin = (PRO == VX_PRO_SWIGLU && a.p.ss_in) ? vx_rms_inv((float)a.p.ss_in[m], a.p.ss_K)
+                                                                  : 1.0f;
+            float v[GL][8];
+            float ss = 0.0f, amax = 0.0f;
+#pragma unroll
+            for (int j = 0; j < GL; j++) {
+                const int g = lane + 64 * j, e0 = k0 + 8 * g;
+#pragma unroll
+                for (int kk = 0; kk < 8; kk++) v[j][kk] = 0.0f;
+                if (g < ng && e0 < a.p.K) {
+                    vx_pro_raw r;
+                    if constexpr (PRELOAD) r = raw[rr][j];
+                    else vx_pro_load<PRO>(a.p, m, e0, r);
+                    float *xo = (lead && a.p.x_out) ? a.p.x_out + (size_t)m * a.p.ld_xout + e0 : nullptr;
+                    vx_pro_values<PRO>(a.p, r, rin, xo, v[j], ss);
+                }
+#pragma unroll
+                for (int kk = 0; kk < 8; kk++) amax = fmaxf(amax, fabsf(v[j][kk]));
+            }
+            amax = vx_wave_max64(amax);
+            float rs;
+            const float sc = vx_row_scale(amax, &rs);
+            if (lane == 0) lrs[m] = rs;
+            if (PRO != VX_PRO_SWIGLU && lead && a.p.ss) {
+                ss = vx_wave_sum64(ss);
+                if (lane == 0)
+                    __hip_atomic_fetch_add(&a.p.ss[m], (double)ss, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+#pragma unroll
+            for (int j = 0; j < GL; j++) {
+                const int g = lane + 64 * j;
+                if (g >= ng) continue;
+                vx_half8 hi, lo;
+#pragma unroll
+                for (int kk = 0; kk < 8; kk++) {
+                    const float xv = v[j][kk] * sc;
+                    const _Float16 t = (_Float16)xv;
+                    hi[kk] = t;
+                    lo[kk] = (_Float16)(xv - (float)t);
+                }
+                const int b = g >> 2, h2 = (g >> 1) & 1, s2 = g & 1;
+                const int base = ((b * 2 + s2) * 2 + h2) * NS;
+                lds[base + m] = __builtin_bit_cast(uint4, hi);
+                lds[base + M + m] = __builtin_bit_cast(uint4, lo);
+            }
+        }
+    }
     if (AVX2) {
         if ((int)threadIdx.x < PPW * 2 * M) lcorr[threadIdx.x] = cv0;
         if ((int)threadIdx.x + 256 < PPW * 2 * M) lcorr[threadIdx.x + 256] = cv1;
@@ -295,7 +493,7 @@ __global__ __launch_bounds__(256) void vx_gemm_kernel(vx_gemm_args a)
             const int m = 8 * (r / 4) + 4 * h + (r % 4);
             if (m >= M) continue;
             if (a.gate && fabsf(a.gate[(size_t)m * a.ld_gate + n]) < a.thr) continue;
-            float osc = a.rscale[m * a.rs_ld + chunk] * a.scale;
+            float osc = (PANEL ? a.rscale[m * a.rs_ld + chunk] : lrs[m]) * a.scale;
             if (a.ss) osc *= vx_rms_inv((float)a.ss[m], a.ss_K);
             const float v = (acc[r] + acc[r + 8]) * osc;
             __hip_atomic_fetch_add(&a.acc[(size_t)m * a.ld_acc + n], (double)v, __ATOMIC_RELAXED,
@@ -339,27 +537,27 @@ __global__ __launch_bounds__(256) void vx_gemm_kernel(vx_gemm_args a)
     }
 }
 
-template <int QT, int M, bool AVX2, int PPW, int EPI>
+template <int QT, int M, bool AVX2, int PPW, int EPI, int PRO>
 static int vx_launch_ppw(const vxh_qmat *W, vx_gemm_args &a, hipStream_t st, hipEvent_t e0,
                          hipEvent_t e1)
 {
     a.n_tiles = W->n_rows / 32;
     a.n_pairs = W->n_pairs;
     a.n_splits = (W->n_pairs + PPW - 1) / PPW;
-    if (a.rs_ld > 1 && a.rs_chunk % PPW)
+    if (PRO == VX_PRO_PANEL && a.rs_ld > 1 && a.rs_chunk % PPW)
         return vxh_fail(VXH_ERR_PARAM, "gemm: K slice of %d pairs crosses a %d-pair scale chunk", PPW,
                         a.rs_chunk);
     const int groups = (a.n_tiles + 3) / 4;
     if (e0 || e1)   // events recorded by the dispatch itself around the kernel
-        hipExtLaunchKernelGGL(vx_gemm_kernel<QT, M, AVX2, PPW, EPI>, dim3(groups * a.n_splits), dim3(256),
-                              0, st, e0, e1, 0, a);
+        hipExtLaunchKernelGGL(vx_gemm_kernel<QT, M, AVX2, PPW, EPI, PRO>, dim3(groups * a.n_splits),
+                              dim3(256), 0, st, e0, e1, 0, a);
     else
-        vx_gemm_kernel<QT, M, AVX2, PPW, EPI><<<groups * a.n_splits, 256, 0, st>>>(a);
+        vx_gemm_kernel<QT, M, AVX2, PPW, EPI, PRO><<<groups * a.n_splits, 256, 0, st>>>(a);
     VXH_LAUNCHED();
     return VXH_OK;
 }
 
-template <int QT, int M, bool AVX2, int EPI>
+template <int QT, int M, bool AVX2, int EPI, int PRO>
 static int vx_launch_gemm(const vxh_qmat *W, vx_gemm_args &a, hipStream_t st, hipEvent_t e0,
                           hipEvent_t e1)
 {
@@ -369,45 +567,45 @@ static int vx_launch_gemm(const vxh_qmat *W, vx_gemm_args &a, hipStream_t st, hi
     int pick = S::n - 1;
     for (int i = 0; i < S::n; i++)
         if (groups * ((W->n_pairs + cand[i] - 1) / cand[i]) <= VX_WG_TARGET) { pick = i; break; }
-    if (pick == 0) return vx_launch_ppw<QT, M, AVX2, S::v0, EPI>(W, a, st, e0, e1);
-    if (pick == 1) return vx_launch_ppw<QT, M, AVX2, S::v1, EPI>(W, a, st, e0, e1);
-    return vx_launch_ppw<QT, M, AVX2, S::v2, EPI>(W, a, st, e0, e1);
+    if (pick == 0) return vx_launch_ppw<QT, M, AVX2, S::v0, EPI, PRO>(W, a, st, e0, e1);
+    if (pick == 1) return vx_launch_ppw<QT, M, AVX2, S::v1, EPI, PRO>(W, a, st, e0, e1);
+    return vx_launch_ppw<QT, M, AVX2, S::v2, EPI, PRO>(W, a, st, e0, e1);
 }
 
-template <int M, int EPI>
+template <int M, int EPI, int PRO>
 static int vx_dispatch_m(const vxh_qmat *W, int avx2, vx_gemm_args &a, hipStream_t st, hipEvent_t e0,
                          hipEvent_t e1)
 {
     if (W->type == 2) {
-        if constexpr (EPI == VX_EPI_NONE)
-            if (avx2) return vx_launch_gemm<2, M, true, EPI>(W, a, st, e0, e1);
-        return vx_launch_gemm<2, M, false, EPI>(W, a, st, e0, e1);
+        if constexpr (EPI == VX_EPI_NONE && PRO == VX_PRO_PANEL)
+            if (avx2) return vx_launch_gemm<2, M, true, EPI, PRO>(W, a, st, e0, e1);
+        return vx_launch_gemm<2, M, false, EPI, PRO>(W, a, st, e0, e1);
     }
     if (avx2) return vxh_fail(VXH_ERR_UNSUPPORTED, "AVX2-lane panels apply to Q4_0 only");
-    return vx_launch_gemm<8, M, false, EPI>(W, a, st, e0, e1);
+    return vx_launch_gemm<8, M, false, EPI, PRO>(W, a, st, e0, e1);
 }
 
 // M = 1..16 to the templates
-template <int EPI>
+template <int EPI, int PRO = VX_PRO_PANEL>
 static int vx_dispatch(const vxh_qmat *W, int M, int avx2, vx_gemm_args &a, hipStream_t st, hipEvent_t e0,
                        hipEvent_t e1)
 {
     switch (M) {
-    case 1: return vx_dispatch_m<1, EPI>(W, avx2, a, st, e0, e1);
-    case 2: return vx_dispatch_m<2, EPI>(W, avx2, a, st, e0, e1);
-    case 3: return vx_dispatch_m<3, EPI>(W, avx2, a, st, e0, e1);
-    case 4: return vx_dispatch_m<4, EPI>(W, avx2, a, st, e0, e1);
-    case 5: return vx_dispatch_m<5, EPI>(W, avx2, a, st, e0, e1);
-    case 6: return vx_dispatch_m<6, EPI>(W, avx2, a, st, e0, e1);
-    case 7: return vx_dispatch_m<7, EPI>(W, avx2, a, st, e0, e1);
-    case 8: return vx_dispatch_m<8, EPI>(W, avx2, a, st, e0, e1);
-    case 9: return vx_dispatch_m<9, EPI>(W, avx2, a, st, e0, e1);
-    case 10: return vx_dispatch_m<10, EPI>(W, avx2, a, st, e0, e1);
-    case 11: return vx_dispatch_m<11, EPI>(W, avx2, a, st, e0, e1);
-    case 12: return vx_dispatch_m<12, EPI>(W, avx2, a, st, e0, e1);
-    case 13: return vx_dispatch_m<13, EPI>(W, avx2, a, st, e0, e1);
-    case 14: return vx_dispatch_m<14, EPI>(W, avx2, a, st, e0, e1);
-    case 15: return vx_dispatch_m<15, EPI>(W, avx2, a, st, e0, e1);
-    default: return vx_dispatch_m<16, EPI>(W, avx2, a, st, e0, e1);
+    case 1: return vx_dispatch_m<1, EPI, PRO>(W, avx2, a, st, e0, e1);
+    case 2: return vx_dispatch_m<2, EPI, PRO>(W, avx2, a, st, e0, e1);
+    case 3: return vx_dispatch_m<3, EPI, PRO>(W, avx2, a, st, e0, e1);
+    case 4: return vx_dispatch_m<4, EPI, PRO>(W, avx2, a, st, e0, e1);
+    case 5: return vx_dispatch_m<5, EPI, PRO>(W, avx2, a, st, e0, e1);
+    case 6: return vx_dispatch_m<6, EPI, PRO>(W, avx2, a, st, e0, e1);
+    case 7: return vx_dispatch_m<7, EPI, PRO>(W, avx2, a, st, e0, e1);
+    case 8: return vx_dispatch_m<8, EPI, PRO>(W, avx2, a, st, e0, e1);
+    case 9: return vx_dispatch_m<9, EPI, PRO>(W, avx2, a, st, e0, e1);
+    case 10: return vx_dispatch_m<10, EPI, PRO>(W, avx2, a, st, e0, e1);
+    case 11: return vx_dispatch_m<11, EPI, PRO>(W, avx2, a, st, e0, e1);
+    case 12: return vx_dispatch_m<12, EPI, PRO>(W, avx2, a, st, e0, e1);
+    case 13: return vx_dispatch_m<13, EPI, PRO>(W, avx2, a, st, e0, e1);
+    case 14: return vx_dispatch_m<14, EPI, PRO>(W, avx2, a, st, e0, e1);
+    case 15: return vx_dispatch_m<15, EPI, PRO>(W, avx2, a, st, e0, e1);
+    default: return vx_dispatch_m<16, EPI, PRO>(W, avx2, a, st, e0, e1);
     }
 }

@@ -42,3 +42,11 @@ __device__ __forceinline__ float vx_half_bits_to_float(uint32_t bits16)
 {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
 }
+
+// inv = 1/sqrt(ss/K + 1e-5) as in the reference (src/tensor.c:134-139);
+// returns 0 when the rms is below 1e-10 (the reference then writes zeros).
+__device__ __forceinline__ float vx_rms_inv(float ss, int K)
+{
+    float rms = sqrtf(ss / (float)K + 1e-5f);
+    return rms < 1e-10f ? 0.0f : 1.0f / rms;
+}

@@ -178,6 +178,7 @@ static void dev_free(vx_dev *d)
     vxh_free(d->acc_qkv); vxh_free(d->acc_x); vxh_free(d->acc_gu); vxh_free(d->acc_lg);
     vxh_free(d->stats); vxh_free(d->acc_out);
     vxh_free(d->ss); vxh_free(d->hrows); vxh_free(d->cnt); vxh_free(d->cnt_row);
+    vxh_free(d->x2); vxh_free(d->acc_y);
     vxh_panel_free(&d->pan_d);
     vxh_panel_free(&d->pan_f);
     vxh_xpanel_free(&d->xp_att);
@@ -208,7 +209,8 @@ static vx_error dev_alloc_common(vx_model *m)
     d->opt.q4_kernel = VX_Q4_EXACT;
     d->opt.attn_cap = 4096;
     d->opt.ffn_gate_threshold = 0.01f;
-    d->opt.fused = 0;   /* separate row kernels: faster than the last-arriver tails on MI355X */
+    d->opt.fused = VX_FUSED_PROLOGUE;
+    d->opt.pro_max_rows = VX_MAX_BATCH;
     if (d->d % 32 || d->F % 32 || d->F <= 0 || d->d <= 0 || d->n_heads * d->hd != d->d ||
         d->hd % 2 || d->n_kv <= 0 || d->n_heads % d->n_kv) {
         vx_set_error("unsupported shape: n_embd %d n_ff %d heads %d/%d head_dim %d", d->d, d->F,
@@ -246,6 +248,8 @@ static vx_error dev_alloc_common(vx_model *m)
     TRY(vxh_malloc((void **)&d->hrows, sizeof(float) * B * (size_t)d->F));
     TRY(vxh_malloc((void **)&d->cnt, sizeof(unsigned) * VX_N_COUNTERS));
     TRY(vxh_malloc((void **)&d->cnt_row, sizeof(unsigned) * B * 64));
+    TRY(vxh_malloc((void **)&d->x2, sizeof(float) * B * d->d));
+    TRY(vxh_malloc((void **)&d->acc_y, sizeof(double) * B * (size_t)d->d));
     TRY(vxh_fill_f32((float *)d->cnt, 0.0f, VX_N_COUNTERS, d->stream));
     TRY(vxh_fill_f32((float *)d->cnt_row, 0.0f, (size_t)B * 64, d->stream));
     return VX_OK;
@@ -635,6 +639,8 @@ vx_error vx_model_set_options(vx_model *m, const vx_model_options *opt)
     if (!d || !opt) return VX_ERR_PARAM;
     if (opt->q4_kernel != VX_Q4_EXACT && opt->q4_kernel != VX_Q4_AVX2_LANES) return VX_ERR_PARAM;
     if (opt->attn_cap < 0) return VX_ERR_PARAM;
+    if (opt->fused < VX_FUSED_NONE || opt->fused > VX_FUSED_PROLOGUE || opt->pro_max_rows < 0)
+        return VX_ERR_PARAM;
     int cap_changed = opt->attn_cap != d->opt.attn_cap;
     d->opt = *opt;
     if (cap_changed && m->k_cache) return dev_alloc_workspace(d, d->n_ctx_alloc, d->opt.attn_cap);
@@ -753,6 +759,7 @@ static vx_error zero_acc(vx_dev *d)
     TRY(vxh_fill_f32((float *)d->acc_x, 0.0f, 2 * (size_t)B * d->d, s));
     TRY(vxh_fill_f32((float *)d->acc_gu, 0.0f, 2 * (size_t)B * d->ld_gu, s));
     TRY(vxh_fill_f32((float *)d->acc_lg, 0.0f, 2 * (size_t)B * d->ld_lg, s));
+    TRY(vxh_fill_f32((float *)d->acc_y, 0.0f, 2 * (size_t)B * d->d, s));
     TRY(vxh_fill_f32((float *)d->cnt, 0.0f, VX_N_COUNTERS, s));
     TRY(vxh_fill_f32((float *)d->cnt_row, 0.0f, (size_t)B * 64, s));
     d->acc_dirty = 0;
@@ -764,7 +771,7 @@ static vx_error zero_acc(vx_dev *d)
  * the exact one (the AVX2-lane tails need the separate row kernels). */
 static int fused_ok(const vx_dev *d)
 {
-    if (!d->opt.fused || d->opt.q4_kernel != VX_Q4_EXACT) return 0;
+    if (d->opt.fused != VX_FUSED_EPILOGUE || d->opt.q4_kernel != VX_Q4_EXACT) return 0;
     if ((d->d + 2 * d->kvd) % 32 || d->hd % 8 || d->F % 32) return 0;
     for (int l = 0; l < d->n_layers; l++)
         if (!d->layers[l].has_o) return 0;
@@ -889,6 +896,125 @@ static vx_error forward_fused(vx_model *m, int M, int n_past, int logits_mode)
     return VX_OK;
 }
 
+/* The prologue path needs the exact Q4_0 kernel (the AVX2-lane corrections
+ * come with the separate panels) and an output projection in every layer;
+ * it runs batches of at most pro_max_rows rows. */
+static int pro_ok(const vx_dev *d, int M)
+{
+    if (d->opt.fused != VX_FUSED_PROLOGUE || M > d->opt.pro_max_rows) return 0;
+    if (d->opt.q4_kernel != VX_Q4_EXACT) return 0;
+    for (int l = 0; l < d->n_layers; l++)
+        if (!d->layers[l].has_o) return 0;
+    return 1;
+}
+
+static vx_error pgemm(vx_dev *d, const vxh_qmat *W, const vxh_pro *p, int M, double *acc, int ld_acc,
+                      int n_out, int cls, int rows_logical)
+{
+    vxh_event e0, e1;
+    vx_error e = prof_slot(d, W, M, n_out, cls, rows_logical, &e0, &e1);
+    if (e != VX_OK) return e;
+    TRY(vxh_gemm_pro(W, M, p, acc, ld_acc, n_out, scale_for(d, W->type), e0, e1, d->stream));
+    return VX_OK;
+}
+
+/* Prologue forward: each GEMM builds its own input panel slice, so a layer
+ * is QKV -> RoPE/KV -> attention (2) -> O -> gate/up -> down, 7 launches.
+ *   QKV     t = x + acc_x (previous down projection) -> x2, panel attn_norm .* t
+ *   RoPE    q|k|v = acc_qkv / rms(t)
+ *   O       panel att -> acc_y
+ *   gate/up t = x2 + acc_y -> x, panel ffn_norm .* t -> acc_gu
+ *   down    panel SwiGLU(acc_gu / rms(t)) -> acc_x
+ * An accumulator is cleared by a later launch that no longer races with its
+ * readers: acc_gu by the next QKV (or the output GEMM), acc_x by O, acc_y by
+ * down; acc_qkv by RoPE. */
+static vx_error forward_pro(vx_model *m, int M, int n_past, int logits_mode)
+{
+    vx_dev *d = vx_dev_of(m);
+    const int dd = d->d, kvd = d->kvd, V = d->V, L = d->n_layers, n_ctx = d->n_ctx_alloc;
+    const int B = VX_MAX_BATCH;
+    vxh_stream s = d->stream;
+    vx_error e;
+#define SS(l, j) (d->ss + ((size_t)(l) * 2 + (j)) * B)
+    if (d->acc_dirty && (e = zero_acc(d)) != VX_OK) return e;
+    d->acc_dirty = 1;
+    TRY(vxh_fill_f32((float *)d->ss, 0.0f, 2 * (size_t)(L + 1) * 2 * B, s));
+    if (d->has_embd) TRY(vxh_qmat_gather_rows(&d->embd, d->tok, M, vx_get_synthetic_weight_scale(), d->x, dd, s));
+    else TRY(vxh_fill_f32(d->x, 0.0f, (size_t)M * dd, s));
+
+    vxh_pro p;
+    for (int l = 0; l < L; l++) {
+        vx_dev_layer *Ld = &d->layers[l];
+        float *kc = m->k_cache + (size_t)l * n_ctx * kvd;
+        float *vc = m->v_cache + (size_t)l * n_ctx * kvd;
+        memset(&p, 0, sizeof(p));
+        p.kind = VXH_PRO_RESID;
+        p.x = d->x; p.ldx = dd;
+        p.src = d->acc_x; p.ld_src = dd;
+        p.w = Ld->attn_norm;
+        p.x_out = d->x2; p.ld_xout = dd;
+        p.ss = SS(l, 0);
+        p.clear = d->acc_gu; p.n_clear = (size_t)M * d->ld_gu;
+        if ((e = pgemm(d, &Ld->wqkv, &p, M, d->acc_qkv, d->ld_qkv, dd + 2 * kvd, VX_PROF_QKV, dd + 2 * kvd)))
+            return e;
+        TRY(vxh_rope_kv_norm(d->acc_qkv, d->ld_qkv, M, n_past, n_ctx, d->n_heads, d->n_kv, d->hd, Ld->bq,
+                             Ld->bk, Ld->bv, d->rope_cos, d->rope_sin, d->n_pos, SS(l, 0), dd, d->q, kc,
+                             vc, s));
+        TRY(vxh_attention(d->q, M, n_past, n_ctx, d->n_heads, d->n_kv, d->hd, d->opt.attn_cap, kc, vc,
+                          d->att, dd, &d->ws, s));
+        memset(&p, 0, sizeof(p));
+        p.kind = VXH_PRO_ROWS;
+        p.x = d->att; p.ldx = dd;
+        p.clear = d->acc_x; p.n_clear = (size_t)M * dd;
+        if ((e = pgemm(d, &Ld->wo, &p, M, d->acc_y, dd, dd, VX_PROF_O, dd))) return e;
+        memset(&p, 0, sizeof(p));
+        p.kind = VXH_PRO_RESID;
+        p.x = d->x2; p.ldx = dd;
+        p.src = d->acc_y; p.ld_src = dd;
+        p.w = Ld->ffn_norm;
+        p.x_out = d->x; p.ld_xout = dd;
+        p.ss = SS(l, 1);
+        if ((e = pgemm(d, &Ld->wgu, &p, M, d->acc_gu, d->ld_gu, d->ld_gu, VX_PROF_GATEUP, 2 * d->F)))
+            return e;
+        memset(&p, 0, sizeof(p));
+        p.kind = VXH_PRO_SWIGLU;
+        p.src = d->acc_gu; p.ld_src = d->ld_gu;
+        p.ss_in = SS(l, 1); p.ss_K = dd;
+        p.thr = d->opt.ffn_gate_threshold;
+        p.clear = d->acc_y; p.n_clear = (size_t)M * dd;
+        if ((e = pgemm(d, &Ld->wd, &p, M, d->acc_x, dd, dd, VX_PROF_DOWN, dd))) return e;
+    }
+    /* x += last down projection (clears acc_x) */
+    TRY(vxh_acc_store(d->acc_x, dd, M, dd, d->x, dd, d->x, dd, s));
+
+    int gu_cleared = 0;
+    if (logits_mode != VX_LOGITS_NONE) {
+        const int rows = logits_mode == VX_LOGITS_LAST ? 1 : M;
+        const int r0 = logits_mode == VX_LOGITS_LAST ? M - 1 : 0;
+        const int orows = d->has_out ? d->out_rows : 0;
+        if (orows < V) TRY(vxh_fill_rows(d->logits, V, rows, orows, V - orows, -1e30f, s));
+        if (d->has_out) {
+            memset(&p, 0, sizeof(p));
+            p.kind = VXH_PRO_ROWS;
+            p.x = d->x + (size_t)r0 * dd; p.ldx = dd;
+            p.w = d->has_out_norm ? d->out_norm : NULL;
+            p.ss = d->has_out_norm ? SS(L, 0) : NULL;
+            p.clear = d->acc_gu; p.n_clear = (size_t)M * d->ld_gu;
+            if ((e = pgemm(d, &d->out, &p, rows, d->acc_lg, d->ld_lg, orows, VX_PROF_OUTPUT, orows)))
+                return e;
+            gu_cleared = 1;
+            if (d->has_out_norm)
+                TRY(vxh_acc_store_norm(d->acc_lg, d->ld_lg, rows, orows, d->logits, V, SS(L, 0), dd, s));
+            else
+                TRY(vxh_acc_store(d->acc_lg, d->ld_lg, rows, orows, d->logits, V, NULL, 0, s));
+        }
+    }
+    if (!gu_cleared && L > 0) TRY(vxh_fill_f32((float *)d->acc_gu, 0.0f, 2 * (size_t)M * d->ld_gu, s));
+#undef SS
+    d->acc_dirty = 0;
+    return VX_OK;
+}
+
 /* One batched forward.  Every GEMM adds into an fp64 accumulator that the
  * next kernel consumes (and clears): q|k|v -> RoPE/KV write, attention
  * output projection and down projection -> the residual + RMSNorm panel of
@@ -897,6 +1023,7 @@ vx_error vx_dev_forward(vx_model *m, int M, int n_past, int logits_mode)
 {
     vx_dev *d = vx_dev_of(m);
     if (M < 1 || M > VX_MAX_BATCH) return VX_ERR_PARAM;
+    if (pro_ok(d, M)) return forward_pro(m, M, n_past, logits_mode);
     if (fused_ok(d)) return forward_fused(m, M, n_past, logits_mode);
     const int dd = d->d, kvd = d->kvd, F = d->F, V = d->V, n_ctx = d->n_ctx_alloc;
     const int avx2 = d->opt.q4_kernel == VX_Q4_AVX2_LANES;

@@ -95,6 +95,11 @@ typedef struct vx_dev {
     float *hrows;                      /* [16][F] SwiGLU output of the fused path    */
     unsigned *cnt;                     /* [VX_N_COUNTERS] GEMM arrival counters      */
     unsigned *cnt_row;                 /* [16 * 64] attention rows, 64 words apart   */
+    /* prologue path: the second residual buffer (the residual alternates
+     * between x and x2 inside a layer) and the attention projection's
+     * accumulator (acc_x holds the down projection's) */
+    float *x2;
+    double *acc_y;
     /* GEMM profiling (vx_model_set_profiling) */
     int prof_on;
     int prof_n, prof_cap;
