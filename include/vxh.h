@@ -238,6 +238,10 @@ int vxh_gemm(const vxh_qmat *W, const vxh_panel *X, int M, const vxh_epilogue *e
  *                   g, u the fp32 roundings of the tile-interleaved gate/up
  *                   sums in src (layout as vxh_swiglu_panel) times
  *                   1/sqrt(ss_in[m]/ss_K + 1e-5) (ss_in NULL: times 1)
+ *   VXH_PRO_ATTN    a = the attention rows combined from the per-chunk
+ *                   partials of vxh_attention_parts_qkv (part, n_chunks,
+ *                   n_heads, n_kv_heads, head_dim as that call; K =
+ *                   n_heads * head_dim; M <= VXH_PRO_ATTN_MAX_ROWS)
  * ROWS and RESID add sum x^2 (resp. t^2) of each row into ss[m] when ss is
  * not NULL, so that the RMSNorm (src/tensor.c:128-142) is applied to the
  * product instead of the input: W (w .* t) / sqrt(ss/K + 1e-5), by the
@@ -246,7 +250,8 @@ int vxh_gemm(const vxh_qmat *W, const vxh_panel *X, int M, const vxh_epilogue *e
  * accumulator that this launch neither reads nor writes) are zeroed.
  * x, src, w, x_out: 16-byte aligned, ldx and ld_xout multiples of 4, ld_src
  * even; x_out must not overlap x; acc must not overlap src or clear. */
-enum { VXH_PRO_ROWS = 1, VXH_PRO_RESID = 2, VXH_PRO_SWIGLU = 3 };
+enum { VXH_PRO_ROWS = 1, VXH_PRO_RESID = 2, VXH_PRO_SWIGLU = 3, VXH_PRO_ATTN = 4 };
+#define VXH_PRO_ATTN_MAX_ROWS 2
 typedef struct {
     int kind;
     const float *x; int ldx;        /* ROWS, RESID: input rows [M][ldx]                 */
@@ -257,6 +262,8 @@ typedef struct {
     const double *ss_in; int ss_K;  /* SWIGLU: deferred RMSNorm of the gate/up product   */
     float thr;                      /* SWIGLU: gate-skip threshold                       */
     double *clear; size_t n_clear;  /* zeroed by the launch                              */
+    const float *part; int n_chunks;/* ATTN: attention partials and their chunk count    */
+    int n_heads, n_kv_heads, head_dim;
 } vxh_pro;
 int vxh_gemm_pro(const vxh_qmat *W, int M, const vxh_pro *p, double *acc, int ld_acc, int n_out,
                  float scale, vxh_event start, vxh_event stop, vxh_stream s);
@@ -354,6 +361,32 @@ int vxh_attention(const float *q, int M, int n_past, int n_ctx, int n_heads, int
                   int head_dim, int cap, const float *k_cache_layer,
                   const float *v_cache_layer, float *out, int ld_out,
                   vxh_workspace *ws, vxh_stream s);
+
+/* vxh_rope_kv_norm + vxh_attention in two launches: the first reads q and
+ * this forward's own k/v rows straight from the q|k|v sums qkv[M][ld_qkv]
+ * (deferred RMSNorm from ss when not NULL, biases, RoPE; bit-for-bit the
+ * values vxh_rope_kv_norm writes) and stores the new k/v rows into the cache;
+ * the second combines the chunks and clears qkv.  A batch whose last row
+ * reaches past n_ctx - 1 must be a single row (the reference's clamp keeps
+ * one row at n_ctx - 1). */
+int vxh_attention_qkv(double *qkv, int ld_qkv, const double *ss, int ss_K, const float *bq,
+                      const float *bk, const float *bv, const float *cos_tab, const float *sin_tab,
+                      int n_pos, int M, int n_past, int n_ctx, int n_heads, int n_kv_heads,
+                      int head_dim, int cap, float *k_cache_layer, float *v_cache_layer, float *out,
+                      int ld_out, vxh_workspace *ws, vxh_stream s);
+
+/* The first launch of vxh_attention_qkv alone: the partials stay in
+ * ws->part for a VXH_PRO_ATTN GEMM, which combines them (and must clear qkv,
+ * see vxh_pro.clear); *n_chunks receives their chunk count.  Layout: query
+ * qi = (head % G) * M + m of kv head g (G = n_heads / n_kv_heads) has chunk c
+ * at part + ((g * n_chunks + c) * G * M + qi) * (head_dim + 4): max, sum, two
+ * unused floats, then the head_dim weighted value sums. */
+int vxh_attention_parts_qkv(double *qkv, int ld_qkv, const double *ss, int ss_K, const float *bq,
+                            const float *bk, const float *bv, const float *cos_tab,
+                            const float *sin_tab, int n_pos, int M, int n_past, int n_ctx,
+                            int n_heads, int n_kv_heads, int head_dim, int cap,
+                            float *k_cache_layer, float *v_cache_layer, vxh_workspace *ws,
+                            int *n_chunks, vxh_stream s);
 
 /* vxh_attention whose second launch also builds the output projection's
  * x-panel p (K = n_heads * head_dim, one scale per row): the last head of

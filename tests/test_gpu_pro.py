@@ -25,7 +25,7 @@ pytestmark = pytest.mark.gpu
 O = N.oracle()
 vp = C.c_void_p
 
-PRO_ROWS, PRO_RESID, PRO_SWIGLU = 1, 2, 3
+PRO_ROWS, PRO_RESID, PRO_SWIGLU, PRO_ATTN = 1, 2, 3, 4
 
 
 class Qmat(C.Structure):
@@ -36,7 +36,9 @@ class Qmat(C.Structure):
 class Pro(C.Structure):
     _fields_ = [("kind", C.c_int), ("x", vp), ("ldx", C.c_int), ("src", vp), ("ld_src", C.c_int),
                 ("w", vp), ("x_out", vp), ("ld_xout", C.c_int), ("ss", vp), ("ss_in", vp),
-                ("ss_K", C.c_int), ("thr", C.c_float), ("clear", vp), ("n_clear", C.c_size_t)]
+                ("ss_K", C.c_int), ("thr", C.c_float), ("clear", vp), ("n_clear", C.c_size_t),
+                ("part", vp), ("n_chunks", C.c_int), ("n_heads", C.c_int), ("n_kv_heads", C.c_int),
+                ("head_dim", C.c_int)]
 
 
 @pytest.fixture(scope="module")
@@ -345,3 +347,171 @@ def test_pro_path_repeats_bit_exactly(P, tmp_path):
         assert np.array_equal(a, b)
     finally:
         g.close()
+
+
+# ---------------------------------------------------------------------------
+# attention reading the q|k|v sums directly
+# ---------------------------------------------------------------------------
+class Workspace(C.Structure):
+    _fields_ = [("acc", vp), ("acc_elems", C.c_size_t), ("part", vp), ("part_floats", C.c_size_t)]
+
+
+def bind_attention(P):
+    i, f = C.c_int, C.c_float
+    P.vxh_workspace_alloc.argtypes = [C.POINTER(Workspace), C.c_size_t, C.c_size_t]
+    P.vxh_workspace_free.argtypes = [C.POINTER(Workspace)]
+    P.vxh_attention_workspace_floats.restype = C.c_size_t
+    P.vxh_attention_workspace_floats.argtypes = [i, i, i, i, i, i]
+    P.vxh_rope_kv_norm.argtypes = [vp, i, i, i, i, i, i, i, vp, vp, vp, vp, vp, i, vp, i, vp, vp, vp, vp]
+    P.vxh_attention.argtypes = [vp, i, i, i, i, i, i, i, vp, vp, vp, i, C.POINTER(Workspace), vp]
+    P.vxh_attention_qkv.argtypes = [vp, i, vp, i, vp, vp, vp, vp, vp, i, i, i, i, i, i, i, i, vp, vp, vp,
+                                    i, C.POINTER(Workspace), vp]
+    P.vxh_attention_parts_qkv.argtypes = [vp, i, vp, i, vp, vp, vp, vp, vp, i, i, i, i, i, i, i, i, vp, vp,
+                                          C.POINTER(Workspace), C.POINTER(C.c_int), vp]
+
+
+@pytest.mark.parametrize("H,KV,hd,M,n_past,n_ctx,cap,bias", [
+    (32, 4, 64, 1, 2200, 4096, 4096, False),     # draft decode step
+    (8, 8, 128, 9, 300, 512, 4096, True),        # verify batch with biases
+    (4, 2, 64, 1, 130, 120, 4096, False),        # past the context: row clamped to n_ctx - 1
+    (8, 2, 32, 5, 70, 256, 40, True),            # attention cap below the positions
+])
+def test_attention_qkv_matches_rope_then_attention(P, H, KV, hd, M, n_past, n_ctx, cap, bias):
+    """vxh_attention_qkv against vxh_rope_kv_norm followed by vxh_attention on
+    the same sums, cache and tables: same attention rows, same new cache rows,
+    the sums cleared by both."""
+    print(f"attention_qkv H={H} KV={KV} hd={hd} M={M} n_past={n_past} n_ctx={n_ctx} cap={cap}", flush=True)
+    bind_attention(P)
+    rng = np.random.default_rng(H * 7 + hd + M + n_past)
+    qd, kvd = H * hd, KV * hd
+    ld = qd + 2 * kvd + 6
+    qkv = np.zeros((M, ld))
+    qkv[:, :qd + 2 * kvd] = rng.normal(0, 3.0, (M, qd + 2 * kvd))
+    ss = rng.uniform(50.0, 500.0, M)
+    n_pos = max(n_past + M, n_ctx) + 8
+    half = hd // 2
+    inv = 1.0 / np.power(10000.0, np.arange(half) * 2.0 / hd)
+    ang = np.arange(n_pos)[:, None] * inv[None, :]
+    cos, sin = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    kc0 = rng.normal(0, 1, (n_ctx, kvd)).astype(np.float32)
+    vc0 = rng.normal(0, 1, (n_ctx, kvd)).astype(np.float32)
+    bq = rng.normal(0, 0.1, qd).astype(np.float32) if bias else None
+    bk = rng.normal(0, 0.1, kvd).astype(np.float32) if bias else None
+    bv = rng.normal(0, 0.1, kvd).astype(np.float32) if bias else None
+    dcs, dsn, dss = N.DevBuf(P, cos), N.DevBuf(P, sin), N.DevBuf(P, ss)
+    db = [N.DevBuf(P, b) if b is not None else None for b in (bq, bk, bv)]
+    bp = [b.ptr if b else None for b in db]
+    ws = Workspace()
+    nf = P.vxh_attention_workspace_floats(M, n_ctx, cap, H, KV, hd)
+    assert P.vxh_workspace_alloc(C.byref(ws), 32, nf) == 0
+    outs = []
+    for fused in (False, True):
+        dqkv = N.DevBuf(P, qkv)
+        dkc, dvc = N.DevBuf(P, kc0), N.DevBuf(P, vc0)
+        dout = N.DevBuf(P, np.zeros((M, qd), np.float32))
+        if fused:
+            rc = P.vxh_attention_qkv(dqkv.ptr, ld, dss.ptr, 2048, bp[0], bp[1], bp[2], dcs.ptr, dsn.ptr, n_pos,
+                                     M, n_past, n_ctx, H, KV, hd, cap, dkc.ptr, dvc.ptr, dout.ptr, qd,
+                                     C.byref(ws), None)
+            assert rc == 0, P.vxh_last_error()
+        else:
+            dq = N.DevBuf(P, nbytes=4 * M * qd)
+            rc = P.vxh_rope_kv_norm(dqkv.ptr, ld, M, n_past, n_ctx, H, KV, hd, bp[0], bp[1], bp[2], dcs.ptr,
+                                    dsn.ptr, n_pos, dss.ptr, 2048, dq.ptr, dkc.ptr, dvc.ptr, None)
+            assert rc == 0, P.vxh_last_error()
+            rc = P.vxh_attention(dq.ptr, M, n_past, n_ctx, H, KV, hd, cap, dkc.ptr, dvc.ptr, dout.ptr, qd,
+                                 C.byref(ws), None)
+            assert rc == 0, P.vxh_last_error()
+            dq.free()
+        assert P.vxh_stream_sync(None) == 0
+        outs.append((dout.get(np.float32, M * qd).reshape(M, qd), dkc.get(np.float32, n_ctx * kvd),
+                     dvc.get(np.float32, n_ctx * kvd)))
+        assert not np.any(dqkv.get(np.float64, M * ld)), "q|k|v sums cleared"
+        for b in (dqkv, dkc, dvc, dout):
+            b.free()
+    (oa, ka, va), (ob, kb, vb) = outs
+    assert close(ob, oa, atol=1e-6, rtol=1e-5), max_violation(ob, oa, 1e-6, 1e-5)
+    assert close(kb, ka, atol=1e-6, rtol=1e-5) and close(vb, va, atol=1e-6, rtol=1e-5)
+    rows = sorted({min(n_past + m, n_ctx - 1) for m in range(M)})
+    assert not np.array_equal(ka.reshape(n_ctx, kvd)[rows], kc0[rows]), "new rows were written"
+    P.vxh_workspace_free(C.byref(ws))
+    for b in [dcs, dsn, dss] + [b for b in db if b]:
+        b.free()
+
+
+def test_attention_qkv_rejects_clamped_batches(P):
+    bind_attention(P)
+    ws = Workspace()
+    assert P.vxh_workspace_alloc(C.byref(ws), 32, 1 << 16) == 0
+    d = N.DevBuf(P, nbytes=1 << 16)
+    rc = P.vxh_attention_qkv(d.ptr, 64, None, 0, None, None, None, d.ptr, d.ptr, 200, 3, 99, 100, 2, 1, 16,
+                             0, d.ptr, d.ptr, d.ptr, 32, C.byref(ws), None)
+    assert rc != 0
+    P.vxh_workspace_free(C.byref(ws))
+    d.free()
+
+
+@pytest.mark.parametrize("H,KV,hd,M,typ", [(32, 4, 64, 1, 2), (8, 8, 128, 2, 2), (16, 2, 64, 2, 8),
+                                           (4, 4, 32, 1, 2)])
+def test_pro_attn_combines_partials(P, H, KV, hd, M, typ):
+    """Output projection combining the attention partials itself (the draft's
+    one-row step) against vxh_attention_qkv followed by a ROWS product of the
+    combined rows; the q|k|v sums are cleared by the projection launch."""
+    print(f"gemm_pro attn H={H} KV={KV} hd={hd} M={M} type={typ}", flush=True)
+    bind_attention(P)
+    rng = np.random.default_rng(H + hd * 3 + M + typ)
+    qd, kvd = H * hd, KV * hd
+    ld = qd + 2 * kvd
+    n_past, n_ctx = 700, 1024
+    qkv = rng.normal(0, 3.0, (M, ld))
+    ss = rng.uniform(50.0, 500.0, M)
+    n_pos = n_ctx + 8
+    half = hd // 2
+    inv = 1.0 / np.power(10000.0, np.arange(half) * 2.0 / hd)
+    ang = np.arange(n_pos)[:, None] * inv[None, :]
+    cos, sin = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    kc0 = rng.normal(0, 1, (n_ctx, kvd)).astype(np.float32)
+    vc0 = rng.normal(0, 1, (n_ctx, kvd)).astype(np.float32)
+    W = rand_w(rng, typ, 640, qd)
+    q = qmat(P, W, typ)
+    dcs, dsn, dss = N.DevBuf(P, cos), N.DevBuf(P, sin), N.DevBuf(P, ss)
+    ws = Workspace()
+    assert P.vxh_workspace_alloc(C.byref(ws), 32, P.vxh_attention_workspace_floats(M, n_ctx, 4096, H, KV, hd)) == 0
+    res = []
+    for combined_in_gemm in (False, True):
+        dqkv, dkc, dvc = N.DevBuf(P, qkv), N.DevBuf(P, kc0), N.DevBuf(P, vc0)
+        datt = N.DevBuf(P, np.zeros((M, qd), np.float32))
+        acc = N.DevBuf(P, np.zeros(M * 640))
+        if combined_in_gemm:
+            nch = C.c_int()
+            rc = P.vxh_attention_parts_qkv(dqkv.ptr, ld, dss.ptr, 4096, None, None, None, dcs.ptr, dsn.ptr,
+                                           n_pos, M, n_past, n_ctx, H, KV, hd, 4096, dkc.ptr, dvc.ptr,
+                                           C.byref(ws), C.byref(nch), None)
+            assert rc == 0, P.vxh_last_error()
+            assert nch.value == (n_past + M + 31) // 32
+            pro = Pro(kind=PRO_ATTN, part=ws.part, n_chunks=nch.value, n_heads=H, n_kv_heads=KV, head_dim=hd,
+                      clear=dqkv.ptr, n_clear=M * ld)
+        else:
+            rc = P.vxh_attention_qkv(dqkv.ptr, ld, dss.ptr, 4096, None, None, None, dcs.ptr, dsn.ptr, n_pos, M,
+                                     n_past, n_ctx, H, KV, hd, 4096, dkc.ptr, dvc.ptr, datt.ptr, qd,
+                                     C.byref(ws), None)
+            assert rc == 0, P.vxh_last_error()
+            pro = Pro(kind=PRO_ROWS, x=datt.ptr, ldx=qd)
+        rc = P.vxh_gemm_pro(C.byref(q), M, C.byref(pro), acc.ptr, 640, 640, 1.0, None, None, None)
+        assert rc == 0, P.vxh_last_error()
+        assert P.vxh_stream_sync(None) == 0
+        assert not np.any(dqkv.get(np.float64, M * ld)), "q|k|v sums cleared"
+        res.append((acc.get(np.float64, M * 640).reshape(M, 640), dkc.get(np.float32, n_ctx * kvd)))
+        for b in (dqkv, dkc, dvc, datt, acc):
+            b.free()
+    (a0, k0), (a1, k1) = res
+    assert np.array_equal(k0, k1), "same new cache rows"
+    assert close(a1, a0, atol=1e-5, rtol=1e-4), max_violation(a1, a0, 1e-5, 1e-4)
+    bad = Pro(kind=PRO_ATTN, part=ws.part, n_chunks=4, n_heads=H, n_kv_heads=KV, head_dim=hd)
+    acc = N.DevBuf(P, np.zeros(3 * 640))
+    assert P.vxh_gemm_pro(C.byref(q), 3, C.byref(bad), acc.ptr, 640, 640, 1.0, None, None, None) != 0
+    acc.free()
+    P.vxh_workspace_free(C.byref(ws))
+    P.vxh_qmat_free(C.byref(q))
+    for b in (dcs, dsn, dss):
+        b.free()

@@ -1,5 +1,7 @@
 // Attention block of the verify step: RoPE + KV-cache write, and causal
 // attention of M query rows against the resident fp32 KV cache.
+#include <string.h>
+
 #include "vxh_internal.h"
 
 // ---------------------------------------------------------------------------
@@ -95,15 +97,53 @@ extern "C" int vxh_rope_kv(double *qkv, int ld_qkv, int M, int n_past, int n_ctx
 #define ATT_MAX_HD 128
 #define PART_STRIDE(hd) ((hd) + 4)
 
+// QKV variant: q and this forward's own k/v rows come straight from the fp64
+// q|k|v GEMM sums (deferred RMSNorm, biases and RoPE applied on the way, as
+// vx_rope_kv_kernel does), and the workgroups of query group 0 store the new
+// k/v rows into the cache.
+struct vx_qkv_args {
+    const double *qkv;
+    int ld;
+    const double *ss;       // NULL: no deferred RMSNorm
+    int ss_K;
+    const float *bq, *bk, *bv;
+    const float *cs, *sn;   // RoPE tables [n_pos][hd/2]
+};
+
+// Elements col..col+3 of row m of the sums, times rin plus bias[el..el+3],
+// rotated as the pairs i, i+1 of a head at rope position rp (rot = false: v).
+__device__ __forceinline__ float4 vx_qkv4(const vx_qkv_args &a, int m, int col, int el, int i, int rp,
+                                          int half, const float *bias, bool rot)
+{
+    const float rin = a.ss ? vx_rms_inv((float)a.ss[m], a.ss_K) : 1.0f;
+    const double *r = a.qkv + (size_t)m * a.ld + col;
+    const double2 p0 = *(const double2 *)r, p1 = *(const double2 *)(r + 2);
+    float x0 = (float)p0.x * rin, x1 = (float)p0.y * rin, x2 = (float)p1.x * rin, x3 = (float)p1.y * rin;
+    if (bias) {
+        x0 += bias[el];
+        x1 += bias[el + 1];
+        x2 += bias[el + 2];
+        x3 += bias[el + 3];
+    }
+    if (!rot) return make_float4(x0, x1, x2, x3);
+    const float c0 = a.cs[(size_t)rp * half + i], s0 = a.sn[(size_t)rp * half + i];
+    const float c1 = a.cs[(size_t)rp * half + i + 1], s1 = a.sn[(size_t)rp * half + i + 1];
+    return make_float4(x0 * c0 - x1 * s0, x0 * s0 + x1 * c0, x2 * c1 - x3 * s1, x2 * s1 + x3 * c1);
+}
+
+template <bool QKV>
 __global__ __launch_bounds__(ATT_THREADS) void vx_attention_kernel(
     const float *__restrict__ q, int M, int n_past, int n_ctx, int n_heads, int n_kv, int hd,
-    int cap, const float *__restrict__ kc, const float *__restrict__ vc, int n_chunks, int qpg,
-    int n_qg, float *__restrict__ part)
+    int cap, float *__restrict__ kc, float *__restrict__ vc, int n_chunks, int n_chunks_w, int qpg,
+    int n_qg, float *__restrict__ part, vx_qkv_args qa)
 {
+    // chunks [n_chunks, n_chunks_w) (QKV, attention cap below the new rows)
+    // only store the new k/v rows
     extern __shared__ float4 sm4[];
-    const int per_g = n_chunks * n_qg;
+    const int per_g = n_chunks_w * n_qg;
     const int g = blockIdx.x / per_g;
     const int ch = (blockIdx.x % per_g) / n_qg, qg = blockIdx.x % n_qg;
+    if (ch >= n_chunks && qg != 0) return;
     const int G = n_heads / n_kv;
     const int QM = G * M;
     const int q0 = qg * qpg;
@@ -121,19 +161,44 @@ __global__ __launch_bounds__(ATT_THREADS) void vx_attention_kernel(
     // cache end read as zeros (their scores are masked below)
     constexpr int KV4 = ACH * ATT_MAX_HD / 4 / ATT_THREADS;
     float4 kr[KV4], vr[KV4];
+    const int qd = n_heads * hd, half = hd / 2;
 #pragma unroll
     for (int j = 0; j < KV4; j++) {
         const int i = j * ATT_THREADS + threadIdx.x;
         const int t = i / hd4, d4 = i % hd4;
-        const bool ok = t < ACH && t0 + t < n_ctx;
-        const size_t off = (size_t)(t0 + t) * kvd + (size_t)g * hd + 4 * d4;
-        kr[j] = ok ? *(const float4 *)(kc + off) : make_float4(0.f, 0.f, 0.f, 0.f);
-        vr[j] = ok ? *(const float4 *)(vc + off) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const int pos = t0 + t;
+        const bool ok = t < ACH && pos < n_ctx;
+        const size_t off = (size_t)pos * kvd + (size_t)g * hd + 4 * d4;
+        // QKV: the row of this forward whose k/v land at pos (rows sit at
+        // min(n_past + m, n_ctx - 1); only a one-row forward is clamped)
+        int mn = -1;
+        if (QKV && ok) {
+            mn = pos - n_past;
+            if (mn >= M) mn = -1;
+            if (mn < 0 && n_past >= n_ctx && pos == n_ctx - 1) mn = 0;
+        }
+        if (mn >= 0) {
+            const int el = g * hd + 4 * d4;
+            kr[j] = vx_qkv4(qa, mn, qd + el, el, 2 * d4, n_past + mn, half, qa.bk, true);
+            vr[j] = vx_qkv4(qa, mn, qd + kvd + el, el, 0, 0, half, qa.bv, false);
+            if (qg == 0) {
+                *(float4 *)(kc + off) = kr[j];
+                *(float4 *)(vc + off) = vr[j];
+            }
+        } else {
+            kr[j] = ok ? *(const float4 *)(kc + off) : make_float4(0.f, 0.f, 0.f, 0.f);
+            vr[j] = ok ? *(const float4 *)(vc + off) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
     }
+    if (ch >= n_chunks) return;
     for (int i = threadIdx.x; i < nq * hd4; i += ATT_THREADS) {
         const int ql = i / hd4, d4 = i % hd4;
         const int qi = q0 + ql, hl = qi / M, m = qi % M;
-        sq4[ql * hd4 + d4] = *(const float4 *)(q + (size_t)m * n_heads * hd + (size_t)(g * G + hl) * hd + 4 * d4);
+        const int el = (g * G + hl) * hd + 4 * d4;
+        if constexpr (QKV)
+            sq4[ql * hd4 + d4] = vx_qkv4(qa, m, el, el, 2 * d4, n_past + m, half, qa.bq, true);
+        else
+            sq4[ql * hd4 + d4] = *(const float4 *)(q + (size_t)m * qd + el);
     }
 #pragma unroll
     for (int j = 0; j < KV4; j++) {
@@ -257,9 +322,16 @@ __device__ void vx_att_row_panel(const float *att, int d, int M, int m, uint4 *p
 template <bool XP>
 __global__ __launch_bounds__(CMB_THREADS) void vx_attention_combine_kernel(
     const float *__restrict__ part, int M, int n_heads, int n_kv, int hd, int n_chunks,
-    float *__restrict__ out, int ld_out, unsigned *cnt, uint4 *pan, float *rs, int rs_ld)
+    float *__restrict__ out, int ld_out, unsigned *cnt, uint4 *pan, float *rs, int rs_ld,
+    double *clr, long n_clr)
 {
     __shared__ float4 s_acc[CMB_THREADS];
+    if (clr) {
+        // the q|k|v sums the first launch consumed
+        const long per = (n_clr + gridDim.x - 1) / gridDim.x;
+        const long b = (long)blockIdx.x * per, e = min(b + per, n_clr);
+        for (long i = b + threadIdx.x; i < e; i += CMB_THREADS) clr[i] = 0.0;
+    }
     __shared__ float s_m[CMB_THREADS], s_l[CMB_THREADS];
     const int m = blockIdx.x % M, head = blockIdx.x / M;
     const int G = n_heads / n_kv, QM = G * M;
@@ -372,10 +444,13 @@ extern "C" size_t vxh_attention_workspace_floats(int M, int n_ctx, int cap, int 
     return (size_t)n_kv_heads * n_chunks * (n_heads / n_kv_heads) * M * PART_STRIDE(head_dim);
 }
 
-static int vx_attention_run(const float *q, int M, int n_past, int n_ctx, int n_heads,
-                            int n_kv_heads, int head_dim, int cap, const float *kc, const float *vc,
-                            float *out, int ld_out, vxh_workspace *ws, unsigned *row_counters,
-                            vxh_xpanel *xp, vxh_stream s)
+// parts_only: the first launch alone; the partials stay in ws->part for a
+// consumer that combines them itself (*n_chunks_out chunks per query).
+static int vx_attention_run(const float *q, const vx_qkv_args *qa, long n_clr, int M, int n_past,
+                            int n_ctx, int n_heads, int n_kv_heads, int head_dim, int cap, float *kc,
+                            float *vc, float *out, int ld_out, vxh_workspace *ws,
+                            unsigned *row_counters, vxh_xpanel *xp, int parts_only, int *n_chunks_out,
+                            vxh_stream s)
 {
     if (M < 1 || n_kv_heads < 1 || n_heads % n_kv_heads)
         return vxh_fail(VXH_ERR_PARAM, "attention: M %d heads %d kv %d", M, n_heads, n_kv_heads);
@@ -386,6 +461,8 @@ static int vx_attention_run(const float *q, int M, int n_past, int n_ctx, int n_
     int ctx = last + 1;
     if (cap > 0 && ctx > cap) ctx = cap;
     int n_chunks = (ctx + ACH - 1) / ACH;
+    int n_chunks_w = n_chunks;      // QKV: chunks holding new rows, cap or not
+    if (qa && (last + 1 + ACH - 1) / ACH > n_chunks_w) n_chunks_w = (last + 1 + ACH - 1) / ACH;
     int G = n_heads / n_kv_heads;
     int QM = G * M;
     int qpg = vx_attn_qpg(head_dim);
@@ -395,18 +472,28 @@ static int vx_attention_run(const float *q, int M, int n_past, int n_ctx, int n_
     if (need > ws->part_floats)
         return vxh_fail(VXH_ERR_PARAM, "attention workspace too small (%zu floats needed)", need);
     size_t lds = vx_attn_lds(qpg, head_dim);
-    vx_attention_kernel<<<n_kv_heads * n_chunks * n_qg, ATT_THREADS, lds, vxh_hs(s)>>>(
-        q, M, n_past, n_ctx, n_heads, n_kv_heads, head_dim, cap, kc, vc, n_chunks, qpg, n_qg,
-        ws->part);
+    vx_qkv_args none;
+    memset(&none, 0, sizeof(none));
+    if (qa)
+        vx_attention_kernel<true><<<n_kv_heads * n_chunks_w * n_qg, ATT_THREADS, lds, vxh_hs(s)>>>(
+            nullptr, M, n_past, n_ctx, n_heads, n_kv_heads, head_dim, cap, kc, vc, n_chunks, n_chunks_w,
+            qpg, n_qg, ws->part, *qa);
+    else
+        vx_attention_kernel<false><<<n_kv_heads * n_chunks * n_qg, ATT_THREADS, lds, vxh_hs(s)>>>(
+            q, M, n_past, n_ctx, n_heads, n_kv_heads, head_dim, cap, kc, vc, n_chunks, n_chunks, qpg,
+            n_qg, ws->part, none);
     VXH_LAUNCHED();
+    if (n_chunks_out) *n_chunks_out = n_chunks;
+    if (parts_only) return VXH_OK;
+    double *clr = qa ? (double *)qa->qkv : nullptr;
     if (xp)
         vx_attention_combine_kernel<true><<<M * n_heads, CMB_THREADS, 0, vxh_hs(s)>>>(
             ws->part, M, n_heads, n_kv_heads, head_dim, n_chunks, out, ld_out, row_counters,
-            (uint4 *)xp->data, xp->rs, xp->rs_ld);
+            (uint4 *)xp->data, xp->rs, xp->rs_ld, clr, n_clr);
     else
         vx_attention_combine_kernel<false><<<M * n_heads, CMB_THREADS, 0, vxh_hs(s)>>>(
             ws->part, M, n_heads, n_kv_heads, head_dim, n_chunks, out, ld_out, nullptr, nullptr,
-            nullptr, 0);
+            nullptr, 0, clr, n_clr);
     VXH_LAUNCHED();
     return VXH_OK;
 }
@@ -416,8 +503,59 @@ extern "C" int vxh_attention(const float *q, int M, int n_past, int n_ctx, int n
                              const float *vc, float *out, int ld_out, vxh_workspace *ws,
                              vxh_stream s)
 {
-    return vx_attention_run(q, M, n_past, n_ctx, n_heads, n_kv_heads, head_dim, cap, kc, vc, out,
-                            ld_out, ws, nullptr, nullptr, s);
+    return vx_attention_run(q, nullptr, 0, M, n_past, n_ctx, n_heads, n_kv_heads, head_dim, cap,
+                            (float *)kc, (float *)vc, out, ld_out, ws, nullptr, nullptr, 0, nullptr, s);
+}
+
+static int vx_attention_qkv(double *qkv, int ld_qkv, const double *ss, int ss_K, const float *bq,
+                            const float *bk, const float *bv, const float *cos_tab, const float *sin_tab,
+                            int n_pos, int M, int n_past, int n_ctx, int n_heads, int n_kv_heads,
+                            int head_dim, int cap, float *kc, float *vc, float *out, int ld_out,
+                            vxh_workspace *ws, int *n_chunks_out, vxh_stream s)
+{
+    if (!qkv || ((uintptr_t)qkv & 15) || ld_qkv % 2 || M < 1 || n_kv_heads < 1 ||
+        ld_qkv < (n_heads + 2 * n_kv_heads) * head_dim)
+        return vxh_fail(VXH_ERR_PARAM, "attention_qkv: ld %d for %d+2x%d heads of %d", ld_qkv, n_heads,
+                        n_kv_heads, head_dim);
+    if (n_past < 0 || n_past + M - 1 >= n_pos || (n_past + M - 1 >= n_ctx && M > 1))
+        return vxh_fail(VXH_ERR_PARAM, "attention_qkv: M %d n_past %d n_ctx %d n_pos %d", M, n_past,
+                        n_ctx, n_pos);
+    if (ss && ss_K < 1) return vxh_fail(VXH_ERR_PARAM, "attention_qkv: norm length %d", ss_K);
+    vx_qkv_args qa;
+    qa.qkv = qkv;
+    qa.ld = ld_qkv;
+    qa.ss = ss;
+    qa.ss_K = ss_K;
+    qa.bq = bq;
+    qa.bk = bk;
+    qa.bv = bv;
+    qa.cs = cos_tab;
+    qa.sn = sin_tab;
+    return vx_attention_run(nullptr, &qa, (long)M * ld_qkv, M, n_past, n_ctx, n_heads, n_kv_heads,
+                            head_dim, cap, kc, vc, out, ld_out, ws, nullptr, nullptr, n_chunks_out != nullptr,
+                            n_chunks_out, s);
+}
+
+extern "C" int vxh_attention_qkv(double *qkv, int ld_qkv, const double *ss, int ss_K, const float *bq,
+                                 const float *bk, const float *bv, const float *cos_tab,
+                                 const float *sin_tab, int n_pos, int M, int n_past, int n_ctx,
+                                 int n_heads, int n_kv_heads, int head_dim, int cap, float *kc,
+                                 float *vc, float *out, int ld_out, vxh_workspace *ws, vxh_stream s)
+{
+    return vx_attention_qkv(qkv, ld_qkv, ss, ss_K, bq, bk, bv, cos_tab, sin_tab, n_pos, M, n_past, n_ctx,
+                            n_heads, n_kv_heads, head_dim, cap, kc, vc, out, ld_out, ws, nullptr, s);
+}
+
+extern "C" int vxh_attention_parts_qkv(double *qkv, int ld_qkv, const double *ss, int ss_K,
+                                       const float *bq, const float *bk, const float *bv,
+                                       const float *cos_tab, const float *sin_tab, int n_pos, int M,
+                                       int n_past, int n_ctx, int n_heads, int n_kv_heads, int head_dim,
+                                       int cap, float *kc, float *vc, vxh_workspace *ws, int *n_chunks,
+                                       vxh_stream s)
+{
+    if (!n_chunks) return vxh_fail(VXH_ERR_PARAM, "attention_parts_qkv: n_chunks output missing");
+    return vx_attention_qkv(qkv, ld_qkv, ss, ss_K, bq, bk, bv, cos_tab, sin_tab, n_pos, M, n_past, n_ctx,
+                            n_heads, n_kv_heads, head_dim, cap, kc, vc, nullptr, 0, ws, n_chunks, s);
 }
 
 extern "C" int vxh_attention_xpanel(const float *q, int M, int n_past, int n_ctx, int n_heads,
@@ -429,8 +567,8 @@ extern "C" int vxh_attention_xpanel(const float *q, int M, int n_past, int n_ctx
         return vxh_fail(VXH_ERR_PARAM, "attention_xpanel: panel K %d, need %d", p ? p->K : -1,
                         n_heads * head_dim);
     p->M = M;
-    return vx_attention_run(q, M, n_past, n_ctx, n_heads, n_kv_heads, head_dim, cap, kc, vc, out,
-                            ld_out, ws, row_counters, p, s);
+    return vx_attention_run(q, nullptr, 0, M, n_past, n_ctx, n_heads, n_kv_heads, head_dim, cap,
+                            (float *)kc, (float *)vc, out, ld_out, ws, row_counters, p, 0, nullptr, s);
 }
 
 __global__ void vx_add_rows_kernel(float *__restrict__ y, int ldy, const float *__restrict__ x,

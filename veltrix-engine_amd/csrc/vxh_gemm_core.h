@@ -151,7 +151,8 @@ struct vx_epi_args {
 // panel is made of.  Every workgroup sharing a K slice builds the same slice;
 // the first tile group also stores the updated residual and adds the row's
 // sum of squares, so the consumer of the product can apply the RMSNorm.
-enum { VX_PRO_PANEL = 0, VX_PRO_ROWS = 1, VX_PRO_RESID = 2, VX_PRO_SWIGLU = 3 };
+enum { VX_PRO_PANEL = 0, VX_PRO_ROWS = 1, VX_PRO_RESID = 2, VX_PRO_SWIGLU = 3, VX_PRO_ATTN = 4 };
+#define VX_PRO_ATTN_MAX_M VXH_PRO_ATTN_MAX_ROWS   // ATTN: M * PPW * 16 float4 columns <= 256 threads
 
 struct vx_pro_args {
     const float *x;         // ROWS, RESID: input rows
@@ -168,6 +169,8 @@ struct vx_pro_args {
     int K;                  // row length
     double *clr;            // n_clr doubles zeroed by the launch (an accumulator already consumed)
     long n_clr;
+    const float *part;      // ATTN: per-chunk attention partials (max, sum, pad 2, acc[hd])
+    int n_chunks, G, hd;    // ATTN: chunks per query, query heads per kv head, head_dim
 };
 
 struct vx_gemm_args {
@@ -287,6 +290,124 @@ __device__ __forceinline__ void vx_pro_values(const vx_pro_args &p, const vx_pro
     }
 }
 
+
+// ATTN: the K slice of the attention rows, combined from the per-chunk
+// partials of the attention's first launch (online-softmax rescale and
+// 1/(sum + 1e-10), src/tensor.c:156-171), then converted to the panel.
+// Thread t owns float4 column u = t % U of the slice (U = M * L/4: row m,
+// head, lane d4) and every S-th chunk from t / U (S = 256 / U slices); the
+// slices merge in LDS.
+template <int M, int PPW>
+__device__ __forceinline__ void vx_pro_attn(const vx_pro_args &p, int p0, int np, uint4 *lds, float *lrs)
+{
+    constexpr int NS = 2 * M;
+    constexpr int LMAX = PPW * 64;
+    __shared__ float s_m[256], s_l[256];
+    __shared__ float4 s_a[256];
+    __shared__ float s_row[M][LMAX];
+    const int L4 = np * 16, k0 = p0 * 64;
+    const int U = M * L4, S = 256 / U;
+    const int t = threadIdx.x, u = t % U, sl = t / U;
+    const int hd = p.hd, QM = p.G * M, PS = hd + 4;
+    const size_t cstride = (size_t)QM * PS;
+    const int m = u / L4, c4 = u % L4;
+    float mx = -INFINITY, l = 0.0f;
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (sl < S) {
+        const int e = k0 + 4 * c4;
+        const int head = e / hd, d4 = (e % hd) / 4;
+        const int g = head / p.G, qi = (head % p.G) * M + m;
+        const float *pq = p.part + (size_t)g * p.n_chunks * cstride + (size_t)qi * PS;
+        for (int c0 = sl; c0 < p.n_chunks; c0 += 4 * S) {
+            float cm[4], cl[4];
+            float4 ca[4];
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int c = c0 + v * S;
+                const float *pc = pq + (size_t)min(c, p.n_chunks - 1) * cstride;
+                cm[v] = c < p.n_chunks ? pc[0] : -INFINITY;
+                cl[v] = pc[1];
+                ca[v] = *(const float4 *)(pc + 4 + 4 * d4);
+            }
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                if (cm[v] == -INFINITY) continue;
+                const float nm = fmaxf(mx, cm[v]);
+                const float fo = mx == -INFINITY ? 0.0f : expf(mx - nm);
+                const float fn = expf(cm[v] - nm);
+                l = l * fo + cl[v] * fn;
+                a.x = a.x * fo + ca[v].x * fn;
+                a.y = a.y * fo + ca[v].y * fn;
+                a.z = a.z * fo + ca[v].z * fn;
+                a.w = a.w * fo + ca[v].w * fn;
+                mx = nm;
+            }
+        }
+    }
+    s_m[t] = mx;
+    s_l[t] = l;
+    s_a[t] = a;
+    __syncthreads();
+    if (t < U) {
+        float gm = -INFINITY;
+        for (int j = 0; j < S; j++) gm = fmaxf(gm, s_m[j * U + t]);
+        float lt = 0.0f;
+        float4 at = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int j = 0; j < S; j++) {
+            const float cm = s_m[j * U + t];
+            if (cm == -INFINITY) continue;
+            const float f = expf(cm - gm);
+            const float4 v = s_a[j * U + t];
+            lt = fmaf(f, s_l[j * U + t], lt);
+            at.x = fmaf(f, v.x, at.x);
+            at.y = fmaf(f, v.y, at.y);
+            at.z = fmaf(f, v.z, at.z);
+            at.w = fmaf(f, v.w, at.w);
+        }
+        const float inv = 1.0f / (lt + 1e-10f);
+        *(float4 *)&s_row[m][4 * c4] = make_float4(at.x * inv, at.y * inv, at.z * inv, at.w * inv);
+    }
+    __syncthreads();
+    // panel of the slice: wavefront w builds rows m = w + 4r, lane l the
+    // 8-column groups l + 64j (as the other prologue kinds)
+    const int lane = t & 63, wave = t >> 6, ng = np * 8;
+    constexpr int GL = (PPW * 8 + 63) / 64;
+#pragma unroll
+    for (int rr = 0; rr < (M + 3) / 4; rr++) {
+        const int mm = wave + 4 * rr;
+        if (mm >= M) continue;
+        float amax = 0.0f;
+#pragma unroll
+        for (int j = 0; j < GL; j++) {
+            const int g = lane + 64 * j;
+            if (g < ng)
+#pragma unroll
+                for (int kk = 0; kk < 8; kk++) amax = fmaxf(amax, fabsf(s_row[mm][8 * g + kk]));
+        }
+        amax = vx_wave_max64(amax);
+        float rs;
+        const float sc = vx_row_scale(amax, &rs);
+        if (lane == 0) lrs[mm] = rs;
+#pragma unroll
+        for (int j = 0; j < GL; j++) {
+            const int g = lane + 64 * j;
+            if (g >= ng) continue;
+            vx_half8 hi, lo;
+#pragma unroll
+            for (int kk = 0; kk < 8; kk++) {
+                const float xv = s_row[mm][8 * g + kk] * sc;
+                const _Float16 h = (_Float16)xv;
+                hi[kk] = h;
+                lo[kk] = (_Float16)(xv - (float)h);
+            }
+            const int b = g >> 2, h2 = (g >> 1) & 1, s2 = g & 1;
+            const int base = ((b * 2 + s2) * 2 + h2) * NS;
+            lds[base + mm] = __builtin_bit_cast(uint4, hi);
+            lds[base + M + mm] = __builtin_bit_cast(uint4, lo);
+        }
+    }
+}
+
 #define VX_RING 4
 
 // QT: 2 = Q4_0, 8 = Q8_0.
@@ -338,7 +459,7 @@ __global__ __launch_bounds__(256) void vx_gemm_kernel(vx_gemm_args a)
     // here, ahead of the weights; larger ones row by row after them.
     constexpr int RW = PANEL ? 1 : (M + 3) / 4;
     constexpr int GL = PANEL ? 1 : (PPW * 8 + 63) / 64;
-    constexpr bool PRELOAD = !PANEL && RW * GL <= 2;
+    constexpr bool PRELOAD = !PANEL && PRO != VX_PRO_ATTN && RW * GL <= 2;
     const int ng = np * 8, k0 = p0 * 64;
     vx_pro_raw raw[PRELOAD ? RW : 1][PRELOAD ? GL : 1];
     if constexpr (PRELOAD) {
@@ -376,6 +497,9 @@ __global__ __launch_bounds__(256) void vx_gemm_kernel(vx_gemm_args a)
     if constexpr (PANEL) {
 #pragma unroll
         for (int j = 0; j < UPT; j++) lds[j * 256 + threadIdx.x] = pv[j];
+    } else if constexpr (PRO == VX_PRO_ATTN) {
+        static_assert(M <= VX_PRO_ATTN_MAX_M && M * PPW * 16 <= 256, "ATTN slice columns exceed the workgroup");
+        vx_pro_attn<M, PPW>(a.p, p0, np, lds, lrs);
     } else {
         const bool lead = grp == 0;
 #pragma unroll

@@ -2,9 +2,10 @@
 // (vxh_gemm_pro): the residual add, RMSNorm weight, SwiGLU and the panel
 // conversion of the forward (src/model.c:514-594) run inside the GEMM that
 // consumes them instead of in a row kernel of their own, and the RMSNorm's
-// 1/rms is applied to the product by its consumer.  One prologue kind per
-// translation unit (vxh_pro_resid.hip, vxh_pro_swiglu.hip) so that the
-// template instances compile in parallel.
+// 1/rms is applied to the product by its consumer; or the attention combine
+// runs inside the output projection.  The residual and SwiGLU kinds have
+// translation units of their own (vxh_pro_resid.hip, vxh_pro_swiglu.hip) so
+// that the template instances compile in parallel.
 #include "vxh_gemm_core.h"
 
 int vx_gemm_pro_resid(const vxh_qmat *W, int M, vx_gemm_args &a, hipStream_t st, hipEvent_t e0,
@@ -47,6 +48,12 @@ extern "C" int vxh_gemm_pro(const vxh_qmat *W, int M, const vxh_pro *p, double *
         }
         break;
     }
+    case VXH_PRO_ATTN:
+        if (M > VX_PRO_ATTN_MAX_M || !p->part || p->n_chunks < 1 || p->n_kv_heads < 1 || p->head_dim < 4 ||
+            p->head_dim % 4 || p->n_heads % p->n_kv_heads || p->n_heads * p->head_dim != K)
+            return vxh_fail(VXH_ERR_PARAM, "gemm_pro: attention slice (M %d, %d heads of %d, K %d)", M,
+                            p->n_heads, p->head_dim, K);
+        break;
     case VXH_PRO_SWIGLU: {
         const int phys = (K + 15) / 16 * 32;
         if (!p->src || p->ld_src < phys || p->ld_src % 2 || !vx_al16(p->src))
@@ -92,11 +99,20 @@ extern "C" int vxh_gemm_pro(const vxh_qmat *W, int M, const vxh_pro *p, double *
     a.p.K = K;
     a.p.clr = p->n_clear ? p->clear : nullptr;
     a.p.n_clr = (long)p->n_clear;
+    if (p->kind == VXH_PRO_ATTN) {
+        a.p.part = p->part;
+        a.p.n_chunks = p->n_chunks;
+        a.p.G = p->n_heads / p->n_kv_heads;
+        a.p.hd = p->head_dim;
+    }
     hipStream_t st = vxh_hs(s);
     hipEvent_t e0 = (hipEvent_t)start, e1 = (hipEvent_t)stop;
     switch (p->kind) {
     case VXH_PRO_ROWS: return vx_dispatch<VX_EPI_NONE, VX_PRO_ROWS>(W, M, 0, a, st, e0, e1);
     case VXH_PRO_RESID: return vx_gemm_pro_resid(W, M, a, st, e0, e1);
+    case VXH_PRO_ATTN:
+        if (M == 1) return vx_dispatch_m<1, VX_EPI_NONE, VX_PRO_ATTN>(W, 0, a, st, e0, e1);
+        return vx_dispatch_m<2, VX_EPI_NONE, VX_PRO_ATTN>(W, 0, a, st, e0, e1);
     default: return vx_gemm_pro_swiglu(W, M, a, st, e0, e1);
     }
 }

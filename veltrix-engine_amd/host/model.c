@@ -918,16 +918,18 @@ static vx_error pgemm(vx_dev *d, const vxh_qmat *W, const vxh_pro *p, int M, dou
     return VX_OK;
 }
 
-/* Prologue forward: each GEMM builds its own input panel slice, so a layer
- * is QKV -> RoPE/KV -> attention (2) -> O -> gate/up -> down, 7 launches.
+/* Prologue forward: each GEMM builds its own input panel slice.
  *   QKV     t = x + acc_x (previous down projection) -> x2, panel attn_norm .* t
- *   RoPE    q|k|v = acc_qkv / rms(t)
+ *   RoPE    q|k|v = RoPE(acc_qkv / rms(t)), new k/v rows into the cache
+ *   attn    partials per chunk, combined
  *   O       panel att -> acc_y
  *   gate/up t = x2 + acc_y -> x, panel ffn_norm .* t -> acc_gu
  *   down    panel SwiGLU(acc_gu / rms(t)) -> acc_x
+ * 7 launches per layer; for one or two rows the attention's first launch
+ * does the RoPE and the output projection the combine, 5 launches.
  * An accumulator is cleared by a later launch that no longer races with its
- * readers: acc_gu by the next QKV (or the output GEMM), acc_x by O, acc_y by
- * down; acc_qkv by RoPE. */
+ * readers: acc_gu by the next QKV (or the output GEMM), acc_x by gate/up,
+ * acc_y by down; acc_qkv by RoPE (or the output projection). */
 static vx_error forward_pro(vx_model *m, int M, int n_past, int logits_mode)
 {
     vx_dev *d = vx_dev_of(m);
@@ -942,6 +944,9 @@ static vx_error forward_pro(vx_model *m, int M, int n_past, int logits_mode)
     if (d->has_embd) TRY(vxh_qmat_gather_rows(&d->embd, d->tok, M, vx_get_synthetic_weight_scale(), d->x, dd, s));
     else TRY(vxh_fill_f32(d->x, 0.0f, (size_t)M * dd, s));
 
+    /* one- and two-row forwards (draft decode): the output projection
+     * combines the attention partials itself */
+    const int attn_in_o = M <= VXH_PRO_ATTN_MAX_ROWS && d->hd % 4 == 0;
     vxh_pro p;
     for (int l = 0; l < L; l++) {
         vx_dev_layer *Ld = &d->layers[l];
@@ -957,15 +962,26 @@ static vx_error forward_pro(vx_model *m, int M, int n_past, int logits_mode)
         p.clear = d->acc_gu; p.n_clear = (size_t)M * d->ld_gu;
         if ((e = pgemm(d, &Ld->wqkv, &p, M, d->acc_qkv, d->ld_qkv, dd + 2 * kvd, VX_PROF_QKV, dd + 2 * kvd)))
             return e;
-        TRY(vxh_rope_kv_norm(d->acc_qkv, d->ld_qkv, M, n_past, n_ctx, d->n_heads, d->n_kv, d->hd, Ld->bq,
-                             Ld->bk, Ld->bv, d->rope_cos, d->rope_sin, d->n_pos, SS(l, 0), dd, d->q, kc,
-                             vc, s));
-        TRY(vxh_attention(d->q, M, n_past, n_ctx, d->n_heads, d->n_kv, d->hd, d->opt.attn_cap, kc, vc,
-                          d->att, dd, &d->ws, s));
         memset(&p, 0, sizeof(p));
-        p.kind = VXH_PRO_ROWS;
-        p.x = d->att; p.ldx = dd;
-        p.clear = d->acc_x; p.n_clear = (size_t)M * dd;
+        if (attn_in_o) {
+            /* partials of the attention, combined by the output projection */
+            int n_chunks = 0;
+            TRY(vxh_attention_parts_qkv(d->acc_qkv, d->ld_qkv, SS(l, 0), dd, Ld->bq, Ld->bk, Ld->bv,
+                                        d->rope_cos, d->rope_sin, d->n_pos, M, n_past, n_ctx, d->n_heads,
+                                        d->n_kv, d->hd, d->opt.attn_cap, kc, vc, &d->ws, &n_chunks, s));
+            p.kind = VXH_PRO_ATTN;
+            p.part = d->ws.part; p.n_chunks = n_chunks;
+            p.n_heads = d->n_heads; p.n_kv_heads = d->n_kv; p.head_dim = d->hd;
+            p.clear = d->acc_qkv; p.n_clear = (size_t)M * d->ld_qkv;
+        } else {
+            TRY(vxh_rope_kv_norm(d->acc_qkv, d->ld_qkv, M, n_past, n_ctx, d->n_heads, d->n_kv, d->hd,
+                                 Ld->bq, Ld->bk, Ld->bv, d->rope_cos, d->rope_sin, d->n_pos, SS(l, 0), dd,
+                                 d->q, kc, vc, s));
+            TRY(vxh_attention(d->q, M, n_past, n_ctx, d->n_heads, d->n_kv, d->hd, d->opt.attn_cap, kc, vc,
+                              d->att, dd, &d->ws, s));
+            p.kind = VXH_PRO_ROWS;
+            p.x = d->att; p.ldx = dd;
+        }
         if ((e = pgemm(d, &Ld->wo, &p, M, d->acc_y, dd, dd, VX_PROF_O, dd))) return e;
         memset(&p, 0, sizeof(p));
         p.kind = VXH_PRO_RESID;
@@ -974,6 +990,7 @@ static vx_error forward_pro(vx_model *m, int M, int n_past, int logits_mode)
         p.w = Ld->ffn_norm;
         p.x_out = d->x; p.ld_xout = dd;
         p.ss = SS(l, 1);
+        p.clear = d->acc_x; p.n_clear = (size_t)M * dd;
         if ((e = pgemm(d, &Ld->wgu, &p, M, d->acc_gu, d->ld_gu, d->ld_gu, VX_PROF_GATEUP, 2 * d->F)))
             return e;
         memset(&p, 0, sizeof(p));
