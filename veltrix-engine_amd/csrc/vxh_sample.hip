@@ -257,11 +257,116 @@ __global__ __launch_bounds__(SB) void vx_sample_kernel(const float *__restrict__
     }
 }
 
+// The sampler without a nucleus for V <= SB * SE: thread t owns the
+// contiguous entries [t*SE, t*SE + SE), loaded once; exponentials, masses and
+// the inverse-CDF prefix stay in registers (one wavefront-shuffle scan and
+// one LDS exchange instead of passes over the row).  Same arithmetic as
+// vx_sample_kernel with top_p = 1.
+#define SE 32
+
+__device__ __forceinline__ uint64_t vx_shfl_up_u64(uint64_t v, int o)
+{
+    uint32_t lo = __shfl_up((uint32_t)v, o, 64), hi = __shfl_up((uint32_t)(v >> 32), o, 64);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+__global__ __launch_bounds__(SB) void vx_sample_reg_kernel(const float *__restrict__ l, int V, float T,
+                                                           const float *__restrict__ u,
+                                                           int *__restrict__ token_out,
+                                                           float *__restrict__ nuc)
+{
+    __shared__ float redv[SB / 64];
+    __shared__ int redi[SB / 64];
+    __shared__ uint64_t wsum[SB / 64];
+    __shared__ int res;
+    const int b = threadIdx.x * SE, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float x[SE];
+    if (b + SE <= V) {
+#pragma unroll
+        for (int j = 0; j < SE / 4; j++) {
+            const float4 v = *(const float4 *)(l + b + 4 * j);
+            x[4 * j] = v.x; x[4 * j + 1] = v.y; x[4 * j + 2] = v.z; x[4 * j + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < SE; j++) x[j] = b + j < V ? l[b + j] : 0.0f;
+    }
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < SE; j++)
+        if (b + j < V && (x[j] > bv || (x[j] == bv && b + j < bi))) { bv = x[j]; bi = b + j; }
+    const int am = vx_wg_argmax(bv, bi, redv, redi);
+    if (!(T > 0.0f)) {
+        if (threadIdx.x == 0) {
+            token_out[0] = am;
+            nuc[0] = l[am]; nuc[1] = 0.0f; nuc[2] = -1.0f; nuc[3] = __int_as_float(V - 1);
+            nuc[4] = 0.0f; nuc[5] = __int_as_float(am); nuc[6] = 0.0f; nuc[7] = 0.0f;
+        }
+        return;
+    }
+    const float mx = l[am];
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < SE; j++) {
+        x[j] = b + j < V ? expf((x[j] - mx) / T) : 0.0f;
+        sum += x[j];
+    }
+    sum = vx_wg_sum(sum, redv);
+    const float inv = 1.0f / (sum + 1e-30f);
+    uint64_t St = 0;
+#pragma unroll
+    for (int j = 0; j < SE; j++) {
+        x[j] *= inv;                      // p_v = expf((l_v - max)/T) * inv
+        St += vx_fixed32(x[j]);
+    }
+    // exclusive prefix of the per-thread masses in index order
+    uint64_t incl = St;
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint64_t y = vx_shfl_up_u64(incl, o);
+        if (lane >= o) incl += y;
+    }
+    if (lane == 63) wsum[wave] = incl;
+    if (threadIdx.x == 0) res = am;
+    __syncthreads();
+    uint64_t off = 0, S = 0;
+    for (int w = 0; w < SB / 64; w++) {
+        if (w < wave) off += wsum[w];
+        S += wsum[w];
+    }
+    if (S > 0) {
+        const uint64_t thr = vx_threshold(u[0], S);
+        const uint64_t before = off + incl - St;
+        if (before < thr && before + St >= thr) {
+            // first entry whose inclusive prefix reaches thr
+            uint64_t c = before;
+            int tok = b + SE - 1;
+            bool found = false;
+#pragma unroll
+            for (int j = 0; j < SE; j++) {
+                c += vx_fixed32(x[j]);
+                if (!found && c >= thr) { tok = b + j; found = true; }
+            }
+            res = tok;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        token_out[0] = res;
+        nuc[0] = mx; nuc[1] = inv; nuc[2] = -1.0f; nuc[3] = __int_as_float(V - 1);
+        nuc[4] = (float)((double)S / 4294967296.0); nuc[5] = __int_as_float(am);
+        nuc[6] = 0.0f; nuc[7] = 0.0f;
+    }
+}
+
 extern "C" int vxh_sample(const float *l, int V, float T, float top_p, const float *u_dev,
                           int *token_out, float *nuc, vxh_stream s)
 {
     if (V <= 0) return vxh_fail(VXH_ERR_PARAM, "sample: V %d", V);
-    vx_sample_kernel<<<1, SB, 0, vxh_hs(s)>>>(l, V, T, top_p, u_dev, token_out, nuc);
+    if (!(top_p < 1.0f) && V <= SB * SE && ((uintptr_t)l & 15) == 0)
+        vx_sample_reg_kernel<<<1, SB, 0, vxh_hs(s)>>>(l, V, T, u_dev, token_out, nuc);
+    else
+        vx_sample_kernel<<<1, SB, 0, vxh_hs(s)>>>(l, V, T, top_p, u_dev, token_out, nuc);
     VXH_LAUNCHED();
     return VXH_OK;
 }
