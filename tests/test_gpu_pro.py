@@ -488,7 +488,7 @@ def test_pro_attn_combines_partials(P, H, KV, hd, M, typ):
                                            n_pos, M, n_past, n_ctx, H, KV, hd, 4096, dkc.ptr, dvc.ptr,
                                            C.byref(ws), C.byref(nch), None)
             assert rc == 0, P.vxh_last_error()
-            assert nch.value == (n_past + M + 31) // 32
+            assert 1 <= nch.value <= (n_past + M + 31) // 32
             pro = Pro(kind=PRO_ATTN, part=ws.part, n_chunks=nch.value, n_heads=H, n_kv_heads=KV, head_dim=hd,
                       clear=dqkv.ptr, n_clear=M * ld)
         else:
@@ -506,7 +506,10 @@ def test_pro_attn_combines_partials(P, H, KV, hd, M, typ):
             b.free()
     (a0, k0), (a1, k1) = res
     assert np.array_equal(k0, k1), "same new cache rows"
-    assert close(a1, a0, atol=1e-5, rtol=1e-4), max_violation(a1, a0, 1e-5, 1e-4)
+    # the two combine orders differ by float rounding of terms as large as
+    # the largest output
+    tol = 1e-6 * float(np.abs(a0).max())
+    assert close(a1, a0, atol=tol, rtol=1e-4), max_violation(a1, a0, tol, 1e-4)
     bad = Pro(kind=PRO_ATTN, part=ws.part, n_chunks=4, n_heads=H, n_kv_heads=KV, head_dim=hd)
     acc = N.DevBuf(P, np.zeros(3 * 640))
     assert P.vxh_gemm_pro(C.byref(q), 3, C.byref(bad), acc.ptr, 640, 640, 1.0, None, None, None) != 0
@@ -515,3 +518,76 @@ def test_pro_attn_combines_partials(P, H, KV, hd, M, typ):
     P.vxh_qmat_free(C.byref(q))
     for b in (dcs, dsn, dss):
         b.free()
+
+
+@pytest.mark.parametrize("H,KV,hd,M,n_past,n_ctx,cap", [
+    (32, 32, 128, 9, 2100, 4096, 4096),   # verify: MHA, 9 rows, 128-position chunks
+    (32, 4, 64, 1, 2200, 4096, 4096),     # draft decode: 8 query heads per kv head
+    (8, 1, 64, 2, 50, 300, 40),           # cap below the positions, partial last chunk
+    (4, 4, 128, 1, 260, 200, 4096),       # past the context: clamped row
+    (8, 8, 128, 16, 100, 512, 4096),      # 16 query vectors per kv head
+    (16, 2, 32, 3, 90, 256, 4096),        # head_dim 32: 32-position chunks
+])
+def test_attention_matches_reference(P, H, KV, hd, M, n_past, n_ctx, cap):
+    """vxh_attention against softmax attention in float64 on the same cache
+    (src/model.c:300-338: row m attends to [0, min(pos_m + 1, cap)), pos_m =
+    min(n_past + m, n_ctx - 1); 1/(sum + 1e-10))."""
+    print(f"attention H={H} KV={KV} hd={hd} M={M} n_past={n_past} n_ctx={n_ctx} cap={cap}", flush=True)
+    bind_attention(P)
+    rng = np.random.default_rng(H + KV * 5 + hd + M + n_past)
+    qd, kvd = H * hd, KV * hd
+    qv = rng.normal(0, 1.0, (M, qd)).astype(np.float32)
+    kc = rng.normal(0, 1.0, (n_ctx, kvd)).astype(np.float32)
+    vc = rng.normal(0, 1.0, (n_ctx, kvd)).astype(np.float32)
+    dq, dk, dv = N.DevBuf(P, qv), N.DevBuf(P, kc), N.DevBuf(P, vc)
+    dout = N.DevBuf(P, np.zeros((M, qd), np.float32))
+    ws = Workspace()
+    assert P.vxh_workspace_alloc(C.byref(ws), 32, P.vxh_attention_workspace_floats(M, n_ctx, cap, H, KV, hd)) == 0
+    rc = P.vxh_attention(dq.ptr, M, n_past, n_ctx, H, KV, hd, cap, dk.ptr, dv.ptr, dout.ptr, qd, C.byref(ws), None)
+    assert rc == 0, P.vxh_last_error()
+    assert P.vxh_stream_sync(None) == 0
+    got = dout.get(np.float32, M * qd).reshape(M, qd)
+    ref = np.zeros((M, qd))
+    G = H // KV
+    for m in range(M):
+        pos = min(n_past + m, n_ctx - 1)
+        cs = min(pos + 1, cap) if cap > 0 else pos + 1
+        for h in range(H):
+            g = h // G
+            K = kc[:cs, g * hd:(g + 1) * hd].astype(np.float64)
+            Vv = vc[:cs, g * hd:(g + 1) * hd].astype(np.float64)
+            s = K @ qv[m, h * hd:(h + 1) * hd].astype(np.float64) / np.sqrt(hd)
+            p = np.exp(s - s.max())
+            ref[m, h * hd:(h + 1) * hd] = (p @ Vv) / (p.sum() + 1e-10)
+    assert close(got, ref, atol=1e-5, rtol=1e-4), max_violation(got, ref, 1e-5, 1e-4)
+    P.vxh_workspace_free(C.byref(ws))
+    for b in (dq, dk, dv, dout):
+        b.free()
+
+
+def test_wide_attention_clamp_and_cap_in_model(P, tmp_path):
+    """The model path with head_dim 128 (clamped context) and head_dim 64 with
+    an attention cap, in batches small enough for the wide-chunk kernel."""
+    print("wide attention clamp/cap in the model", flush=True)
+    path, raw, (L, d, h, kv, ff, V) = make(tmp_path, 74, L=1, d=256, h=2, kv=1, ff=256, V=64)
+    g = GpuModel(P, path, n_ctx=6)
+    om = OracleModel(raw, L, d, h, kv, ff, V, n_ctx=6)
+    toks = np.random.default_rng(6).integers(0, V, 9).astype(np.int32)
+    try:
+        got = g.verify(toks)
+        ref = np.zeros((9, V), np.float32)
+        O.or_forward_all(om.ptr, toks, 9, ref)
+        assert close(got, ref), max_violation(got, ref)
+    finally:
+        g.close()
+    path, raw, (L, d, h, kv, ff, V) = make(tmp_path, 75, L=1, d=256, h=4, kv=2, ff=256, V=80)
+    g = GpuModel(P, path, cap=8)
+    om = OracleModel(raw, L, d, h, kv, ff, V, n_ctx=4096, attn_cap=8)
+    toks = np.random.default_rng(7).integers(0, V, 21).astype(np.int32)
+    try:
+        got = np.concatenate([g.verify(toks[i:i + 7]) for i in range(0, 21, 7)])
+        ref = np.zeros((21, V), np.float32)
+        O.or_forward_all(om.ptr, toks, 21, ref)
+        assert close(got, ref), max_violation(got, ref)
+    finally:
+        g.close()

@@ -106,17 +106,18 @@ struct vx_mcfg {
 
 // Block pairs per K slice.  Each M has up to three slice lengths (in
 // ascending order); the launcher takes the shortest one whose launch stays
-// within VX_WG_TARGET workgroups, or the longest.  Short slices suit the small
-// draft matrices at M = 1, long ones the large verify matrices; M > 12 stays
-// short for LDS.
+// within `target` workgroups, or the longest.  Short slices suit the small
+// draft matrices at M = 1 (in the decode pipeline 2 pairs beat 1 and 4 by
+// 5-10% of the draft time), long ones the large verify matrices; M > 12
+// stays short for LDS.
 template <int QT, int M>
 struct vx_ppw_set {
     static constexpr int n = QT == 8 ? (M <= 4 ? 2 : 1) : (M <= 4 ? 3 : 2);
     static constexpr int v0 = QT == 8 ? (M <= 4 ? 2 : 8) : (M <= 4 ? 2 : (M <= 12 ? 8 : 4));
     static constexpr int v1 = QT == 8 ? 8 : (M <= 4 ? 4 : (M <= 12 ? 16 : 8));
     static constexpr int v2 = QT == 8 ? 8 : (M <= 4 ? 8 : (M <= 12 ? 16 : 8));
+    static constexpr int target = 1600;
 };
-#define VX_WG_TARGET 1600
 
 // Fused-epilogue arguments (vxh_fused.hip): the last workgroup to finish a
 // super-group of output rows runs the epilogue on its final sums.
@@ -690,7 +691,7 @@ static int vx_launch_gemm(const vxh_qmat *W, vx_gemm_args &a, hipStream_t st, hi
     const int cand[3] = {S::v0, S::v1, S::v2};
     int pick = S::n - 1;
     for (int i = 0; i < S::n; i++)
-        if (groups * ((W->n_pairs + cand[i] - 1) / cand[i]) <= VX_WG_TARGET) { pick = i; break; }
+        if (groups * ((W->n_pairs + cand[i] - 1) / cand[i]) <= S::target) { pick = i; break; }
     if (pick == 0) return vx_launch_ppw<QT, M, AVX2, S::v0, EPI, PRO>(W, a, st, e0, e1);
     if (pick == 1) return vx_launch_ppw<QT, M, AVX2, S::v1, EPI, PRO>(W, a, st, e0, e1);
     return vx_launch_ppw<QT, M, AVX2, S::v2, EPI, PRO>(W, a, st, e0, e1);
