@@ -316,9 +316,11 @@ def run_spec(args):
 
 
 def run_gemm(args):
-    """Isolated verify-shaped GEMM kernels (vxh_gemm_acc) at M = k+1 on the
-    7B shapes, weights rotated over > 300 MB so the Infinity Cache does not
-    serve them."""
+    """Isolated verify GEMM kernels at M = k+1 on the 7B shapes, each with the
+    panel prologue the verify forward gives it (vxh_gemm_pro: residual add +
+    norm weight for QKV and gate/up, attention rows for the output
+    projection, SwiGLU for down, norm weight for the logits), weights rotated
+    over > 300 MB so the Infinity Cache does not serve them."""
     N, P = load_product()
     import ctypes as CC
     vp = CC.c_void_p
@@ -326,10 +328,8 @@ def run_gemm(args):
     L.vxh_qmat_alloc.argtypes = [vp, CC.c_int, CC.c_int, CC.c_int]
     L.vxh_synth_blocks.argtypes = [vp, CC.c_int, CC.c_int, CC.c_int, CC.c_uint64, CC.c_float, vp]
     L.vxh_qmat_set_rows.argtypes = [vp, vp, CC.c_int, CC.c_int, CC.c_int, CC.c_int, CC.c_int, vp]
-    L.vxh_panel_alloc.argtypes = [vp, CC.c_int, CC.c_int]
-    L.vxh_prep_panel.argtypes = [vp, vp, CC.c_int, CC.c_int, CC.c_int, CC.c_int, vp, CC.c_int, vp]
-    L.vxh_gemm_acc.argtypes = [vp, vp, CC.c_int, vp, CC.c_int, CC.c_int, CC.c_float, vp, CC.c_int,
-                               CC.c_float, CC.c_int, vp]
+    L.vxh_gemm_pro.argtypes = [vp, CC.c_int, vp, vp, CC.c_int, CC.c_int, CC.c_float, vp, vp, vp]
+    L.vxh_qmat_free.argtypes = [vp]
     L.vxh_event_create.argtypes = [vp]
     L.vxh_event_record.argtypes = [vp, vp]
     L.vxh_event_elapsed_ms.argtypes = [vp, vp, vp]
@@ -338,9 +338,13 @@ def run_gemm(args):
         _fields_ = [("type", CC.c_int), ("n_rows", CC.c_int), ("n_cols", CC.c_int), ("n_pairs", CC.c_int),
                     ("qs", vp), ("d", vp)]
 
-    class Panel(CC.Structure):
-        _fields_ = [("data", vp), ("corr", vp), ("rscale", vp), ("xs", vp), ("M", CC.c_int),
-                    ("K", CC.c_int), ("avx2", CC.c_int)]
+    class Pro(CC.Structure):
+        _fields_ = [("kind", CC.c_int), ("x", vp), ("ldx", CC.c_int), ("src", vp), ("ld_src", CC.c_int),
+                    ("w", vp), ("x_out", vp), ("ld_xout", CC.c_int), ("ss", vp), ("ss_in", vp),
+                    ("ss_K", CC.c_int), ("thr", CC.c_float), ("clear", vp), ("n_clear", CC.c_size_t),
+                    ("part", vp), ("n_chunks", CC.c_int), ("n_heads", CC.c_int), ("n_kv_heads", CC.c_int),
+                    ("head_dim", CC.c_int)]
+    PRO_ROWS, PRO_RESID, PRO_SWIGLU = 1, 2, 3
 
     M = args.k + 1
     results = []
@@ -355,6 +359,9 @@ def run_gemm(args):
     log(json.dumps({"calibration_copy_bytes": cal_bytes, "copies": 3}))
     ca.free()
     cb.free()
+    kinds = {(4096, 4096): PRO_ROWS, (12288, 4096): PRO_RESID, (4096, 11008): PRO_SWIGLU,
+             (22016, 4096): PRO_RESID, (32000, 4096): PRO_ROWS, (11008, 4096): PRO_RESID}
+    rng = np.random.default_rng(1)
     for rows, cols, qt in ((4096, 4096, 2), (12288, 4096, 2), (4096, 11008, 2), (22016, 4096, 2),
                            (32000, 4096, 2), (11008, 4096, 8), (4096, 11008, 8)):
         bpw = 18 if qt == 2 else 34
@@ -369,18 +376,28 @@ def run_gemm(args):
             assert L.vxh_qmat_set_rows(CC.byref(q), stage.ptr, 1, rows, rows, 0, 0, None) == 0
             mats.append(q)
         stage.free()
-        x = N.DevBuf(L, np.random.default_rng(1).normal(0, 1, (M, cols)).astype(np.float32))
+        kind = kinds[(rows, cols)]
+        ld_src = (cols + 15) // 16 * 32 if kind == PRO_SWIGLU else cols
+        bufs = [N.DevBuf(L, rng.normal(0, 1, (M, cols)).astype(np.float32)),     # x
+                N.DevBuf(L, rng.normal(0, 1, (M, ld_src))),                       # src
+                N.DevBuf(L, rng.normal(1, 0.1, cols).astype(np.float32)),        # w
+                N.DevBuf(L, nbytes=4 * M * cols),                                 # x_out
+                N.DevBuf(L, np.zeros(16, np.float64)),                            # ss
+                N.DevBuf(L, rng.uniform(100, 1000, 16))]                          # ss_in
+        pro = Pro(kind=kind)
+        if kind in (PRO_ROWS, PRO_RESID):
+            pro.x, pro.ldx, pro.w, pro.ss = bufs[0].ptr, cols, bufs[2].ptr, bufs[4].ptr
+        if kind == PRO_RESID:
+            pro.src, pro.ld_src, pro.x_out, pro.ld_xout = bufs[1].ptr, cols, bufs[3].ptr, cols
+        if kind == PRO_SWIGLU:
+            pro.src, pro.ld_src, pro.ss_in, pro.ss_K, pro.thr = bufs[1].ptr, ld_src, bufs[5].ptr, 4096, 0.01
         acc = N.DevBuf(L, np.zeros(M * rows, np.float64))
-        pan = Panel()
-        assert L.vxh_panel_alloc(CC.byref(pan), 16, cols) == 0
-        assert L.vxh_prep_panel(CC.byref(pan), x.ptr, cols, M, cols, 0, None, 0, None) == 0
         e0, e1 = vp(), vp()
         L.vxh_event_create(CC.byref(e0))
         L.vxh_event_create(CC.byref(e1))
 
         def launch(q):
-            return L.vxh_gemm_acc(CC.byref(q), CC.byref(pan), M, acc.ptr, rows, rows, 1.0, None, 0, 0.0,
-                                  0, None)
+            return L.vxh_gemm_pro(CC.byref(q), M, CC.byref(pro), acc.ptr, rows, rows, 1.0, None, None, None)
         for q in mats:
             assert launch(q) == 0, L.vxh_last_error()
         reps = args.steps * 10
@@ -397,9 +414,14 @@ def run_gemm(args):
         alg = mat_bytes + 4 * M * cols + 4 * M * rows
         gbs = alg / (avg_us * 1e-6) / 1e9
         results.append({"shape": f"{'Q4_0' if qt == 2 else 'Q8_0'} {rows}x{cols} M={M}",
+                        "prologue": {PRO_ROWS: "rows", PRO_RESID: "resid", PRO_SWIGLU: "swiglu"}[kind],
                         "avg_us": round(avg_us, 2), "GB/s": round(gbs, 1),
                         "frac": round(gbs / PEAK_HBM_GBS, 4)})
         log(json.dumps(results[-1]))
+        for b in bufs + [acc]:
+            b.free()
+        for q in mats:
+            L.vxh_qmat_free(CC.byref(q))
     print(json.dumps({"mode": "gemm", "M": M, "results": results}), flush=True)
 
 
