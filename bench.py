@@ -238,7 +238,11 @@ def run_spec(args):
     for _ in range(args.warmup):
         if P.vx_speculative_decode(st, out, args.tokens) != args.tokens:
             sys.exit("bench.py: decode failed: " + N.product_error())
-    P.vx_model_set_profiling(tm, 1)
+    # kernel-execution events around every --prof-every-th verify GEMM of each
+    # class (7: a stride that walks through the 32 layers): a launch with
+    # events costs ~18 us of host time, enough to starve the GPU when every
+    # verify GEMM carries them (174.7 vs 186.3 tok/s)
+    P.vx_model_set_profiling(tm, args.prof_every)
     P.vxh_device_sync()
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -305,7 +309,8 @@ def run_spec(args):
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
             "traffic": read_traffic(),
-            "kernel": f"vx_gemm_kernel (Q4_0, M={args.k + 1}), all verify GEMM launches (kernel-execution events)",
+            "kernel": (f"vx_gemm_kernel (Q4_0, M={args.k + 1}), every {args.prof_every}th verify GEMM launch "
+                       f"of each class (kernel-execution events)"),
             "launches": launches,
             "avg_launch_us": round(1e3 * ms / max(launches, 1), 3),
             "bytes_per_launch": round(byt / max(launches, 1)),
@@ -435,6 +440,8 @@ def main():
     ap.add_argument("--k", type=int, default=8)
     ap.add_argument("--mode", choices=["spec", "gemm"], default="spec")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--prof-every", type=int, default=7,
+                    help="time every n-th verify GEMM of each class with kernel events")
     args = ap.parse_args()
     ws = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or ws != 1:

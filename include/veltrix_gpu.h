@@ -125,10 +125,11 @@ void vx_speculative_set_trace(vx_speculative_state *state, int *drafts, int *emi
                               int *accepted, int max_rounds);
 
 /* ---- GEMM profiling ------------------------------------------------------------
- * When enabled, every GEMM launch of the model is bracketed by two HIP events
- * recorded on the model's stream; vx_model_get_profile folds the elapsed
- * times per matrix class.  bytes are algorithmic: weight blocks + fp32
- * activations in + fp32 results out. */
+ * vx_model_set_profiling(model, n), n >= 1: every n-th GEMM launch of each
+ * matrix class is bracketed by two HIP events that the dispatch records
+ * around the kernel on the model's stream (n = 1: every launch; 0: off);
+ * vx_model_get_profile folds the elapsed times per class.  bytes are
+ * algorithmic: weight blocks + fp32 activations in + fp32 results out. */
 enum { VX_PROF_QKV = 0, VX_PROF_O, VX_PROF_GATEUP, VX_PROF_DOWN, VX_PROF_OUTPUT, VX_PROF_N };
 typedef struct {
     int launches;

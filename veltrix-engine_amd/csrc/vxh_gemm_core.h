@@ -11,17 +11,6 @@
 
 #include "vxh_internal.h"
 
-// Power-of-two row scale: s = 2^-e with amax = f * 2^e, f in [0.5, 1), so
-// that every scaled value has magnitude < 1 (fp16 hi/lo keep 22 bits).
-__device__ __forceinline__ float vx_row_scale(float amax, float *rs_out)
-{
-    if (!(amax > 0.0f) || !isfinite(amax)) { *rs_out = 1.0f; return 1.0f; }
-    int e;
-    frexpf(amax, &e);
-    *rs_out = ldexpf(1.0f, e);
-    return ldexpf(1.0f, -e);
-}
-
 __device__ __forceinline__ float vx_silu(float g) { return g / (1.0f + expf(-g)); }
 
 // Panel unit of group g (elements 8g..8g+7): block b = g/4, lane half h =
@@ -204,18 +193,6 @@ __device__ void vx_gemm_epilogue(const vx_gemm_args &a, int sg, uint4 *lds, int 
 // ---------------------------------------------------------------------------
 // prologue kinds: building the panel slice in the GEMM
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float vx_wave_max64(float v)
-{
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
-
-__device__ __forceinline__ float vx_wave_sum64(float v)
-{
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
-
 // Source values of one 8-column group of a prologue row.
 struct vx_pro_raw {
     float4 x0, x1, w0, w1;

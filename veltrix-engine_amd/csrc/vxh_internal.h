@@ -50,3 +50,26 @@ __device__ __forceinline__ float vx_rms_inv(float ss, int K)
     float rms = sqrtf(ss / (float)K + 1e-5f);
     return rms < 1e-10f ? 0.0f : 1.0f / rms;
 }
+
+// Power-of-two row scale: s = 2^-e with amax = f * 2^e, f in [0.5, 1), so
+// that every scaled value has magnitude < 1 (fp16 hi/lo keep 22 bits).
+__device__ __forceinline__ float vx_row_scale(float amax, float *rs_out)
+{
+    if (!(amax > 0.0f) || !isfinite(amax)) { *rs_out = 1.0f; return 1.0f; }
+    int e;
+    frexpf(amax, &e);
+    *rs_out = ldexpf(1.0f, e);
+    return ldexpf(1.0f, -e);
+}
+
+__device__ __forceinline__ float vx_wave_max64(float v)
+{
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+__device__ __forceinline__ float vx_wave_sum64(float v)
+{
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}

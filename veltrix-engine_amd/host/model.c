@@ -696,7 +696,8 @@ void vx_model_set_profiling(vx_model *m, int on)
     if (!d) return;
     prof_fold(d);
     memset(d->prof, 0, sizeof(d->prof));
-    d->prof_on = on ? 1 : 0;
+    d->prof_on = on > 0 ? on : 0;
+    memset(d->prof_tick, 0, sizeof(d->prof_tick));
     if (d->prof_on && !d->prof_cap) {
         int cap = 4096;
         d->prof_ev = (vxh_event *)calloc((size_t)cap * 2, sizeof(vxh_event));
@@ -725,6 +726,7 @@ static vx_error prof_slot(vx_dev *d, const vxh_qmat *W, int M, int n_out, int cl
 {
     *e0 = *e1 = NULL;
     if (!d->prof_on) return VX_OK;
+    if (d->prof_tick[cls]++ % d->prof_on) return VX_OK;   /* every prof_on-th launch of the class */
     if (d->prof_n == d->prof_cap) {
         vx_error e = prof_fold(d);
         if (e != VX_OK) return e;

@@ -101,7 +101,8 @@ typedef struct vx_dev {
     float *x2;
     double *acc_y;
     /* GEMM profiling (vx_model_set_profiling) */
-    int prof_on;
+    int prof_on;                       /* 0: off; n: every n-th launch per class   */
+    int prof_tick[VX_PROF_N];
     int prof_n, prof_cap;
     vxh_event *prof_ev;                /* [2 * prof_cap]                            */
     int *prof_cls;
