@@ -433,11 +433,13 @@ __global__ __launch_bounds__(256) void vx_gemm_kernel(vx_gemm_args a)
         for (int j = 0; j < UPT; j++) pv[j] = psrc[min(j * 256 + (int)threadIdx.x, units - 1)];
     }
     // prologue kinds: the slice's source rows; wavefront w builds rows
-    // m = w + 4r, lane l the 8-column groups l + 64j.  Small slices are loaded
-    // here, ahead of the weights; larger ones row by row after them.
+    // m = w + 4r, lane l the 8-column groups l + 64j.  Up to 4 groups per lane
+    // are loaded here, ahead of the weights, so their round trips overlap
+    // (verify at M = 9: 3 groups; 186 -> 192 tok/s); larger slices go row by
+    // row after them (8 preloaded groups cost occupancy: logits GEMM 24 -> 30 us).
     constexpr int RW = PANEL ? 1 : (M + 3) / 4;
     constexpr int GL = PANEL ? 1 : (PPW * 8 + 63) / 64;
-    constexpr bool PRELOAD = !PANEL && PRO != VX_PRO_ATTN && RW * GL <= 2;
+    constexpr bool PRELOAD = !PANEL && PRO != VX_PRO_ATTN && RW * GL <= 4;
     const int ng = np * 8, k0 = p0 * 64;
     vx_pro_raw raw[PRELOAD ? RW : 1][PRELOAD ? GL : 1];
     if constexpr (PRELOAD) {
