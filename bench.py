@@ -23,7 +23,13 @@ its sources by oracle/Makefile) on this host's cores: single-token forwards
 of same-shape models at context 2048, combined with the acceptance trace of
 the GPU run (the reference verifies one token per forward).
 
-Usage: python bench.py [--gpus 1] [--steps 3] [--warmup 1] [--mode spec|gemm]
+--mode gemm: the verify GEMMs of this workload in isolation.  --mode
+configs: the isolated Q4_0/Q8_0 GEMMs at M = 1, 5, 9 (4096x4096, 11008x4096,
+4096x11008) and single verify steps of a 22L d2048 model at 512 positions
+(k=4, greedy) and of a 28L d3584 V152064 model at 8192 positions (k=8, T=1),
+each beside the reference's x86 build.
+
+Usage: python bench.py [--gpus 1] [--steps 3] [--warmup 1] [--mode spec|gemm|configs]
 """
 import argparse
 import ctypes as C
@@ -76,18 +82,21 @@ def synth_model(N, P, shape, n_ctx, seed):
 # ---------------------------------------------------------------------------
 # CPU baseline: the reference engine (oracle/_ref) on same-shape GGUF files
 # ---------------------------------------------------------------------------
-def _gguf_stream(path, shape, rng):
+def _gguf_stream(path, shape, rng, emb_type=2):
     """Writes a random Q4_0 Llama GGUF of the given shape, streaming; one
     layer's random blocks are reused by every layer (timing does not depend
-    on the values)."""
+    on the values).  emb_type 8: Q8_0 token embedding and output matrix."""
     d, F, V, L = shape["n_embd"], shape["n_ff"], shape["n_vocab"], shape["n_layers"]
     kvd = shape["n_kv_heads"] * (d // shape["n_heads"])
 
-    def blocks(rows, cols):
+    def blocks(rows, cols, typ=2):
         nb = rows * cols // 32
-        b = np.empty((nb, 18), np.uint8)
+        bb = 18 if typ == 2 else 34
+        b = np.empty((nb, bb), np.uint8)
         b[:, :2] = (np.abs(rng.normal(0, 0.02, nb)).astype(np.float16)).view(np.uint8).reshape(nb, 2)
-        b[:, 2:] = rng.integers(0, 256, (nb, 16), dtype=np.uint8)
+        b[:, 2:] = rng.integers(0, 256, (nb, bb - 2), dtype=np.uint8)
+        if typ == 8:
+            b[:, 2:][b[:, 2:] == 128] = 129          # int8 in [-127, 127]
         return b.tobytes()
 
     layer = {"attn_q": blocks(d, d), "attn_k": blocks(kvd, d), "attn_v": blocks(kvd, d),
@@ -95,9 +104,9 @@ def _gguf_stream(path, shape, rng):
              "ffn_down": blocks(d, F)}
     dims = {"attn_q": (d, d), "attn_k": (d, kvd), "attn_v": (d, kvd), "attn_output": (d, d),
             "ffn_gate": (d, F), "ffn_up": (d, F), "ffn_down": (F, d)}
-    emb = blocks(V, d)
+    emb = blocks(V, d, emb_type)
     ones = np.ones(d, np.float32).tobytes()
-    tensors = [("token_embd.weight", 2, (d, V), emb)]
+    tensors = [("token_embd.weight", emb_type, (d, V), emb)]
     for l in range(L):
         tensors.append((f"blk.{l}.attn_norm.weight", 0, (d,), ones))
         for nm in ("attn_q", "attn_k", "attn_v", "attn_output"):
@@ -106,7 +115,7 @@ def _gguf_stream(path, shape, rng):
         for nm in ("ffn_gate", "ffn_up", "ffn_down"):
             tensors.append((f"blk.{l}.{nm}.weight", 2, dims[nm], layer[nm]))
     tensors.append(("output_norm.weight", 0, (d,), ones))
-    tensors.append(("output.weight", 2, (d, V), emb))
+    tensors.append(("output.weight", emb_type, (d, V), emb))
 
     def s(x):
         b = x.encode()
@@ -157,6 +166,17 @@ def _ref_forward_ms(N, R, path, n_tok, ctx):
         R.vx_model_destroy(mp)
 
 
+def _tmpdir(need):
+    import shutil
+    for cand in ("/dev/shm", tempfile.gettempdir(), HERE):
+        try:
+            if os.access(cand, os.W_OK) and shutil.disk_usage(cand).free > need:
+                return cand
+        except OSError:
+            pass
+    raise RuntimeError(f"no directory with {need / 1e9:.0f} GB free for the reference's GGUF files")
+
+
 def cpu_baseline(N, stats_emitted, stats_drafted, ctx, n_target=3, n_draft=8):
     if not N.ref_available("avx2"):
         return None
@@ -164,17 +184,7 @@ def cpu_baseline(N, stats_emitted, stats_drafted, ctx, n_target=3, n_draft=8):
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     R.vx_set_n_threads(threads)
     rng = np.random.default_rng(99)
-    import shutil
-    tmpdir = None
-    for cand in ("/dev/shm", tempfile.gettempdir(), HERE):
-        try:
-            if os.access(cand, os.W_OK) and shutil.disk_usage(cand).free > 6e9:
-                tmpdir = cand
-                break
-        except OSError:
-            pass
-    if tmpdir is None:
-        raise RuntimeError("no directory with 6 GB free for the reference's GGUF files")
+    tmpdir = _tmpdir(6e9)
     t_start = time.perf_counter()
     with tempfile.TemporaryDirectory(dir=tmpdir) as td:
         tp, dp = os.path.join(td, "target.gguf"), os.path.join(td, "draft.gguf")
@@ -320,6 +330,74 @@ def run_spec(args):
     print(json.dumps(line), flush=True)
 
 
+class _QMat(C.Structure):
+    _fields_ = [("type", C.c_int), ("n_rows", C.c_int), ("n_cols", C.c_int), ("n_pairs", C.c_int),
+                ("qs", C.c_void_p), ("d", C.c_void_p)]
+
+
+class _Pro(C.Structure):
+    _fields_ = [("kind", C.c_int), ("x", C.c_void_p), ("ldx", C.c_int), ("src", C.c_void_p),
+                ("ld_src", C.c_int), ("w", C.c_void_p), ("x_out", C.c_void_p), ("ld_xout", C.c_int),
+                ("ss", C.c_void_p), ("ss_in", C.c_void_p), ("ss_K", C.c_int), ("thr", C.c_float),
+                ("clear", C.c_void_p), ("n_clear", C.c_size_t), ("part", C.c_void_p), ("n_chunks", C.c_int),
+                ("n_heads", C.c_int), ("n_kv_heads", C.c_int), ("head_dim", C.c_int)]
+
+
+PRO_ROWS, PRO_RESID, PRO_SWIGLU = 1, 2, 3
+
+
+def _bind_gemm(N, P):
+    vp = C.c_void_p
+    L = N.bind_vxh(P)
+    L.vxh_qmat_alloc.argtypes = [vp, C.c_int, C.c_int, C.c_int]
+    L.vxh_synth_blocks.argtypes = [vp, C.c_int, C.c_int, C.c_int, C.c_uint64, C.c_float, vp]
+    L.vxh_qmat_set_rows.argtypes = [vp, vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, vp]
+    L.vxh_gemm_pro.argtypes = [vp, C.c_int, vp, vp, C.c_int, C.c_int, C.c_float, vp, vp, vp]
+    L.vxh_acc_store.argtypes = [vp, C.c_int, C.c_int, C.c_int, vp, C.c_int, vp, C.c_int, vp]
+    L.vxh_qmat_free.argtypes = [vp]
+    L.vxh_event_create.argtypes = [vp]
+    L.vxh_event_destroy.argtypes = [vp]
+    L.vxh_event_record.argtypes = [vp, vp]
+    L.vxh_event_elapsed_ms.argtypes = [vp, vp, vp]
+    L.vxh_copy.argtypes = [vp, vp, C.c_size_t, vp]
+    return L
+
+
+def _rotated_mats(N, L, qt, rows, cols, seed0=1000):
+    """Enough copies of a seeded random matrix (> 300 MB together) that a
+    loop over them streams from HBM, not from the 256 MB Infinity Cache."""
+    mat_bytes = rows * cols // 32 * (18 if qt == 2 else 34)
+    n_rot = max(2, int(np.ceil(300e6 / mat_bytes)))
+    mats = []
+    stage = N.DevBuf(L, nbytes=mat_bytes)
+    for i in range(n_rot):
+        q = _QMat()
+        assert L.vxh_qmat_alloc(C.byref(q), qt, rows, cols) == 0, L.vxh_last_error()
+        assert L.vxh_synth_blocks(stage.ptr, qt, rows, cols, seed0 + i, 0.02, None) == 0
+        assert L.vxh_qmat_set_rows(C.byref(q), stage.ptr, 1, rows, rows, 0, 0, None) == 0
+        mats.append(q)
+    stage.free()
+    return mats, mat_bytes
+
+
+def _time_loop(L, reps, body):
+    """Device time of reps passes of body() between two events on the
+    default stream, in ms."""
+    e0, e1 = C.c_void_p(), C.c_void_p()
+    L.vxh_event_create(C.byref(e0))
+    L.vxh_event_create(C.byref(e1))
+    L.vxh_device_sync()
+    L.vxh_event_record(e0, None)
+    for _ in range(reps):
+        body()
+    L.vxh_event_record(e1, None)
+    ms = C.c_float()
+    assert L.vxh_event_elapsed_ms(e0, e1, C.byref(ms)) == 0, L.vxh_last_error()
+    L.vxh_event_destroy(e0)
+    L.vxh_event_destroy(e1)
+    return ms.value
+
+
 def run_gemm(args):
     """Isolated verify GEMM kernels at M = k+1 on the 7B shapes, each with the
     panel prologue the verify forward gives it (vxh_gemm_pro: residual add +
@@ -328,36 +406,14 @@ def run_gemm(args):
     over > 300 MB so the Infinity Cache does not serve them."""
     N, P = load_product()
     import ctypes as CC
-    vp = CC.c_void_p
-    L = N.bind_vxh(P)
-    L.vxh_qmat_alloc.argtypes = [vp, CC.c_int, CC.c_int, CC.c_int]
-    L.vxh_synth_blocks.argtypes = [vp, CC.c_int, CC.c_int, CC.c_int, CC.c_uint64, CC.c_float, vp]
-    L.vxh_qmat_set_rows.argtypes = [vp, vp, CC.c_int, CC.c_int, CC.c_int, CC.c_int, CC.c_int, vp]
-    L.vxh_gemm_pro.argtypes = [vp, CC.c_int, vp, vp, CC.c_int, CC.c_int, CC.c_float, vp, vp, vp]
-    L.vxh_qmat_free.argtypes = [vp]
-    L.vxh_event_create.argtypes = [vp]
-    L.vxh_event_record.argtypes = [vp, vp]
-    L.vxh_event_elapsed_ms.argtypes = [vp, vp, vp]
-
-    class QMat(CC.Structure):
-        _fields_ = [("type", CC.c_int), ("n_rows", CC.c_int), ("n_cols", CC.c_int), ("n_pairs", CC.c_int),
-                    ("qs", vp), ("d", vp)]
-
-    class Pro(CC.Structure):
-        _fields_ = [("kind", CC.c_int), ("x", vp), ("ldx", CC.c_int), ("src", vp), ("ld_src", CC.c_int),
-                    ("w", vp), ("x_out", vp), ("ld_xout", CC.c_int), ("ss", vp), ("ss_in", vp),
-                    ("ss_K", CC.c_int), ("thr", CC.c_float), ("clear", vp), ("n_clear", CC.c_size_t),
-                    ("part", vp), ("n_chunks", CC.c_int), ("n_heads", CC.c_int), ("n_kv_heads", CC.c_int),
-                    ("head_dim", CC.c_int)]
-    PRO_ROWS, PRO_RESID, PRO_SWIGLU = 1, 2, 3
-
+    L = _bind_gemm(N, P)
+    QMat, Pro = _QMat, _Pro
     M = args.k + 1
     results = []
     # calibration for rocprofv3 byte counters: a device-to-device copy of a
     # known size (FETCH_SIZE and WRITE_SIZE of that copy should read 256 MiB)
     cal_bytes = 256 << 20
     ca, cb = N.DevBuf(L, nbytes=cal_bytes), N.DevBuf(L, nbytes=cal_bytes)
-    L.vxh_copy.argtypes = [vp, vp, CC.c_size_t, vp]
     for _ in range(3):
         assert L.vxh_copy(cb.ptr, ca.ptr, cal_bytes, None) == 0
     L.vxh_device_sync()
@@ -369,18 +425,7 @@ def run_gemm(args):
     rng = np.random.default_rng(1)
     for rows, cols, qt in ((4096, 4096, 2), (12288, 4096, 2), (4096, 11008, 2), (22016, 4096, 2),
                            (32000, 4096, 2), (11008, 4096, 8), (4096, 11008, 8)):
-        bpw = 18 if qt == 2 else 34
-        mat_bytes = rows * cols // 32 * bpw
-        n_rot = max(2, int(np.ceil(300e6 / mat_bytes)))
-        mats = []
-        stage = N.DevBuf(L, nbytes=mat_bytes)
-        for i in range(n_rot):
-            q = QMat()
-            assert L.vxh_qmat_alloc(CC.byref(q), qt, rows, cols) == 0, L.vxh_last_error()
-            assert L.vxh_synth_blocks(stage.ptr, qt, rows, cols, 1000 + i, 0.02, None) == 0
-            assert L.vxh_qmat_set_rows(CC.byref(q), stage.ptr, 1, rows, rows, 0, 0, None) == 0
-            mats.append(q)
-        stage.free()
+        mats, mat_bytes = _rotated_mats(N, L, qt, rows, cols)
         kind = kinds[(rows, cols)]
         ld_src = (cols + 15) // 16 * 32 if kind == PRO_SWIGLU else cols
         bufs = [N.DevBuf(L, rng.normal(0, 1, (M, cols)).astype(np.float32)),     # x
@@ -397,25 +442,19 @@ def run_gemm(args):
         if kind == PRO_SWIGLU:
             pro.src, pro.ld_src, pro.ss_in, pro.ss_K, pro.thr = bufs[1].ptr, ld_src, bufs[5].ptr, 4096, 0.01
         acc = N.DevBuf(L, np.zeros(M * rows, np.float64))
-        e0, e1 = vp(), vp()
-        L.vxh_event_create(CC.byref(e0))
-        L.vxh_event_create(CC.byref(e1))
 
         def launch(q):
             return L.vxh_gemm_pro(CC.byref(q), M, CC.byref(pro), acc.ptr, rows, rows, 1.0, None, None, None)
         for q in mats:
             assert launch(q) == 0, L.vxh_last_error()
         reps = args.steps * 10
-        L.vxh_device_sync()
-        L.vxh_event_record(e0, None)
-        for r in range(reps):
+
+        def one_pass():
             for q in mats:
                 launch(q)
-        L.vxh_event_record(e1, None)
-        ms = CC.c_float()
-        L.vxh_event_elapsed_ms(e0, e1, CC.byref(ms))
+        ms = _time_loop(L, reps, one_pass)
         n = reps * len(mats)
-        avg_us = 1e3 * ms.value / n
+        avg_us = 1e3 * ms / n
         alg = mat_bytes + 4 * M * cols + 4 * M * rows
         gbs = alg / (avg_us * 1e-6) / 1e9
         results.append({"shape": f"{'Q4_0' if qt == 2 else 'Q8_0'} {rows}x{cols} M={M}",
@@ -430,6 +469,197 @@ def run_gemm(args):
     print(json.dumps({"mode": "gemm", "M": M, "results": results}), flush=True)
 
 
+# ---------------------------------------------------------------------------
+# the other benchmark configurations: isolated GEMMs and single verify steps
+# ---------------------------------------------------------------------------
+C3_SHAPE = dict(n_layers=22, n_heads=32, n_kv_heads=4, n_embd=2048, n_ff=5632, n_vocab=32000)
+C5_SHAPE = dict(n_layers=28, n_heads=28, n_kv_heads=4, n_embd=3584, n_ff=18944, n_vocab=152064)
+
+
+def _cpu_gemv_ms(N, R, qt, rows, cols, reps=3):
+    """The reference's matrix-vector product for one activation row
+    (src/model.c:203-241 on its x86 build): vx_gemv_q4_0_avx2 for Q4_0; for
+    Q8_0 the whole matrix is dequantised (vx_dequantize_row_q8_0) and
+    vx_gemv_f32_avx2 runs on it, every call.  Median of reps, in ms."""
+    rng = np.random.default_rng(rows + cols + qt)
+    W = N.rand_q4_0(rng, rows, cols) if qt == 2 else N.rand_q8_0(rng, rows, cols)
+    x = np.zeros(cols + 8, np.float32)
+    x[:cols] = rng.normal(0, 1, cols)
+    y = np.zeros(rows, np.float32)
+    tmp = np.zeros(rows * cols, np.float32) if qt == 8 else None
+    times = []
+    for _ in range(reps + 1):
+        t0 = time.perf_counter()
+        if qt == 2:
+            R.vx_gemv_q4_0_avx2(N._ptr(W), x, y, rows, cols)
+        else:
+            R.vx_dequantize_row_q8_0(N._ptr(W), tmp, rows * cols)
+            R.vx_gemv_f32_avx2(y, tmp, x, rows, cols)
+        times.append(time.perf_counter() - t0)
+    return 1e3 * float(np.median(times[1:]))
+
+
+def _configs_gemm(N, P, L, args, R, threads):
+    """C1 / C2: Y[M][rows] = X[M][cols] . W^T from device-resident fp32 rows,
+    W rotated over > 300 MB.  gemm_us: the GEMM kernel alone (vxh_gemm_pro,
+    panel built from the fp32 rows in its prologue, fp64 accumulator);
+    op_us: GEMM + the store kernel that rounds the accumulator to the fp32
+    result and clears it (vxh_acc_store)."""
+    cases = [("C1", 4096, 4096, 2, 5)] + [
+        ("C2", r, c, t, m) for (r, c) in ((11008, 4096), (4096, 11008)) for t in (2, 8) for m in (1, 5, 9)]
+    out = []
+    cpu_cache = {}
+    rng = np.random.default_rng(5)
+    for cfg, rows, cols, qt, M in cases:
+        mats, mat_bytes = _rotated_mats(N, L, qt, rows, cols)
+        x = N.DevBuf(L, rng.normal(0, 1, (M, cols)).astype(np.float32))
+        y = N.DevBuf(L, nbytes=4 * M * rows)
+        acc = N.DevBuf(L, np.zeros(M * rows, np.float64))
+        pro = _Pro(kind=PRO_ROWS, x=x.ptr, ldx=cols)
+
+        def gemm(q):
+            return L.vxh_gemm_pro(C.byref(q), M, C.byref(pro), acc.ptr, rows, rows, 1.0, None, None, None)
+
+        def store():
+            return L.vxh_acc_store(acc.ptr, rows, M, rows, y.ptr, rows, None, 0, None)
+        for q in mats:
+            assert gemm(q) == 0 and store() == 0, L.vxh_last_error()
+        reps = max(10, args.steps * 10)
+
+        def p_gemm():
+            for q in mats:
+                gemm(q)
+
+        def p_op():
+            for q in mats:
+                gemm(q)
+                store()
+        n = reps * len(mats)
+        g_us = 1e3 * _time_loop(L, reps, p_gemm) / n
+        store()
+        o_us = 1e3 * _time_loop(L, reps, p_op) / n
+        alg = mat_bytes + 4 * M * cols + 4 * M * rows
+        gbs = alg / (g_us * 1e-6) / 1e9
+        r = {"config": cfg, "shape": f"{'Q4_0' if qt == 2 else 'Q8_0'} {rows}x{cols}", "M": M,
+             "gemm_us": round(g_us, 2), "op_us": round(o_us, 2), "GB/s": round(gbs, 1),
+             "frac": round(gbs / PEAK_HBM_GBS, 4), "bytes": alg}
+        if R is not None:
+            key = (qt, rows, cols)
+            if key not in cpu_cache:
+                cpu_cache[key] = _cpu_gemv_ms(N, R, qt, rows, cols)
+            r["cpu_ref_us"] = round(1e3 * M * cpu_cache[key], 1)
+            r["gpu_vs_cpu"] = round(1e3 * M * cpu_cache[key] / o_us, 1)
+        log(json.dumps(r))
+        out.append(r)
+        for b in (x, y, acc):
+            b.free()
+        for q in mats:
+            L.vxh_qmat_free(C.byref(q))
+    return out
+
+
+def _configs_verify(N, P, L, name, shape, ctx, k, T, emb_type, reps, R, threads):
+    """One verify step of k drafts against ctx prefilled positions: the
+    target forward of k+1 tokens through the public entry point
+    (vx_model_verify, all k+1 logit rows copied to the host), and the
+    acceptance kernels on those logits (vxh_row_stats + vxh_accept; greedy
+    at T = 0, else sampled with seeded uniforms against random draft logits
+    whose nucleus descriptors vxh_sample wrote).  Medians over reps steps,
+    each rolled back to ctx with vx_model_kv_truncate."""
+    V = shape["n_vocab"]
+    cfg = N.VxModelConfig()
+    for kk, v in shape.items():
+        setattr(cfg, kk, v)
+    cfg.n_ctx = ctx + 16
+    cfg.rope_theta = 10000.0
+    spec = N.VxSynthSpec(seed=77, std=0.02, matrix_type=2, embd_type=emb_type, output_type=emb_type)
+    mp = C.POINTER(N.VxModelDev)()
+    t0 = time.perf_counter()
+    if P.vx_model_create_synthetic(C.byref(cfg), C.byref(spec), C.byref(mp)) != 0:
+        sys.exit("bench.py: model creation failed: " + N.product_error())
+    rng = np.random.default_rng(11)
+    lg = np.zeros(V, np.float32)
+    if P.vx_model_forward(mp, rng.integers(0, V, ctx).astype(np.int32), ctx, lg) != 0:
+        sys.exit("bench.py: prefill failed: " + N.product_error())
+    log(f"{name}: model + prefill of {ctx} positions {time.perf_counter() - t0:.1f} s")
+    logits = np.zeros((k + 1, V), np.float32)
+    times = []
+    for i in range(reps + 2):
+        toks = rng.integers(0, V, k + 1).astype(np.int32)
+        t0 = time.perf_counter()
+        if P.vx_model_verify(mp, toks, k + 1, logits) != 0:
+            sys.exit("bench.py: verify failed: " + N.product_error())
+        times.append(time.perf_counter() - t0)
+        P.vx_model_kv_truncate(mp, ctx)
+    fwd_ms = 1e3 * float(np.median(times[2:]))
+    P.vx_model_destroy(mp)
+    # acceptance kernels on the last verify's logits
+    dL = N.DevBuf(L, logits)
+    D = rng.normal(0, 2.0, (k, V)).astype(np.float32)
+    dD = N.DevBuf(L, D)
+    dstats = N.DevBuf(L, nbytes=4 * 3 * (k + 1))
+    dnuc = N.DevBuf(L, nbytes=4 * 8 * k)
+    ddr = N.DevBuf(L, toks[1:].copy())
+    du = N.DevBuf(L, rng.random(k + 1).astype(np.float32))
+    dtok = N.DevBuf(L, nbytes=4)
+    dout = N.DevBuf(L, nbytes=4 * (k + 3))
+    for j in range(k):
+        assert L.vxh_sample(C.c_void_p(dD.ptr.value + 4 * j * V), V, T, 1.0, du.ptr, dtok.ptr,
+                            C.c_void_p(dnuc.ptr.value + 32 * j), None) == 0, L.vxh_last_error()
+
+    def accept():
+        L.vxh_row_stats(dL.ptr, V, k + 1, V, T, dstats.ptr, None)
+        L.vxh_accept(dL.ptr, V, V, dstats.ptr, dD.ptr, V, V, dnuc.ptr, ddr.ptr, k, T, du.ptr, dout.ptr, None)
+    accept()
+    acc_ms = _time_loop(L, 50, accept) / 50
+    res = dout.get(np.int32, k + 3)
+    for b in (dL, dD, dstats, dnuc, ddr, du, dtok, dout):
+        b.free()
+    r = {"config": name,
+         "workload": (f"{shape['n_layers']}L d{shape['n_embd']} {shape['n_heads']}/{shape['n_kv_heads']} heads "
+                      f"FFN{shape['n_ff']} V{V} Q4_0 (embedding/output {'Q8_0' if emb_type == 8 else 'Q4_0'}), "
+                      f"{ctx} prefilled positions (attention cap 4096), k={k}, "
+                      f"{'greedy' if T <= 0 else f'sampled T={T}'}"),
+         "verify_forward_ms": round(fwd_ms, 3), "accept_ms": round(acc_ms, 4),
+         "verify_step_ms": round(fwd_ms + acc_ms, 3),
+         "logits_to_host_bytes": 4 * (k + 1) * V, "accepted_last": int(res[1])}
+    if R is not None:
+        try:
+            with tempfile.TemporaryDirectory(dir=_tmpdir(8e9)) as td:
+                path = os.path.join(td, "m.gguf")
+                t0 = time.perf_counter()
+                _gguf_stream(path, shape, np.random.default_rng(98), emb_type)
+                t_tok = _ref_forward_ms(N, R, path, 2, ctx)
+            r["cpu_ref_ms"] = round((k + 1) * t_tok, 1)
+            r["cpu_ref_sample"] = (f"reference x86 build, {threads} threads: median of 2 single-token forwards at "
+                                   f"cache position {ctx} ({t_tok:.1f} ms; the reference holds 4096 positions "
+                                   f"and clamps later ones to the last slot, attending 4096 either way), "
+                                   f"times k+1 = {k + 1} (it verifies one token per forward)")
+            r["gpu_vs_cpu"] = round((k + 1) * t_tok / (fwd_ms + acc_ms), 1)
+            log(f"{name}: reference forward {t_tok:.1f} ms ({time.perf_counter() - t0:.1f} s)")
+        except Exception as e:
+            log(f"{name}: cpu reference failed: {e!r}")
+    log(json.dumps(r))
+    return r
+
+
+def run_configs(args):
+    """C1/C2 GEMMs and C3/C5 verify steps on one GPU, with the reference's x86
+    build timed beside them; one JSON line (not the headline metric)."""
+    N, P = load_product()
+    L = _bind_gemm(N, P)
+    R, threads = None, 0
+    if not args.no_cpu_baseline and N.ref_available("avx2"):
+        R = N.ref("avx2")
+        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        R.vx_set_n_threads(threads)
+    gemms = _configs_gemm(N, P, L, args, R, threads)
+    c3 = _configs_verify(N, P, L, "C3", C3_SHAPE, 512, 4, 0.0, 2, 20, R, threads)
+    c5 = _configs_verify(N, P, L, "C5", C5_SHAPE, 8192, 8, 1.0, 8, 10, R, threads)
+    print(json.dumps({"mode": "configs", "cpu_threads": threads, "gemm": gemms, "verify": [c3, c5]}),
+          flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -438,7 +668,7 @@ def main():
     ap.add_argument("--tokens", type=int, default=256)
     ap.add_argument("--prompt", type=int, default=2048)
     ap.add_argument("--k", type=int, default=8)
-    ap.add_argument("--mode", choices=["spec", "gemm"], default="spec")
+    ap.add_argument("--mode", choices=["spec", "gemm", "configs"], default="spec")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--prof-every", type=int, default=7,
                     help="time every n-th verify GEMM of each class with kernel events")
@@ -450,6 +680,8 @@ def main():
         sys.exit(2)
     if args.mode == "gemm":
         run_gemm(args)
+    elif args.mode == "configs":
+        run_configs(args)
     else:
         run_spec(args)
 
