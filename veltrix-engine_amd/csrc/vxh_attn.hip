@@ -34,22 +34,19 @@ __global__ void vx_rope_kv_kernel(double *__restrict__ qkv, int ld_qkv, int M, i
         int i = (el % hd) / 2;               // pair index within the head
         double2 ab = *(const double2 *)(row + e);
         *(double2 *)(row + e) = make_double2(0.0, 0.0);
-        float a = (float)ab.x * rin, b = (float)ab.y * rin;
         const float *bias = isq ? bq : bk;
-        if (bias) { a += bias[el]; b += bias[el + 1]; }
+        const float a = vx_norm_bias(ab.x, rin, bias, el), b = vx_norm_bias(ab.y, rin, bias, el + 1);
         float c = cs[(size_t)rope_pos * half + i], s = sn[(size_t)rope_pos * half + i];
-        float o0 = a * c - b * s;
-        float o1 = a * s + b * c;
+        const float2 o = vx_rope_rot(a, b, c, s);
         if (isq) {
-            *(float2 *)(q_out + (size_t)m * qd + el) = make_float2(o0, o1);
+            *(float2 *)(q_out + (size_t)m * qd + el) = o;
         } else {
-            *(float2 *)(kc + (size_t)pos * kvd + el) = make_float2(o0, o1);
+            *(float2 *)(kc + (size_t)pos * kvd + el) = o;
         }
     } else {
         int el = r - (qd + kvd) / 2;
-        float v = (float)row[qd + kvd + el] * rin;
+        const float v = vx_norm_bias(row[qd + kvd + el], rin, bv, el);
         row[qd + kvd + el] = 0.0;
-        if (bv) v += bv[el];
         vc[(size_t)pos * kvd + el] = v;
     }
 }
@@ -118,17 +115,13 @@ __device__ __forceinline__ float4 vx_qkv4(const vx_qkv_args &a, int m, int col, 
     const float rin = a.ss ? vx_rms_inv((float)a.ss[m], a.ss_K) : 1.0f;
     const double *r = a.qkv + (size_t)m * a.ld + col;
     const double2 p0 = *(const double2 *)r, p1 = *(const double2 *)(r + 2);
-    float x0 = (float)p0.x * rin, x1 = (float)p0.y * rin, x2 = (float)p1.x * rin, x3 = (float)p1.y * rin;
-    if (bias) {
-        x0 += bias[el];
-        x1 += bias[el + 1];
-        x2 += bias[el + 2];
-        x3 += bias[el + 3];
-    }
+    const float x0 = vx_norm_bias(p0.x, rin, bias, el), x1 = vx_norm_bias(p0.y, rin, bias, el + 1);
+    const float x2 = vx_norm_bias(p1.x, rin, bias, el + 2), x3 = vx_norm_bias(p1.y, rin, bias, el + 3);
     if (!rot) return make_float4(x0, x1, x2, x3);
     const float c0 = a.cs[(size_t)rp * half + i], s0 = a.sn[(size_t)rp * half + i];
     const float c1 = a.cs[(size_t)rp * half + i + 1], s1 = a.sn[(size_t)rp * half + i + 1];
-    return make_float4(x0 * c0 - x1 * s0, x0 * s0 + x1 * c0, x2 * c1 - x3 * s1, x2 * s1 + x3 * c1);
+    const float2 o0 = vx_rope_rot(x0, x1, c0, s0), o1 = vx_rope_rot(x2, x3, c1, s1);
+    return make_float4(o0.x, o0.y, o1.x, o1.y);
 }
 
 template <bool QKV>
@@ -262,6 +255,272 @@ __global__ __launch_bounds__(ATT_THREADS) void vx_attention_kernel(
         }
         *(float4 *)(pstat + (size_t)(q0 + ql) * ps + 4 + 4 * d4) = a;
     }
+}
+
+// fp32-MFMA variant for head_dim 64 and 128: one wavefront per (kv head,
+// group of <= 16 query vectors, chunk of ACH positions), no LDS.  Scores and
+// P.V run on v_mfma_f32_16x16x4_f32 (fp32 products and sums).  Lane l = n +
+// 16 r (n = l % 16, r = l / 16):
+//  * QK^T, per 16 positions and per (j, i): A = K[position n][16 j + 4 r + i],
+//    B = q[query n][16 j + 4 r + i] (scaled by 1/sqrt(hd)); the result holds
+//    score(position 4 r + i, query n) in item i of lane (n, r).
+//  * P.V, per step s and chain c: A = V[position 4 r + s][NV n + c], B = the
+//    probability in item s of lane (n, r); chain c accumulates output dims
+//    NV (4 r + i) + c of query n in item i, NV = hd / 16.
+// So every lane loads whole float4s: K rows 4 dims at a time, V rows NV dims.
+// The chunk's (max, sum, acc[hd]) per query go to the same partials as
+// vx_attention_kernel writes (the combine kernels read either).
+typedef float vx_f32x4 __attribute__((ext_vector_type(4)));
+
+// Rows of the q|k|v sums as the attention reads them: 4 consecutive elements
+// per load, RoPE'd as two adjacent pairs (rot) with the deferred RMSNorm and
+// the bias applied.  All loads of a batch are issued before the first use and
+// every address is valid (callers clamp), so a wavefront pays one round trip.
+template <int NB>
+__device__ __forceinline__ void vx_qkv4_batch(const vx_qkv_args &a, int row, const int col[NB],
+                                              const int el[NB], const int pr[NB], int rp, int half,
+                                              const float *bias, bool rot, float4 out[NB])
+{
+    const double *rs = a.qkv + (size_t)row * a.ld;
+    const double *ssp = a.ss ? a.ss + row : rs;     // any valid address when there is no norm
+    const float *bp = bias ? bias : a.cs;
+    const float *ct = a.cs + (size_t)rp * half, *st = a.sn + (size_t)rp * half;
+    double2 p0[NB], p1[NB];
+    float4 b4[NB];
+    float c0[NB], c1[NB], s0[NB], s1[NB];
+    const double ssv = *ssp;
+#pragma unroll
+    for (int u = 0; u < NB; u++) {
+        p0[u] = *(const double2 *)(rs + col[u]);
+        p1[u] = *(const double2 *)(rs + col[u] + 2);
+        b4[u] = *(const float4 *)(bp + (bias ? el[u] : 0));
+        if (rot) {
+            c0[u] = ct[pr[u]];
+            c1[u] = ct[pr[u] + 1];
+            s0[u] = st[pr[u]];
+            s1[u] = st[pr[u] + 1];
+        }
+    }
+    const float rin = a.ss ? vx_rms_inv((float)ssv, a.ss_K) : 1.0f;
+#pragma unroll
+    for (int u = 0; u < NB; u++) {
+        const float x0 = bias ? fmaf((float)p0[u].x, rin, b4[u].x) : (float)p0[u].x * rin;
+        const float x1 = bias ? fmaf((float)p0[u].y, rin, b4[u].y) : (float)p0[u].y * rin;
+        const float x2 = bias ? fmaf((float)p1[u].x, rin, b4[u].z) : (float)p1[u].x * rin;
+        const float x3 = bias ? fmaf((float)p1[u].y, rin, b4[u].w) : (float)p1[u].y * rin;
+        if (rot) {
+            const float2 o0 = vx_rope_rot(x0, x1, c0[u], s0[u]), o1 = vx_rope_rot(x2, x3, c1[u], s1[u]);
+            out[u] = make_float4(o0.x, o0.y, o1.x, o1.y);
+        } else {
+            out[u] = make_float4(x0, x1, x2, x3);
+        }
+    }
+}
+
+#define VX_ATT_MFMA_MAX_M 16   // rows of a forward the QKV variant takes
+
+// v where ok, else zeros (per component: a select of whole float4 array
+// elements becomes a select of their addresses and puts the array in scratch)
+__device__ __forceinline__ float4 vx_keep4(bool ok, float4 v)
+{
+    return make_float4(ok ? v.x : 0.0f, ok ? v.y : 0.0f, ok ? v.z : 0.0f, ok ? v.w : 0.0f);
+}
+
+template <bool QKV, int HD>
+__global__ __launch_bounds__(ATT_THREADS) void vx_attention_mfma_kernel(
+    const float *__restrict__ q, int M, int n_past, int n_ctx, int n_heads, int n_kv, int cap,
+    float *__restrict__ kc, float *__restrict__ vc, int n_chunks, int n_chunks_w, int n_qg,
+    float *__restrict__ part, vx_qkv_args qa)
+{
+    constexpr int NJ = HD / 16;      // K float4 per lane per 16 positions; also P.V chains
+    constexpr int NV = HD / 16;      // V floats per lane per step
+    constexpr int NV4 = NV / 4;
+    static_assert(HD == 64 || HD == 128, "head_dim 64 or 128");
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n = lane & 15, r = lane >> 4;
+    const int ncg = (n_chunks_w + 3) / 4;
+    const int g = blockIdx.x / (n_qg * ncg);
+    const int qg = (blockIdx.x / ncg) % n_qg;
+    const int ch = (blockIdx.x % ncg) * 4 + wave;
+    if (!QKV && ch >= n_chunks_w) return;   // QKV: after the workgroup barrier below
+    const bool attend = ch < n_chunks;
+    const int G = n_heads / n_kv, QM = G * M;
+    const int kvd = n_kv * HD, qd = n_heads * HD, half = HD / 2;
+    const int t0 = ch * ACH;
+
+    // K rows of positions t0 + 16 pg + n (dims 16 j + 4 r .. + 3) and V rows
+    // of positions t0 + 16 pg + 4 r + s (dims NV n .. + NV - 1) from the cache;
+    // positions past the cache end read as zeros
+    float4 kr[2][NJ], vr[2][4][NV4];
+#pragma unroll
+    for (int pg = 0; pg < 2; pg++) {
+        const int pos = t0 + 16 * pg + n;
+        const size_t off = (size_t)min(pos, n_ctx - 1) * kvd + g * HD + 4 * r;
+#pragma unroll
+        for (int j = 0; j < NJ; j++) kr[pg][j] = *(const float4 *)(kc + off + 16 * j);
+#pragma unroll
+        for (int st = 0; st < 4; st++) {
+            const int pv = t0 + 16 * pg + 4 * r + st;
+            const size_t ov = (size_t)min(pv, n_ctx - 1) * kvd + g * HD + NV * n;
+#pragma unroll
+            for (int u = 0; u < NV4; u++) vr[pg][st][u] = *(const float4 *)(vc + ov + 4 * u);
+        }
+    }
+
+    // query n of this group: q vector (hl, m), its causal length cs
+    const int qi = qg * 16 + n;
+    const bool qok = qi < QM;
+    const int hl = qok ? qi / M : 0, m = qok ? qi % M : 0;
+    const int head = g * G + hl;
+    const int qpos = n_past + m < n_ctx ? n_past + m : n_ctx - 1;
+    int cs = qpos + 1;
+    if (cap > 0 && cs > cap) cs = cap;
+    if (!qok) cs = 0;
+    const float scale = 1.0f / sqrtf((float)HD);
+    float4 qv[NJ];
+    if constexpr (QKV) {
+        int col[NJ], pr[NJ];
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            col[j] = head * HD + 16 * j + 4 * r;
+            pr[j] = 8 * j + 2 * r;
+        }
+        vx_qkv4_batch<NJ>(qa, m, col, col, pr, n_past + m, half, qa.bq, true, qv);
+    } else {
+        const float *qr = q + (size_t)m * qd + head * HD + 4 * r;
+#pragma unroll
+        for (int j = 0; j < NJ; j++) qv[j] = *(const float4 *)(qr + 16 * j);
+    }
+#pragma unroll
+    for (int j = 0; j < NJ; j++)
+        qv[j] = vx_keep4(qok, make_float4(qv[j].x * scale, qv[j].y * scale, qv[j].z * scale, qv[j].w * scale));
+#pragma unroll
+    for (int pg = 0; pg < 2; pg++) {
+        const bool ok = t0 + 16 * pg + n < n_ctx;
+#pragma unroll
+        for (int j = 0; j < NJ; j++) kr[pg][j] = vx_keep4(ok, kr[pg][j]);
+#pragma unroll
+        for (int st = 0; st < 4; st++) {
+            const bool okv = t0 + 16 * pg + 4 * r + st < n_ctx;
+#pragma unroll
+            for (int u = 0; u < NV4; u++) vr[pg][st][u] = vx_keep4(okv, vr[pg][st][u]);
+        }
+    }
+
+    // QKV: this forward's own k/v rows (at min(n_past + m, n_ctx - 1); only
+    // a one-row forward is clamped) come from the sums.  A workgroup with such
+    // a row in one of its chunks derives head g's new rows once into LDS
+    // (query group 0 also stores them into the cache); its wavefronts then
+    // take those positions from LDS.
+    if constexpr (QKV) {
+        __shared__ float4 s_new[VX_ATT_MFMA_MAX_M * 2 * (HD / 4)];   // [row][k, v][d4]
+        const int lo = n_past < n_ctx ? n_past : n_ctx - 1;
+        const int hi = min(n_past + M - 1, n_ctx - 1);
+        const int c0 = (blockIdx.x % ncg) * 4 * ACH;
+        if (hi >= c0 && lo < c0 + 4 * ACH) {          // uniform over the workgroup
+            for (int it = threadIdx.x; it < M * 2 * (HD / 4); it += ATT_THREADS) {
+                const int d4 = it % (HD / 4), kind = (it / (HD / 4)) % 2, mr = it / (HD / 2);
+                int col[1] = {(kind ? qd + kvd : qd) + g * HD + 4 * d4}, el[1] = {g * HD + 4 * d4},
+                    pr[1] = {2 * d4};
+                float4 o[1];
+                vx_qkv4_batch<1>(qa, mr, col, el, pr, n_past + mr, half, kind ? qa.bv : qa.bk, kind == 0, o);
+                s_new[it] = o[0];
+                if (qg == 0) {
+                    const int pos = min(n_past + mr, n_ctx - 1);
+                    *(float4 *)((kind ? vc : kc) + (size_t)pos * kvd + el[0]) = o[0];
+                }
+            }
+            __syncthreads();
+            auto new_row = [&](int pos) -> int {
+                int mn = pos - n_past;
+                if (mn >= M || pos >= n_ctx) mn = -1;
+                if (mn < 0 && n_past >= n_ctx && pos == n_ctx - 1) mn = 0;
+                return mn;
+            };
+#pragma unroll
+            for (int pg = 0; pg < 2; pg++) {
+                const int mn = new_row(t0 + 16 * pg + n);
+                if (mn >= 0)
+#pragma unroll
+                    for (int j = 0; j < NJ; j++) kr[pg][j] = s_new[(mn * 2) * (HD / 4) + 4 * j + r];
+#pragma unroll
+                for (int st = 0; st < 4; st++) {
+                    const int mv = new_row(t0 + 16 * pg + 4 * r + st);
+                    if (mv >= 0)
+#pragma unroll
+                        for (int u = 0; u < NV4; u++)
+                            vr[pg][st][u] = s_new[(mv * 2 + 1) * (HD / 4) + (NV * n) / 4 + u];
+                }
+            }
+        }
+    }
+    if (ch >= n_chunks_w) return;
+    if (!attend) return;
+
+    // scores of the chunk's 32 positions: S[pg] item i = position 16 pg + 4 r + i
+    vx_f32x4 S[2];
+#pragma unroll
+    for (int pg = 0; pg < 2; pg++) {
+        S[pg] = vx_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            S[pg] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[pg][j].x, qv[j].x, S[pg], 0, 0, 0);
+            S[pg] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[pg][j].y, qv[j].y, S[pg], 0, 0, 0);
+            S[pg] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[pg][j].z, qv[j].z, S[pg], 0, 0, 0);
+            S[pg] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[pg][j].w, qv[j].w, S[pg], 0, 0, 0);
+        }
+    }
+    // chunk softmax statistics of query n (src/tensor.c:156-171 per chunk)
+    float sc[2][4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int pg = 0; pg < 2; pg++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int t = t0 + 16 * pg + 4 * r + i;
+            sc[pg][i] = t < cs ? S[pg][i] : -INFINITY;
+            mx = fmaxf(mx, sc[pg][i]);
+        }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    float p[2][4], l = 0.0f;
+#pragma unroll
+    for (int pg = 0; pg < 2; pg++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            p[pg][i] = mx == -INFINITY || sc[pg][i] == -INFINITY ? 0.0f : expf(sc[pg][i] - mx);
+            l += p[pg][i];
+        }
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+
+    // P.V
+    vx_f32x4 O[NJ];
+#pragma unroll
+    for (int c = 0; c < NJ; c++) O[c] = vx_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int pg = 0; pg < 2; pg++)
+#pragma unroll
+        for (int st = 0; st < 4; st++)
+#pragma unroll
+            for (int c = 0; c < NJ; c++) {
+                const float4 v4 = vr[pg][st][c / 4];
+                const float a = (c % 4) == 0 ? v4.x : (c % 4) == 1 ? v4.y : (c % 4) == 2 ? v4.z : v4.w;
+                O[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, p[pg][st], O[c], 0, 0, 0);
+            }
+    if (!qok) return;
+    const size_t ps = PART_STRIDE(HD);
+    float *pq = part + (((size_t)g * n_chunks + ch) * QM + qi) * ps;
+    if (r == 0) {
+        pq[0] = mx;
+        pq[1] = l;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int u = 0; u < NV4; u++)
+            *(float4 *)(pq + 4 + NV * (4 * r + i) + 4 * u) =
+                make_float4(O[4 * u][i], O[4 * u + 1][i], O[4 * u + 2][i], O[4 * u + 3][i]);
 }
 
 // One workgroup per (row m, head): merge the chunks' partial results with
@@ -474,7 +733,28 @@ static int vx_attention_run(const float *q, const vx_qkv_args *qa, long n_clr, i
     size_t lds = vx_attn_lds(qpg, head_dim);
     vx_qkv_args none;
     memset(&none, 0, sizeof(none));
-    if (qa)
+    if ((head_dim == 64 || head_dim == 128) && (!qa || M <= VX_ATT_MFMA_MAX_M)) {
+        // fp32-MFMA kernel: 4 chunks per workgroup, one per wavefront
+        const int nqg = (QM + 15) / 16, ncg = (n_chunks_w + 3) / 4;
+        const int grid = n_kv_heads * nqg * ncg;
+        const vx_qkv_args &A = qa ? *qa : none;
+        if (head_dim == 64 && qa)
+            vx_attention_mfma_kernel<true, 64><<<grid, ATT_THREADS, 0, vxh_hs(s)>>>(
+                nullptr, M, n_past, n_ctx, n_heads, n_kv_heads, cap, kc, vc, n_chunks, n_chunks_w, nqg,
+                ws->part, A);
+        else if (head_dim == 64)
+            vx_attention_mfma_kernel<false, 64><<<grid, ATT_THREADS, 0, vxh_hs(s)>>>(
+                q, M, n_past, n_ctx, n_heads, n_kv_heads, cap, kc, vc, n_chunks, n_chunks_w, nqg,
+                ws->part, A);
+        else if (qa)
+            vx_attention_mfma_kernel<true, 128><<<grid, ATT_THREADS, 0, vxh_hs(s)>>>(
+                nullptr, M, n_past, n_ctx, n_heads, n_kv_heads, cap, kc, vc, n_chunks, n_chunks_w, nqg,
+                ws->part, A);
+        else
+            vx_attention_mfma_kernel<false, 128><<<grid, ATT_THREADS, 0, vxh_hs(s)>>>(
+                q, M, n_past, n_ctx, n_heads, n_kv_heads, cap, kc, vc, n_chunks, n_chunks_w, nqg,
+                ws->part, A);
+    } else if (qa)
         vx_attention_kernel<true><<<n_kv_heads * n_chunks_w * n_qg, ATT_THREADS, lds, vxh_hs(s)>>>(
             nullptr, M, n_past, n_ctx, n_heads, n_kv_heads, head_dim, cap, kc, vc, n_chunks, n_chunks_w,
             qpg, n_qg, ws->part, *qa);

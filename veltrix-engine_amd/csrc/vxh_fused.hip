@@ -154,7 +154,7 @@ __device__ void vx_gemm_epilogue(const vx_gemm_args &a, int sg, uint4 *lds, int 
                             const int i = (el % e.hd) / 2;
                             const float c = e.cs[(size_t)rope_pos * half + i];
                             const float sn = e.sn[(size_t)rope_pos * half + i];
-                            o = (el & 1) ? xp * sn + x * c : x * c - xp * sn;
+                            o = (el & 1) ? vx_rope_rot(xp, x, c, sn).y : vx_rope_rot(x, xp, c, sn).x;
                         }
                         float *dst = region == 0 ? e.q_out + (size_t)m * qd + el
                                                  : (region == 1 ? e.kc : e.vc) + (size_t)pos * kvd + el;

@@ -62,6 +62,19 @@ __device__ __forceinline__ float vx_row_scale(float amax, float *rs_out)
     return ldexpf(1.0f, -e);
 }
 
+// Deferred RMSNorm and bias of one q|k|v sum, then the RoPE rotation of a
+// pair (src/tensor.c:249-270), written with explicit fmaf so that every
+// kernel that derives q/k rows rounds them the same way.
+__device__ __forceinline__ float vx_norm_bias(double x, float rin, const float *bias, int el)
+{
+    return bias ? fmaf((float)x, rin, bias[el]) : (float)x * rin;
+}
+
+__device__ __forceinline__ float2 vx_rope_rot(float a, float b, float c, float s)
+{
+    return make_float2(fmaf(a, c, -(b * s)), fmaf(a, s, b * c));
+}
+
 __device__ __forceinline__ float vx_wave_max64(float v)
 {
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
