@@ -264,10 +264,11 @@ __global__ __launch_bounds__(ATT_THREADS) void vx_attention_kernel(
 //  * QK^T, per 16 positions and per (j, i): A = K[position n][16 j + 4 r + i],
 //    B = q[query n][16 j + 4 r + i] (scaled by 1/sqrt(hd)); the result holds
 //    score(position 4 r + i, query n) in item i of lane (n, r).
-//  * P.V, per step s and chain c: A = V[position 4 r + s][NV n + c], B = the
-//    probability in item s of lane (n, r); chain c accumulates output dims
-//    NV (4 r + i) + c of query n in item i, NV = hd / 16.
-// So every lane loads whole float4s: K rows 4 dims at a time, V rows NV dims.
+//  * P.V, per step s and chain c = 4 u + e: A = V[position 4 r + s][64 u +
+//    4 n + e], B = the probability in item s of lane (n, r); chain c
+//    accumulates output dim 64 u + 4 (4 r + i) + e of query n in item i.
+// So every lane loads whole float4s: K rows 4 dims at a time (16 rows x 64 B
+// per load), V rows as 4 rows x 256 contiguous bytes per load.
 // The chunk's (max, sum, acc[hd]) per query go to the same partials as
 // vx_attention_kernel writes (the combine kernels read either).
 typedef float vx_f32x4 __attribute__((ext_vector_type(4)));
@@ -327,7 +328,7 @@ __device__ __forceinline__ float4 vx_keep4(bool ok, float4 v)
 }
 
 template <bool QKV, int HD>
-__global__ __launch_bounds__(ATT_THREADS) void vx_attention_mfma_kernel(
+__device__ __forceinline__ void vx_attention_mfma_body(
     const float *__restrict__ q, int M, int n_past, int n_ctx, int n_heads, int n_kv, int cap,
     float *__restrict__ kc, float *__restrict__ vc, int n_chunks, int n_chunks_w, int n_qg,
     float *__restrict__ part, vx_qkv_args qa)
@@ -349,7 +350,7 @@ __global__ __launch_bounds__(ATT_THREADS) void vx_attention_mfma_kernel(
     const int t0 = ch * ACH;
 
     // K rows of positions t0 + 16 pg + n (dims 16 j + 4 r .. + 3) and V rows
-    // of positions t0 + 16 pg + 4 r + s (dims NV n .. + NV - 1) from the cache;
+    // of positions t0 + 16 pg + 4 r + s (dims 64 u + 4 n .. + 3) from the cache;
     // positions past the cache end read as zeros
     float4 kr[2][NJ], vr[2][4][NV4];
 #pragma unroll
@@ -361,9 +362,9 @@ __global__ __launch_bounds__(ATT_THREADS) void vx_attention_mfma_kernel(
 #pragma unroll
         for (int st = 0; st < 4; st++) {
             const int pv = t0 + 16 * pg + 4 * r + st;
-            const size_t ov = (size_t)min(pv, n_ctx - 1) * kvd + g * HD + NV * n;
+            const size_t ov = (size_t)min(pv, n_ctx - 1) * kvd + g * HD + 4 * n;
 #pragma unroll
-            for (int u = 0; u < NV4; u++) vr[pg][st][u] = *(const float4 *)(vc + ov + 4 * u);
+            for (int u = 0; u < NV4; u++) vr[pg][st][u] = *(const float4 *)(vc + ov + 64 * u);
         }
     }
 
@@ -449,7 +450,7 @@ __global__ __launch_bounds__(ATT_THREADS) void vx_attention_mfma_kernel(
                     if (mv >= 0)
 #pragma unroll
                         for (int u = 0; u < NV4; u++)
-                            vr[pg][st][u] = s_new[(mv * 2 + 1) * (HD / 4) + (NV * n) / 4 + u];
+                            vr[pg][st][u] = s_new[(mv * 2 + 1) * (HD / 4) + n + 16 * u];
                 }
             }
         }
@@ -519,8 +520,31 @@ __global__ __launch_bounds__(ATT_THREADS) void vx_attention_mfma_kernel(
     for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int u = 0; u < NV4; u++)
-            *(float4 *)(pq + 4 + NV * (4 * r + i) + 4 * u) =
+            *(float4 *)(pq + 4 + 64 * u + 16 * r + 4 * i) =
                 make_float4(O[4 * u][i], O[4 * u + 1][i], O[4 * u + 2][i], O[4 * u + 3][i]);
+}
+
+// q rows given (the verify forward, after the RoPE kernel): 3 wavefronts per
+// SIMD fit the registers, so a 7B-shape layer's 2304 wavefronts run in one
+// round.  q|k|v sums (draft decode): the default register budget.
+template <int HD>
+__global__ __launch_bounds__(ATT_THREADS) __attribute__((amdgpu_waves_per_eu(3))) void vx_attention_mfma_kernel(
+    const float *__restrict__ q, int M, int n_past, int n_ctx, int n_heads, int n_kv, int cap,
+    float *__restrict__ kc, float *__restrict__ vc, int n_chunks, int n_chunks_w, int n_qg,
+    float *__restrict__ part, vx_qkv_args qa)
+{
+    vx_attention_mfma_body<false, HD>(q, M, n_past, n_ctx, n_heads, n_kv, cap, kc, vc, n_chunks, n_chunks_w,
+                                      n_qg, part, qa);
+}
+
+template <int HD>
+__global__ __launch_bounds__(ATT_THREADS) void vx_attention_mfma_qkv_kernel(
+    const float *__restrict__ q, int M, int n_past, int n_ctx, int n_heads, int n_kv, int cap,
+    float *__restrict__ kc, float *__restrict__ vc, int n_chunks, int n_chunks_w, int n_qg,
+    float *__restrict__ part, vx_qkv_args qa)
+{
+    vx_attention_mfma_body<true, HD>(q, M, n_past, n_ctx, n_heads, n_kv, cap, kc, vc, n_chunks, n_chunks_w,
+                                     n_qg, part, qa);
 }
 
 // One workgroup per (row m, head): merge the chunks' partial results with
@@ -739,19 +763,19 @@ static int vx_attention_run(const float *q, const vx_qkv_args *qa, long n_clr, i
         const int grid = n_kv_heads * nqg * ncg;
         const vx_qkv_args &A = qa ? *qa : none;
         if (head_dim == 64 && qa)
-            vx_attention_mfma_kernel<true, 64><<<grid, ATT_THREADS, 0, vxh_hs(s)>>>(
+            vx_attention_mfma_qkv_kernel<64><<<grid, ATT_THREADS, 0, vxh_hs(s)>>>(
                 nullptr, M, n_past, n_ctx, n_heads, n_kv_heads, cap, kc, vc, n_chunks, n_chunks_w, nqg,
                 ws->part, A);
         else if (head_dim == 64)
-            vx_attention_mfma_kernel<false, 64><<<grid, ATT_THREADS, 0, vxh_hs(s)>>>(
+            vx_attention_mfma_kernel<64><<<grid, ATT_THREADS, 0, vxh_hs(s)>>>(
                 q, M, n_past, n_ctx, n_heads, n_kv_heads, cap, kc, vc, n_chunks, n_chunks_w, nqg,
                 ws->part, A);
         else if (qa)
-            vx_attention_mfma_kernel<true, 128><<<grid, ATT_THREADS, 0, vxh_hs(s)>>>(
+            vx_attention_mfma_qkv_kernel<128><<<grid, ATT_THREADS, 0, vxh_hs(s)>>>(
                 nullptr, M, n_past, n_ctx, n_heads, n_kv_heads, cap, kc, vc, n_chunks, n_chunks_w, nqg,
                 ws->part, A);
         else
-            vx_attention_mfma_kernel<false, 128><<<grid, ATT_THREADS, 0, vxh_hs(s)>>>(
+            vx_attention_mfma_kernel<128><<<grid, ATT_THREADS, 0, vxh_hs(s)>>>(
                 q, M, n_past, n_ctx, n_heads, n_kv_heads, cap, kc, vc, n_chunks, n_chunks_w, nqg,
                 ws->part, A);
     } else if (qa)
