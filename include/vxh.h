@@ -369,6 +369,8 @@ int vxh_attention(const float *q, int M, int n_past, int n_ctx, int n_heads, int
  * the second combines the chunks and clears qkv.  A batch whose last row
  * reaches past n_ctx - 1 must be a single row (the reference's clamp keeps
  * one row at n_ctx - 1). */
+#define VXH_ATTN_QKV_FAST_ROWS 16   /* head_dim 64/128 batches up to this many rows take the
+                                      * fp32-MFMA kernel; larger ones a slower LDS kernel */
 int vxh_attention_qkv(double *qkv, int ld_qkv, const double *ss, int ss_K, const float *bq,
                       const float *bk, const float *bv, const float *cos_tab, const float *sin_tab,
                       int n_pos, int M, int n_past, int n_ctx, int n_heads, int n_kv_heads,

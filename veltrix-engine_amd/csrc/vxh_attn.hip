@@ -318,7 +318,48 @@ __device__ __forceinline__ void vx_qkv4_batch(const vx_qkv_args &a, int row, con
     }
 }
 
-#define VX_ATT_MFMA_MAX_M 16   // rows of a forward the QKV variant takes
+// vx_qkv4_batch for items of different rows, RoPE positions and biases.
+template <int NB>
+__device__ __forceinline__ void vx_qkv4_items(const vx_qkv_args &a, const int row[NB], const int col[NB],
+                                              const int el[NB], const int pr[NB], const int rp[NB],
+                                              const float *const bias[NB], const bool rot[NB], int half,
+                                              float4 out[NB])
+{
+    double2 p0[NB], p1[NB];
+    float4 b4[NB];
+    float c0[NB], c1[NB], s0[NB], s1[NB];
+    double ssv[NB];
+#pragma unroll
+    for (int u = 0; u < NB; u++) {
+        const double *rs = a.qkv + (size_t)row[u] * a.ld;
+        ssv[u] = *(a.ss ? a.ss + row[u] : rs);       // any valid address when there is no norm
+        p0[u] = *(const double2 *)(rs + col[u]);
+        p1[u] = *(const double2 *)(rs + col[u] + 2);
+        b4[u] = *(const float4 *)(bias[u] ? bias[u] + el[u] : a.cs);
+        const float *ct = a.cs + (size_t)rp[u] * half + pr[u], *st = a.sn + (size_t)rp[u] * half + pr[u];
+        c0[u] = ct[0];
+        c1[u] = ct[1];
+        s0[u] = st[0];
+        s1[u] = st[1];
+    }
+#pragma unroll
+    for (int u = 0; u < NB; u++) {
+        const float rin = a.ss ? vx_rms_inv((float)ssv[u], a.ss_K) : 1.0f;
+        const bool bb = bias[u] != nullptr;
+        const float x0 = bb ? fmaf((float)p0[u].x, rin, b4[u].x) : (float)p0[u].x * rin;
+        const float x1 = bb ? fmaf((float)p0[u].y, rin, b4[u].y) : (float)p0[u].y * rin;
+        const float x2 = bb ? fmaf((float)p1[u].x, rin, b4[u].z) : (float)p1[u].x * rin;
+        const float x3 = bb ? fmaf((float)p1[u].y, rin, b4[u].w) : (float)p1[u].y * rin;
+        if (rot[u]) {
+            const float2 o0 = vx_rope_rot(x0, x1, c0[u], s0[u]), o1 = vx_rope_rot(x2, x3, c1[u], s1[u]);
+            out[u] = make_float4(o0.x, o0.y, o1.x, o1.y);
+        } else {
+            out[u] = make_float4(x0, x1, x2, x3);
+        }
+    }
+}
+
+#define VX_ATT_MFMA_MAX_M VXH_ATTN_QKV_FAST_ROWS   // rows of a forward the QKV variant takes
 
 // v where ok, else zeros (per component: a select of whole float4 array
 // elements becomes a select of their addresses and puts the array in scratch)
@@ -379,22 +420,14 @@ __device__ __forceinline__ void vx_attention_mfma_body(
     if (!qok) cs = 0;
     const float scale = 1.0f / sqrtf((float)HD);
     float4 qv[NJ];
-    if constexpr (QKV) {
-        int col[NJ], pr[NJ];
-#pragma unroll
-        for (int j = 0; j < NJ; j++) {
-            col[j] = head * HD + 16 * j + 4 * r;
-            pr[j] = 8 * j + 2 * r;
-        }
-        vx_qkv4_batch<NJ>(qa, m, col, col, pr, n_past + m, half, qa.bq, true, qv);
-    } else {
+    if constexpr (!QKV) {
         const float *qr = q + (size_t)m * qd + head * HD + 4 * r;
 #pragma unroll
         for (int j = 0; j < NJ; j++) qv[j] = *(const float4 *)(qr + 16 * j);
-    }
 #pragma unroll
-    for (int j = 0; j < NJ; j++)
-        qv[j] = vx_keep4(qok, make_float4(qv[j].x * scale, qv[j].y * scale, qv[j].z * scale, qv[j].w * scale));
+        for (int j = 0; j < NJ; j++)
+            qv[j] = vx_keep4(qok, make_float4(qv[j].x * scale, qv[j].y * scale, qv[j].z * scale, qv[j].w * scale));
+    }
 #pragma unroll
     for (int pg = 0; pg < 2; pg++) {
         const bool ok = t0 + 16 * pg + n < n_ctx;
@@ -408,30 +441,82 @@ __device__ __forceinline__ void vx_attention_mfma_body(
         }
     }
 
-    // QKV: this forward's own k/v rows (at min(n_past + m, n_ctx - 1); only
-    // a one-row forward is clamped) come from the sums.  A workgroup with such
-    // a row in one of its chunks derives head g's new rows once into LDS
-    // (query group 0 also stores them into the cache); its wavefronts then
-    // take those positions from LDS.
+    // QKV: the workgroup derives its 16 q vectors (deferred RMSNorm, bias,
+    // RoPE, 1/sqrt(hd)) once into LDS, and -- when one of its chunks holds a
+    // row of this forward (at min(n_past + m, n_ctx - 1); only a one-row
+    // forward is clamped) -- head g's new k/v rows too (query group 0 also
+    // stores them into the cache); the wavefronts take them from LDS.
     if constexpr (QKV) {
-        __shared__ float4 s_new[VX_ATT_MFMA_MAX_M * 2 * (HD / 4)];   // [row][k, v][d4]
+        constexpr int Q4 = HD / 4, QS = Q4 + 1;                      // float4 per row, padded stride
+        __shared__ float4 s_q[16 * QS];
+        __shared__ float4 s_new[VX_ATT_MFMA_MAX_M * 2 * Q4];        // [row][k, v][d4]
+        constexpr int QI = 16 * Q4 / ATT_THREADS;                  // q items per thread (1 or 2)
+        {
+            int row[QI], col[QI], pr[QI], rp[QI];
+            bool ok[QI];
+            const float *bias[QI];
+            bool rot[QI];
+#pragma unroll
+            for (int u = 0; u < QI; u++) {
+                const int it = threadIdx.x + u * ATT_THREADS, qn = it / Q4, d4 = it % Q4;
+                const int qj = qg * 16 + qn;
+                ok[u] = qj < QM;
+                const int mj = ok[u] ? qj % M : 0, hj = ok[u] ? qj / M : 0;
+                row[u] = mj;
+                col[u] = (g * G + hj) * HD + 4 * d4;
+                pr[u] = 2 * d4;
+                rp[u] = n_past + mj;
+                bias[u] = qa.bq;
+                rot[u] = true;
+            }
+            float4 o[QI];
+            vx_qkv4_items<QI>(qa, row, col, col, pr, rp, bias, rot, half, o);
+#pragma unroll
+            for (int u = 0; u < QI; u++) {
+                const int it = threadIdx.x + u * ATT_THREADS;
+                s_q[(it / Q4) * QS + it % Q4] =
+                    vx_keep4(ok[u], make_float4(o[u].x * scale, o[u].y * scale, o[u].z * scale, o[u].w * scale));
+            }
+        }
         const int lo = n_past < n_ctx ? n_past : n_ctx - 1;
         const int hi = min(n_past + M - 1, n_ctx - 1);
         const int c0 = (blockIdx.x % ncg) * 4 * ACH;
-        if (hi >= c0 && lo < c0 + 4 * ACH) {          // uniform over the workgroup
-            for (int it = threadIdx.x; it < M * 2 * (HD / 4); it += ATT_THREADS) {
-                const int d4 = it % (HD / 4), kind = (it / (HD / 4)) % 2, mr = it / (HD / 2);
-                int col[1] = {(kind ? qd + kvd : qd) + g * HD + 4 * d4}, el[1] = {g * HD + 4 * d4},
-                    pr[1] = {2 * d4};
-                float4 o[1];
-                vx_qkv4_batch<1>(qa, mr, col, el, pr, n_past + mr, half, kind ? qa.bv : qa.bk, kind == 0, o);
-                s_new[it] = o[0];
-                if (qg == 0) {
-                    const int pos = min(n_past + mr, n_ctx - 1);
-                    *(float4 *)((kind ? vc : kc) + (size_t)pos * kvd + el[0]) = o[0];
+        const bool has_new = hi >= c0 && lo < c0 + 4 * ACH;          // uniform over the workgroup
+        if (has_new) {
+            for (int it0 = threadIdx.x; it0 < M * 2 * Q4; it0 += 2 * ATT_THREADS) {
+                int row[2], col[2], el[2], pr[2], rp[2];
+                const float *bias[2];
+                bool rot[2];
+#pragma unroll
+                for (int u = 0; u < 2; u++) {
+                    const int it = min(it0 + u * ATT_THREADS, M * 2 * Q4 - 1);
+                    const int d4 = it % Q4, kind = (it / Q4) % 2, mr = it / (2 * Q4);
+                    row[u] = mr;
+                    el[u] = g * HD + 4 * d4;
+                    col[u] = (kind ? qd + kvd : qd) + el[u];
+                    pr[u] = 2 * d4;
+                    rp[u] = n_past + mr;
+                    bias[u] = kind ? qa.bv : qa.bk;
+                    rot[u] = kind == 0;
+                }
+                float4 o[2];
+                vx_qkv4_items<2>(qa, row, col, el, pr, rp, bias, rot, half, o);
+#pragma unroll
+                for (int u = 0; u < 2; u++) {
+                    const int it = it0 + u * ATT_THREADS;
+                    if (it >= M * 2 * Q4) continue;
+                    s_new[it] = o[u];
+                    if (qg == 0) {
+                        const int kind = (it / Q4) % 2, pos = min(n_past + row[u], n_ctx - 1);
+                        *(float4 *)((kind ? vc : kc) + (size_t)pos * kvd + el[u]) = o[u];
+                    }
                 }
             }
-            __syncthreads();
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < NJ; j++) qv[j] = s_q[n * QS + 4 * j + r];
+        if (has_new) {
             auto new_row = [&](int pos) -> int {
                 int mn = pos - n_past;
                 if (mn >= M || pos >= n_ctx) mn = -1;
@@ -443,14 +528,13 @@ __device__ __forceinline__ void vx_attention_mfma_body(
                 const int mn = new_row(t0 + 16 * pg + n);
                 if (mn >= 0)
 #pragma unroll
-                    for (int j = 0; j < NJ; j++) kr[pg][j] = s_new[(mn * 2) * (HD / 4) + 4 * j + r];
+                    for (int j = 0; j < NJ; j++) kr[pg][j] = s_new[(mn * 2) * Q4 + 4 * j + r];
 #pragma unroll
                 for (int st = 0; st < 4; st++) {
                     const int mv = new_row(t0 + 16 * pg + 4 * r + st);
                     if (mv >= 0)
 #pragma unroll
-                        for (int u = 0; u < NV4; u++)
-                            vr[pg][st][u] = s_new[(mv * 2 + 1) * (HD / 4) + n + 16 * u];
+                        for (int u = 0; u < NV4; u++) vr[pg][st][u] = s_new[(mv * 2 + 1) * Q4 + n + 16 * u];
                 }
             }
         }
@@ -482,8 +566,7 @@ __device__ __forceinline__ void vx_attention_mfma_body(
             sc[pg][i] = t < cs ? S[pg][i] : -INFINITY;
             mx = fmaxf(mx, sc[pg][i]);
         }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = vx_max_x32(vx_max_x16(mx));
     float p[2][4], l = 0.0f;
 #pragma unroll
     for (int pg = 0; pg < 2; pg++)
@@ -492,8 +575,7 @@ __device__ __forceinline__ void vx_attention_mfma_body(
             p[pg][i] = mx == -INFINITY || sc[pg][i] == -INFINITY ? 0.0f : expf(sc[pg][i] - mx);
             l += p[pg][i];
         }
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
+    l = vx_sum_x32(vx_sum_x16(l));
 
     // P.V
     vx_f32x4 O[NJ];
@@ -567,7 +649,7 @@ __device__ void vx_att_row_panel(const float *att, int d, int M, int m, uint4 *p
     for (int c = 8 * threadIdx.x; c < d; c += 8 * CMB_THREADS)
         for (int k = 0; k < 8; k++)
             am = fmaxf(am, fabsf(att[c + k]));
-    for (int o = 32; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
+    am = vx_wave_max64(am);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = am;
     __syncthreads();
     if (threadIdx.x == 0) {

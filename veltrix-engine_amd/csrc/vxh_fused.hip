@@ -44,11 +44,7 @@ __device__ __forceinline__ void vx_chunk_scale(float amax, float *s_in, float *s
     *s_out = ldexpf(1.0f, ex - 14);
 }
 
-__device__ __forceinline__ float vx_wave_max(float v)
-{
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
+__device__ __forceinline__ float vx_wave_max(float v) { return vx_wave_max64(v); }
 
 __device__ __forceinline__ double vx_wave_sum_f64(double v)
 {

@@ -100,7 +100,7 @@ struct vx_row_args {
 
 __device__ __forceinline__ float vx_block_sum(float v, float *red)
 {
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    v = vx_wave_sum64(v);
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     if (lane == 0) red[w] = v;
     __syncthreads();
@@ -113,7 +113,7 @@ __device__ __forceinline__ float vx_block_sum(float v, float *red)
 
 __device__ __forceinline__ float vx_block_max(float v, float *red)
 {
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    v = vx_wave_max64(v);
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     if (lane == 0) red[w] = v;
     __syncthreads();

@@ -75,14 +75,57 @@ __device__ __forceinline__ float2 vx_rope_rot(float a, float b, float c, float s
     return make_float2(fmaf(a, c, -(b * s)), fmaf(a, s, b * c));
 }
 
+// Wavefront reductions in VALU: DPP within each row of 16 lanes (quad_perm
+// [1,0,3,2], [2,3,0,1], row_half_mirror, row_mirror), then the gfx950 lane
+// swaps for the lane ^ 16 and lane ^ 32 partners.  A swap of a register
+// with itself returns {own value, partner value} in some order, so max and
+// sum over the two results equal max/sum with the partner.  Every lane ends
+// with the result (as the __shfl_xor butterfly, without its six dependent
+// LDS-crossbar round trips).
+template <int CTRL>
+__device__ __forceinline__ float vx_dpp(float v)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float vx_max_x16(float v)
+{
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float vx_max_x32(float v)
+{
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float vx_sum_x16(float v)
+{
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ float vx_sum_x32(float v)
+{
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 __device__ __forceinline__ float vx_wave_max64(float v)
 {
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+    v = fmaxf(v, vx_dpp<0xB1>(v));
+    v = fmaxf(v, vx_dpp<0x4E>(v));
+    v = fmaxf(v, vx_dpp<0x141>(v));
+    v = fmaxf(v, vx_dpp<0x140>(v));
+    return vx_max_x32(vx_max_x16(v));
 }
 
 __device__ __forceinline__ float vx_wave_sum64(float v)
 {
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+    v += vx_dpp<0xB1>(v);
+    v += vx_dpp<0x4E>(v);
+    v += vx_dpp<0x141>(v);
+    v += vx_dpp<0x140>(v);
+    return vx_sum_x32(vx_sum_x16(v));
 }

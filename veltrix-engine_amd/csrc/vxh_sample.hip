@@ -21,7 +21,7 @@ __device__ __forceinline__ uint64_t vx_fixed32(float w)
 // --- workgroup reductions (SB threads, 16 waves) ----------------------------
 __device__ __forceinline__ float vx_wg_max(float v, float *red)
 {
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    v = vx_wave_max64(v);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
     float r = red[0];
@@ -32,7 +32,7 @@ __device__ __forceinline__ float vx_wg_max(float v, float *red)
 
 __device__ __forceinline__ float vx_wg_sum(float v, float *red)
 {
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    v = vx_wave_sum64(v);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
     float r = 0.0f;
@@ -63,13 +63,49 @@ __device__ __forceinline__ uint64_t vx_wg_sum_u64(uint64_t v, uint64_t *red)
 // NaN or all -inf) keeps that sentinel, which maps to index 0 -- the
 // reference's scan also stays on its first element -- so callers can always
 // index the row with the result.
-__device__ __forceinline__ int vx_wg_argmax(float v, int idx, float *redv, int *redi)
+// (v, idx) <- the better of itself and (ov, oi): larger value, lower index on ties
+__device__ __forceinline__ void vx_am_merge(float &v, int &idx, float ov, int oi)
 {
-    for (int o = 32; o > 0; o >>= 1) {
-        float ov = __shfl_xor(v, o, 64);
-        int oi = __shfl_xor(idx, o, 64);
-        if (ov > v || (ov == v && oi < idx)) { v = ov; idx = oi; }
+    if (ov > v || (ov == v && oi < idx)) { v = ov; idx = oi; }
+}
+
+template <int CTRL>
+__device__ __forceinline__ void vx_am_dpp(float &v, int &idx)
+{
+    const float ov = vx_dpp<CTRL>(v);
+    const int oi = __builtin_amdgcn_update_dpp(idx, idx, CTRL, 0xF, 0xF, false);
+    vx_am_merge(v, idx, ov, oi);
+}
+
+// wavefront argmax in VALU (the same DPP steps and lane swaps as vx_wave_max64)
+__device__ __forceinline__ void vx_wave_argmax64(float &v, int &idx)
+{
+    vx_am_dpp<0xB1>(v, idx);
+    vx_am_dpp<0x4E>(v, idx);
+    vx_am_dpp<0x141>(v, idx);
+    vx_am_dpp<0x140>(v, idx);
+    {
+        const auto rv = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        const auto ri = __builtin_amdgcn_permlane16_swap((unsigned)idx, (unsigned)idx, false, false);
+        v = __uint_as_float(rv[0]);
+        idx = (int)ri[0];
+        vx_am_merge(v, idx, __uint_as_float(rv[1]), (int)ri[1]);
     }
+    {
+        const auto rv = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        const auto ri = __builtin_amdgcn_permlane32_swap((unsigned)idx, (unsigned)idx, false, false);
+        v = __uint_as_float(rv[0]);
+        idx = (int)ri[0];
+        vx_am_merge(v, idx, __uint_as_float(rv[1]), (int)ri[1]);
+    }
+}
+
+// *found (optional): whether some value was above -inf; the maximum itself
+// is then *vmax (the caller reads l[0] otherwise, as the reference does)
+__device__ __forceinline__ int vx_wg_argmax(float v, int idx, float *redv, int *redi, float *vmax = nullptr,
+                                            bool *found = nullptr)
+{
+    vx_wave_argmax64(v, idx);
     if ((threadIdx.x & 63) == 0) { redv[threadIdx.x >> 6] = v; redi[threadIdx.x >> 6] = idx; }
     __syncthreads();
     float bv = redv[0];
@@ -77,6 +113,8 @@ __device__ __forceinline__ int vx_wg_argmax(float v, int idx, float *redv, int *
     for (int i = 1; i < SB / 64; i++)
         if (redv[i] > bv || (redv[i] == bv && redi[i] < bi)) { bv = redv[i]; bi = redi[i]; }
     __syncthreads();
+    if (vmax) *vmax = bv;
+    if (found) *found = bi != 0x7fffffff;
     return bi == 0x7fffffff ? 0 : bi;
 }
 
@@ -296,7 +334,9 @@ __global__ __launch_bounds__(SB) void vx_sample_reg_kernel(const float *__restri
 #pragma unroll
     for (int j = 0; j < SE; j++)
         if (b + j < V && (x[j] > bv || (x[j] == bv && b + j < bi))) { bv = x[j]; bi = b + j; }
-    const int am = vx_wg_argmax(bv, bi, redv, redi);
+    float amv;
+    bool amf;
+    const int am = vx_wg_argmax(bv, bi, redv, redi, &amv, &amf);
     if (!(T > 0.0f)) {
         if (threadIdx.x == 0) {
             token_out[0] = am;
@@ -305,7 +345,7 @@ __global__ __launch_bounds__(SB) void vx_sample_reg_kernel(const float *__restri
         }
         return;
     }
-    const float mx = l[am];
+    const float mx = amf ? amv : l[0];
     float sum = 0.0f;
 #pragma unroll
     for (int j = 0; j < SE; j++) {

@@ -975,6 +975,13 @@ static vx_error forward_pro(vx_model *m, int M, int n_past, int logits_mode)
             p.part = d->ws.part; p.n_chunks = n_chunks;
             p.n_heads = d->n_heads; p.n_kv_heads = d->n_kv; p.head_dim = d->hd;
             p.clear = d->acc_qkv; p.n_clear = (size_t)M * d->ld_qkv;
+        } else if (M <= VXH_ATTN_QKV_FAST_ROWS && (d->hd == 64 || d->hd == 128)) {
+            /* RoPE and the new k/v rows inside the attention's first launch */
+            TRY(vxh_attention_qkv(d->acc_qkv, d->ld_qkv, SS(l, 0), dd, Ld->bq, Ld->bk, Ld->bv, d->rope_cos,
+                                  d->rope_sin, d->n_pos, M, n_past, n_ctx, d->n_heads, d->n_kv, d->hd,
+                                  d->opt.attn_cap, kc, vc, d->att, dd, &d->ws, s));
+            p.kind = VXH_PRO_ROWS;
+            p.x = d->att; p.ldx = dd;
         } else {
             TRY(vxh_rope_kv_norm(d->acc_qkv, d->ld_qkv, M, n_past, n_ctx, d->n_heads, d->n_kv, d->hd,
                                  Ld->bq, Ld->bk, Ld->bv, d->rope_cos, d->rope_sin, d->n_pos, SS(l, 0), dd,
