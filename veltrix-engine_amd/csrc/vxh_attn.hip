@@ -394,20 +394,35 @@ __device__ __forceinline__ void vx_attention_mfma_body(
     // of positions t0 + 16 pg + 4 r + s (dims 64 u + 4 n .. + 3) from the cache;
     // positions past the cache end read as zeros
     float4 kr[2][NJ], vr[2][4][NV4];
+    auto load_kv = [&]() {
 #pragma unroll
-    for (int pg = 0; pg < 2; pg++) {
-        const int pos = t0 + 16 * pg + n;
-        const size_t off = (size_t)min(pos, n_ctx - 1) * kvd + g * HD + 4 * r;
+        for (int pg = 0; pg < 2; pg++) {
+            const int pos = t0 + 16 * pg + n;
+            const size_t off = (size_t)min(pos, n_ctx - 1) * kvd + g * HD + 4 * r;
 #pragma unroll
-        for (int j = 0; j < NJ; j++) kr[pg][j] = *(const float4 *)(kc + off + 16 * j);
+            for (int j = 0; j < NJ; j++) kr[pg][j] = *(const float4 *)(kc + off + 16 * j);
 #pragma unroll
-        for (int st = 0; st < 4; st++) {
-            const int pv = t0 + 16 * pg + 4 * r + st;
-            const size_t ov = (size_t)min(pv, n_ctx - 1) * kvd + g * HD + 4 * n;
+            for (int st = 0; st < 4; st++) {
+                const int pv = t0 + 16 * pg + 4 * r + st;
+                const size_t ov = (size_t)min(pv, n_ctx - 1) * kvd + g * HD + 4 * n;
 #pragma unroll
-            for (int u = 0; u < NV4; u++) vr[pg][st][u] = *(const float4 *)(vc + ov + 64 * u);
+                for (int u = 0; u < NV4; u++) vr[pg][st][u] = *(const float4 *)(vc + ov + 64 * u);
+            }
         }
-    }
+#pragma unroll
+        for (int pg = 0; pg < 2; pg++) {
+            const bool ok = t0 + 16 * pg + n < n_ctx;
+#pragma unroll
+            for (int j = 0; j < NJ; j++) kr[pg][j] = vx_keep4(ok, kr[pg][j]);
+#pragma unroll
+            for (int st = 0; st < 4; st++) {
+                const bool okv = t0 + 16 * pg + 4 * r + st < n_ctx;
+#pragma unroll
+                for (int u = 0; u < NV4; u++) vr[pg][st][u] = vx_keep4(okv, vr[pg][st][u]);
+            }
+        }
+    };
+    load_kv();
 
     // query n of this group: q vector (hl, m), its causal length cs
     const int qi = qg * 16 + n;
@@ -427,18 +442,6 @@ __device__ __forceinline__ void vx_attention_mfma_body(
 #pragma unroll
         for (int j = 0; j < NJ; j++)
             qv[j] = vx_keep4(qok, make_float4(qv[j].x * scale, qv[j].y * scale, qv[j].z * scale, qv[j].w * scale));
-    }
-#pragma unroll
-    for (int pg = 0; pg < 2; pg++) {
-        const bool ok = t0 + 16 * pg + n < n_ctx;
-#pragma unroll
-        for (int j = 0; j < NJ; j++) kr[pg][j] = vx_keep4(ok, kr[pg][j]);
-#pragma unroll
-        for (int st = 0; st < 4; st++) {
-            const bool okv = t0 + 16 * pg + 4 * r + st < n_ctx;
-#pragma unroll
-            for (int u = 0; u < NV4; u++) vr[pg][st][u] = vx_keep4(okv, vr[pg][st][u]);
-        }
     }
 
     // QKV: the workgroup derives its 16 q vectors (deferred RMSNorm, bias,
@@ -620,7 +623,7 @@ __global__ __launch_bounds__(ATT_THREADS) __attribute__((amdgpu_waves_per_eu(3))
 }
 
 template <int HD>
-__global__ __launch_bounds__(ATT_THREADS) void vx_attention_mfma_qkv_kernel(
+__global__ __launch_bounds__(ATT_THREADS) __attribute__((amdgpu_waves_per_eu(HD == 64 ? 3 : 2))) void vx_attention_mfma_qkv_kernel(
     const float *__restrict__ q, int M, int n_past, int n_ctx, int n_heads, int n_kv, int cap,
     float *__restrict__ kc, float *__restrict__ vc, int n_chunks, int n_chunks_w, int n_qg,
     float *__restrict__ part, vx_qkv_args qa)
@@ -636,6 +639,7 @@ __global__ __launch_bounds__(ATT_THREADS) void vx_attention_mfma_qkv_kernel(
 // its running (max, sum, acc) is merged across the slices in LDS, so the
 // chunk walk is spread over the workgroup instead of serialised per thread.
 #define CMB_THREADS 256
+#define CMB_BATCH 12   // chunks whose loads a thread issues together (one round trip per batch)
 
 // Panel of row m of att (XP variant): the last head of the row to finish
 // reads the row back (after an agent-scope acquire) and writes its fp16 hi/lo
@@ -710,11 +714,11 @@ __global__ __launch_bounds__(CMB_THREADS) void vx_attention_combine_kernel(
     float mx = -INFINITY, l = 0.0f;
     float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
     if (sl < S) {
-        for (int c0 = sl; c0 < n_chunks; c0 += 4 * S) {
-            float cm[4], cl[4];
-            float4 ca[4];
+        for (int c0 = sl; c0 < n_chunks; c0 += CMB_BATCH * S) {
+            float cm[CMB_BATCH], cl[CMB_BATCH];
+            float4 ca[CMB_BATCH];
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
+            for (int u = 0; u < CMB_BATCH; u++) {
                 const int c = c0 + u * S;
                 const float *pc = pq + (size_t)min(c, n_chunks - 1) * cstride;
                 cm[u] = c < n_chunks ? pc[0] : -INFINITY;
@@ -722,7 +726,7 @@ __global__ __launch_bounds__(CMB_THREADS) void vx_attention_combine_kernel(
                 ca[u] = *(const float4 *)(pc + 4 + 4 * d4);
             }
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
+            for (int u = 0; u < CMB_BATCH; u++) {
                 if (cm[u] == -INFINITY) continue;
                 const float nm = fmaxf(mx, cm[u]);
                 const float fo = mx == -INFINITY ? 0.0f : expf(mx - nm);
