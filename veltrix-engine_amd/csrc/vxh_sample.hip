@@ -12,10 +12,17 @@
 
 #define SB 1024   // threads per sampling workgroup
 
+// round(w * 2^32) as (uint64)(w * 2^32 + 0.5) in fp64, computed in fp32:
+// w * 2^32 is exact; below 2^23 adding 0.5 is exact too and truncation gives
+// the same floor, from 2^23 on the product is already an integer.  Masses of
+// 2^32 and more (w >= 1) take the fp64 expression itself.
 __device__ __forceinline__ uint64_t vx_fixed32(float w)
 {
     if (!(w > 0.0f)) return 0ull;
-    return (uint64_t)((double)w * 4294967296.0 + 0.5);
+    float x = w * 4294967296.0f;
+    if (x >= 4294967296.0f) return (uint64_t)((double)w * 4294967296.0 + 0.5);
+    if (x < 8388608.0f) x += 0.5f;
+    return (uint64_t)(uint32_t)x;
 }
 
 // --- workgroup reductions (SB threads, 16 waves) ----------------------------
@@ -511,12 +518,131 @@ __global__ __launch_bounds__(SB) void vx_accept_kernel(const float *__restrict__
     }
 }
 
+// vx_accept_kernel for V <= SB * SE: the ratio tests of the k drafts run on
+// k lanes at once (the first rejection is the first failing lane, as in the
+// sequential scan), and thread t computes the probabilities of its
+// contiguous entries [t*SE, t*SE + SE) of the decided row once, keeping them
+// in registers for the mass, the inverse-CDF scan and the argmax fallback.
+// Same arithmetic as vx_accept_kernel.
+__global__ __launch_bounds__(SB) void vx_accept_reg_kernel(const float *__restrict__ L, int ldl, int V,
+                                                           const float *__restrict__ stats,
+                                                           const float *__restrict__ D, int ldd, int Vd,
+                                                           const float *__restrict__ nuc,
+                                                           const int *__restrict__ drafts, int k, float T,
+                                                           const float *__restrict__ u, int *__restrict__ out)
+{
+    __shared__ float redv[SB / 64];
+    __shared__ int redi[SB / 64];
+    __shared__ uint64_t wsum[SB / 64];
+    __shared__ int res;
+    __shared__ int s_rej;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (threadIdx.x < 64) {
+        // ratio test of draft j = lane (src/speculative.c:199-200 on probabilities)
+        bool rej = true;
+        if (lane < k) {
+            const int j = lane;
+            const float *lj = L + (size_t)j * ldl;
+            const float mx = stats[j * 3 + 0], inv = 1.0f / (stats[j * 3 + 1] + 1e-30f);
+            const int d = drafts[j];
+            const float pt = (d >= 0 && d < V) ? expf((lj[d] - mx) / T) * inv : 0.0f;
+            const float qd = (d >= 0 && d < Vd) ? vx_draft_q(D + (size_t)j * ldd, nuc + j * 8, d, T) : 0.0f;
+            const float alpha = fminf(1.0f, pt / fmaxf(qd, 1e-10f));
+            rej = !(u[j] < alpha);
+        }
+        const uint64_t bal = __ballot(rej);
+        const int jr = bal ? __builtin_ctzll(bal) : 64;
+        const int j = jr < k ? jr : k;
+        if (lane < j) out[2 + lane] = drafts[lane];
+        if (lane == 0) s_rej = j;
+    }
+    __syncthreads();
+    const int j = s_rej;
+    const float *lj = L + (size_t)j * ldl;
+    const float mx = stats[j * 3 + 0], inv = 1.0f / (stats[j * 3 + 1] + 1e-30f);
+    const float *dj = D + (size_t)min(j, k - 1) * ldd;
+    const float *nj = nuc + min(j, k - 1) * 8;
+    const bool resample = j < k;
+    const int b = threadIdx.x * SE;
+    float w[SE];
+#pragma unroll
+    for (int e = 0; e < SE; e++) {
+        const int v = b + e;
+        float r = 0.0f;
+        if (v < V) {
+            const float p = expf((lj[v] - mx) / T) * inv;
+            if (resample) {
+                const float q = v < Vd ? vx_draft_q(dj, nj, v, T) : 0.0f;
+                r = fmaxf(0.0f, p - q);
+            } else {
+                r = p;
+            }
+        }
+        w[e] = r;
+    }
+    uint64_t St = 0;
+#pragma unroll
+    for (int e = 0; e < SE; e++) St += vx_fixed32(w[e]);
+    uint64_t incl = St;
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint64_t y = vx_shfl_up_u64(incl, o);
+        if (lane >= o) incl += y;
+    }
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    uint64_t off = 0, S = 0;
+    for (int wv = 0; wv < SB / 64; wv++) {
+        if (wv < wave) off += wsum[wv];
+        S += wsum[wv];
+    }
+    int tok;
+    if (S == 0) {
+        if (resample) {
+            // no residual mass: argmax of the residual (first index on ties)
+            float bv = -INFINITY;
+            int bi = 0x7fffffff;
+#pragma unroll
+            for (int e = 0; e < SE; e++)
+                if (b + e < V && (w[e] > bv || (w[e] == bv && b + e < bi))) { bv = w[e]; bi = b + e; }
+            tok = vx_wg_argmax(bv, bi, redv, redi);
+        } else {
+            tok = __float_as_int(stats[j * 3 + 2]);
+        }
+    } else {
+        const uint64_t thr = vx_threshold(u[k], S);
+        const uint64_t before = off + incl - St;
+        if (threadIdx.x == 0) res = V - 1;
+        __syncthreads();
+        if (before < thr && before + St >= thr) {
+            uint64_t c = before;
+            int t = b + SE - 1;
+            bool found = false;
+#pragma unroll
+            for (int e = 0; e < SE; e++) {
+                c += vx_fixed32(w[e]);
+                if (!found && c >= thr) { t = b + e; found = true; }
+            }
+            res = t;
+        }
+        __syncthreads();
+        tok = res;
+    }
+    if (threadIdx.x == 0) {
+        out[2 + j] = tok;
+        out[0] = j + 1;
+        out[1] = j;
+    }
+}
+
 extern "C" int vxh_accept(const float *L, int ldl, int V, const float *stats, const float *D,
                           int ldd, int Vd, const float *nuc, const int *drafts, int k, float T,
                           const float *u, int *out, vxh_stream s)
 {
     if (k < 0 || V <= 0) return vxh_fail(VXH_ERR_PARAM, "accept: k %d V %d", k, V);
-    vx_accept_kernel<<<1, SB, 0, vxh_hs(s)>>>(L, ldl, V, stats, D, ldd, Vd, nuc, drafts, k, T, u, out);
+    if (T > 0.0f && k >= 1 && k <= 64 && V <= SB * SE)
+        vx_accept_reg_kernel<<<1, SB, 0, vxh_hs(s)>>>(L, ldl, V, stats, D, ldd, Vd, nuc, drafts, k, T, u, out);
+    else
+        vx_accept_kernel<<<1, SB, 0, vxh_hs(s)>>>(L, ldl, V, stats, D, ldd, Vd, nuc, drafts, k, T, u, out);
     VXH_LAUNCHED();
     return VXH_OK;
 }
