@@ -431,6 +431,49 @@ __device__ __forceinline__ float vx_draft_q(const float *d, const float *nuc, in
     return in ? p / nuc[4] : 0.0f;
 }
 
+// One pass over the decided row: thread t sums the fixed-point masses of its
+// contiguous entries [t*C, t*C + C) (C = ceil(V / SB)); a workgroup scan of
+// those sums gives the total and the chunk where the inverse CDF lands, and
+// only that chunk is evaluated again (the first index whose inclusive prefix
+// reaches the threshold).  Entries are evaluated V + C times instead of 3V.
+template <typename WF>
+__device__ int vx_wg_chunk_prefix(int n, uint64_t thr_u, bool by_u, float uval, WF W, uint64_t *wsum, int *res,
+                                  uint64_t *total)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int chunk = (n + SB - 1) / SB;
+    const int b = threadIdx.x * chunk, e = min(b + chunk, n);
+    uint64_t local = 0;
+    for (int v = b; v < e; v++) local += W(v);
+    uint64_t incl = local;
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint64_t y = vx_shfl_up_u64(incl, o);
+        if (lane >= o) incl += y;
+    }
+    if (lane == 63) wsum[wave] = incl;
+    if (threadIdx.x == 0) *res = n - 1;
+    __syncthreads();
+    uint64_t off = 0, S = 0;
+    for (int w = 0; w < SB / 64; w++) {
+        if (w < wave) off += wsum[w];
+        S += wsum[w];
+    }
+    *total = S;
+    const uint64_t thr = by_u ? vx_threshold(uval, S) : thr_u;
+    const uint64_t before = off + incl - local;
+    if (S > 0 && before < thr && before + local >= thr) {
+        uint64_t c = before;
+        for (int v = b; v < e; v++) {
+            c += W(v);
+            if (c >= thr) { *res = v; break; }
+        }
+    }
+    __syncthreads();
+    const int r = *res;
+    __syncthreads();
+    return r;
+}
+
 __global__ __launch_bounds__(SB) void vx_accept_kernel(const float *__restrict__ L, int ldl, int V,
                                                        const float *__restrict__ stats,
                                                        const float *__restrict__ D, int ldd, int Vd,
@@ -441,8 +484,7 @@ __global__ __launch_bounds__(SB) void vx_accept_kernel(const float *__restrict__
 {
     __shared__ float redv[SB / 64];
     __shared__ int redi[SB / 64];
-    __shared__ uint64_t red64[SB / 64];
-    __shared__ uint64_t scan[SB];
+    __shared__ uint64_t wsum[SB / 64];
     __shared__ int res;
     __shared__ int s_rej;
 
@@ -461,25 +503,46 @@ __global__ __launch_bounds__(SB) void vx_accept_kernel(const float *__restrict__
         }
         return;
     }
-    if (threadIdx.x == 0) {
-        int j = 0;
-        for (; j < k; j++) {
-            const float *lj = L + (size_t)j * ldl;
-            const float mx = stats[j * 3 + 0], inv = 1.0f / (stats[j * 3 + 1] + 1e-30f);
-            int d = drafts[j];
-            float pt = (d >= 0 && d < V) ? expf((lj[d] - mx) / T) * inv : 0.0f;
-            float qd = (d >= 0 && d < Vd) ? vx_draft_q(D + (size_t)j * ldd, nuc + j * 8, d, T) : 0.0f;
-            float alpha = fminf(1.0f, pt / fmaxf(qd, 1e-10f));
-            if (!(u[j] < alpha)) break;
-            out[2 + j] = d;
+    if (threadIdx.x < 64) {
+        // ratio tests of the drafts on parallel lanes; the first failing one
+        // is where the sequential scan (src/speculative.c:199-200) stops
+        const int lane = threadIdx.x;
+        bool rej = true;
+        if (lane < k) {
+            const float *lj = L + (size_t)lane * ldl;
+            const float mx = stats[lane * 3 + 0], inv = 1.0f / (stats[lane * 3 + 1] + 1e-30f);
+            const int d = drafts[lane];
+            const float pt = (d >= 0 && d < V) ? expf((lj[d] - mx) / T) * inv : 0.0f;
+            const float qd = (d >= 0 && d < Vd) ? vx_draft_q(D + (size_t)lane * ldd, nuc + lane * 8, d, T) : 0.0f;
+            const float alpha = fminf(1.0f, pt / fmaxf(qd, 1e-10f));
+            rej = !(u[lane] < alpha);
         }
-        s_rej = j;
+        // lanes k..63 count as failing, so the first failing lane is the
+        // decided row (k when every draft is accepted); drafts beyond 64
+        // continue sequentially below
+        const uint64_t bal = __ballot(rej);
+        int j = bal ? __builtin_ctzll(bal) : 64;
+        if (lane < min(j, k)) out[2 + lane] = drafts[lane];
+        if (lane == 0) {
+            for (; j < k; j++) {   // only k > 64
+                const float *lj = L + (size_t)j * ldl;
+                const float mx = stats[j * 3 + 0], inv = 1.0f / (stats[j * 3 + 1] + 1e-30f);
+                const int d = drafts[j];
+                const float pt = (d >= 0 && d < V) ? expf((lj[d] - mx) / T) * inv : 0.0f;
+                const float qd = (d >= 0 && d < Vd) ? vx_draft_q(D + (size_t)j * ldd, nuc + j * 8, d, T) : 0.0f;
+                const float alpha = fminf(1.0f, pt / fmaxf(qd, 1e-10f));
+                if (!(u[j] < alpha)) break;
+                out[2 + j] = d;
+            }
+            s_rej = min(j, k);
+        }
     }
     __syncthreads();
     const int j = s_rej;
     const float *lj = L + (size_t)j * ldl;
     const float mx = stats[j * 3 + 0], inv = 1.0f / (stats[j * 3 + 1] + 1e-30f);
     int tok;
+    uint64_t S = 0;
     if (j < k) {
         const float *dj = D + (size_t)j * ldd;
         const float *nj = nuc + j * 8;
@@ -489,9 +552,7 @@ __global__ __launch_bounds__(SB) void vx_accept_kernel(const float *__restrict__
             return fmaxf(0.0f, p - q);
         };
         auto W = [&](int v) -> uint64_t { return vx_fixed32(resid(v)); };
-        uint64_t S = 0;
-        for (int v = threadIdx.x; v < V; v += SB) S += W(v);
-        S = vx_wg_sum_u64(S, red64);
+        tok = vx_wg_chunk_prefix(V, 0, true, u[k], W, wsum, &res, &S);
         if (S == 0) {
             float bv = -INFINITY;
             int bi = 0x7fffffff;
@@ -500,16 +561,11 @@ __global__ __launch_bounds__(SB) void vx_accept_kernel(const float *__restrict__
                 if (r > bv || (r == bv && v < bi)) { bv = r; bi = v; }
             }
             tok = vx_wg_argmax(bv, bi, redv, redi);
-        } else {
-            tok = vx_wg_find_prefix(V, vx_threshold(u[k], S), W, scan, &res);
         }
     } else {
         auto W = [&](int v) -> uint64_t { return vx_fixed32(expf((lj[v] - mx) / T) * inv); };
-        uint64_t S = 0;
-        for (int v = threadIdx.x; v < V; v += SB) S += W(v);
-        S = vx_wg_sum_u64(S, red64);
+        tok = vx_wg_chunk_prefix(V, 0, true, u[k], W, wsum, &res, &S);
         if (S == 0) tok = __float_as_int(stats[j * 3 + 2]);
-        else tok = vx_wg_find_prefix(V, vx_threshold(u[k], S), W, scan, &res);
     }
     if (threadIdx.x == 0) {
         out[2 + j] = tok;
