@@ -128,6 +128,8 @@ typedef struct {
     float *xs;         /* device, fp32 copy for the dot-product path          */
     int M, K;
     int avx2;          /* 1: lane-pattern weights and corrections             */
+    int rs_ld;         /* 0: one scale per row; n > 0: one per 1024 columns,
+                          rscale[m * n + k / 1024] (vxh_swiglu_panel_norm)    */
 } vxh_panel;
 
 size_t vxh_panel_bytes(int M, int K);
@@ -160,6 +162,15 @@ int vxh_resid_rmsnorm_panel(float *x, int ldx, double *acc, int ld_acc, int M, i
  * (and to h_out when not NULL).  The AVX2 tail of h is zeros. */
 int vxh_swiglu_panel(double *acc, int ld_acc, int M, int F, float thr, int avx2, vxh_panel *p,
                      float *h_out, int ldh, vxh_stream s);
+/* vxh_swiglu_panel on the sums of a prologue GEMM whose RMSNorm is still
+ * pending: g and u are the fp32 roundings of the gate/up sums times
+ * 1/sqrt(ss_in[m]/ss_K + 1e-5) (ss_in NULL: times 1), exactly as the
+ * VXH_PRO_SWIGLU prologue forms them; the launch also zeroes n_clear doubles
+ * at clear.  One workgroup per (row, 1024 columns), each with its own
+ * power-of-two scale (p->rs_ld = chunks per row).  Exact-Q4_0 panel (no
+ * AVX2 tail). */
+int vxh_swiglu_panel_norm(double *acc, int ld_acc, int M, int F, float thr, const double *ss_in,
+                          int ss_K, double *clear, size_t n_clear, vxh_panel *p, vxh_stream s);
 
 /* ---- skinny-M dequant GEMM ---------------------------------------------------
  * Y[m][n] = sum_k X[m][k] * W[n][k] for m < M, n < N, W quantised, X a panel.

@@ -40,6 +40,7 @@ extern "C" int vxh_panel_alloc(vxh_panel *p, int max_M, int K)
     p->M = 0;
     p->K = K;
     p->avx2 = 0;
+    p->rs_ld = 0;
     if (max_M < 1 || max_M > 16 || K % 32 || K > VXH_MAX_K)
         return vxh_fail(VXH_ERR_PARAM, "panel_alloc: M %d K %d", max_M, K);
     int rc = vxh_malloc(&p->data, vxh_panel_bytes(max_M, K));
@@ -47,7 +48,7 @@ extern "C" int vxh_panel_alloc(vxh_panel *p, int max_M, int K)
     int nb = (K / 32 + 1) / 2 * 2;
     rc = vxh_malloc((void **)&p->corr, (size_t)nb * max_M * sizeof(float));
     if (rc) return rc;
-    rc = vxh_malloc((void **)&p->rscale, 16 * sizeof(float));
+    rc = vxh_malloc((void **)&p->rscale, (size_t)16 * ((K + VX_CHUNK - 1) / VX_CHUNK) * sizeof(float));
     if (rc) return rc;
     // padded blocks must read as zeros
     VXH_CHECK(hipMemset(p->data, 0, vxh_panel_bytes(max_M, K)));
@@ -96,6 +97,10 @@ struct vx_row_args {
     float *rscale;
     float *out;          // optional fp32 copy of the panel's values (normalised x / h)
     int ld_out;
+    const double *ss_in; // SWIGLU: gate/up sums times 1/sqrt(ss_in[m]/ss_K + 1e-5) (NULL: times 1)
+    int ss_K;
+    double *clr;         // n_clr doubles zeroed by the launch (an accumulator already consumed)
+    long n_clr;
 };
 
 __device__ __forceinline__ float vx_block_sum(float v, float *red)
@@ -135,6 +140,12 @@ __global__ __launch_bounds__(VX_ROW_THREADS) void vx_row_panel_kernel(vx_row_arg
     const int K = a.K, nb = K / 32, nbp = (nb + 1) / 2 * 2;
     const int ng = nb * 4, ngp = nbp * 4;
     float v[G][8];
+    if (a.clr) {
+        const long per = (a.n_clr + gridDim.x - 1) / gridDim.x;
+        const long b = (long)blockIdx.x * per, e = min(b + per, a.n_clr);
+        for (long i = b + threadIdx.x; i < e; i += blockDim.x) a.clr[i] = 0.0;
+    }
+    const float rin = (MODE == VX_ROW_SWIGLU && a.ss_in) ? vx_rms_inv((float)a.ss_in[m], a.ss_K) : 1.0f;
 
     // ---- load (and, for the accumulator modes, consume) ----
 #pragma unroll
@@ -161,9 +172,11 @@ __global__ __launch_bounds__(VX_ROW_THREADS) void vx_row_panel_kernel(vx_row_arg
             }
 #pragma unroll
             for (int q = 0; q < 4; q++) {
-                float g0 = vx_silu((float)gv[q].x), g1 = vx_silu((float)gv[q].y);
-                v[j][2 * q] = fabsf(g0) < a.thr ? 0.0f : g0 * (float)uv[q].x;
-                v[j][2 * q + 1] = fabsf(g1) < a.thr ? 0.0f : g1 * (float)uv[q].y;
+                // as the SwiGLU prologue of the GEMM: g, u rounded to fp32, times 1/rms
+                const float g0 = vx_silu((float)gv[q].x * rin), g1 = vx_silu((float)gv[q].y * rin);
+                const float u0 = (float)uv[q].x * rin, u1 = (float)uv[q].y * rin;
+                v[j][2 * q] = fabsf(g0) < a.thr ? 0.0f : g0 * u0;
+                v[j][2 * q + 1] = fabsf(g1) < a.thr ? 0.0f : g1 * u1;
             }
         } else {
             float *xr = a.x + (size_t)m * a.ldx + e0;
@@ -312,6 +325,7 @@ static vx_row_args vx_row_base(vxh_panel *p, int M, int K, int avx2)
     a.rscale = p->rscale;
     p->M = M;
     p->avx2 = avx2;
+    p->rs_ld = 0;
     return a;
 }
 
@@ -378,6 +392,85 @@ extern "C" int vxh_swiglu_panel(double *acc, int ld_acc, int M, int F, float thr
     return vx_launch_row<VX_ROW_SWIGLU>(a, s);
 }
 
+// SwiGLU panel of M rows x F with one power-of-two scale per VX_CHUNK
+// columns: workgroup (chunk c, row m) forms h for columns [c*VX_CHUNK,
+// (c+1)*VX_CHUNK), one thread per 8 columns, as the VXH_PRO_SWIGLU prologue
+// does (src/model.c:582-585), clears the gate/up sums it read, and writes
+// its part of the panel; the launch also zeroes `clr`.
+#define VX_SWC_THREADS (VX_CHUNK / 8)
+__global__ __launch_bounds__(VX_SWC_THREADS) void vx_swiglu_chunk_kernel(
+    double *__restrict__ acc, int ld_acc, int M, int F, float thr, const double *__restrict__ ss_in, int ss_K,
+    uint4 *__restrict__ panel, float *__restrict__ rscale, int rs_ld, double *__restrict__ clr, long n_clr)
+{
+    __shared__ float red[VX_SWC_THREADS / 64];
+    const int c = blockIdx.x, m = blockIdx.y;
+    if (clr) {
+        const long nb = (long)gridDim.x * gridDim.y, bi = (long)m * gridDim.x + c;
+        const long per = (n_clr + nb - 1) / nb;
+        const long b = bi * per, e = min(b + per, n_clr);
+        for (long i = b + threadIdx.x; i < e; i += VX_SWC_THREADS) clr[i] = 0.0;
+    }
+    const int nb = F / 32, nbp = (nb + 1) / 2 * 2, ng = nb * 4, ngp = nbp * 4;
+    const int g = c * VX_SWC_THREADS + threadIdx.x;   // group of 8 columns
+    const float rin = ss_in ? vx_rms_inv((float)ss_in[m], ss_K) : 1.0f;
+    float v[8];
+#pragma unroll
+    for (int kk = 0; kk < 8; kk++) v[kk] = 0.0f;
+    if (g < ng) {
+        const int e0 = 8 * g;
+        double *ar = acc + (size_t)m * ld_acc + 32 * (e0 / 16) + e0 % 16;
+        double2 gv[4], uv[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            gv[q] = *(const double2 *)(ar + 2 * q);
+            uv[q] = *(const double2 *)(ar + 16 + 2 * q);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            *(double2 *)(ar + 2 * q) = make_double2(0.0, 0.0);
+            *(double2 *)(ar + 16 + 2 * q) = make_double2(0.0, 0.0);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float g0 = vx_silu((float)gv[q].x * rin), g1 = vx_silu((float)gv[q].y * rin);
+            const float u0 = (float)uv[q].x * rin, u1 = (float)uv[q].y * rin;
+            v[2 * q] = fabsf(g0) < thr ? 0.0f : g0 * u0;
+            v[2 * q + 1] = fabsf(g1) < thr ? 0.0f : g1 * u1;
+        }
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < 8; kk++) amax = fmaxf(amax, fabsf(v[kk]));
+    amax = vx_block_max(amax, red);
+    float rs;
+    const float sc = vx_row_scale(amax, &rs);
+    if (threadIdx.x == 0) rscale[m * rs_ld + c] = rs;
+    if (g < ngp) {   // groups of the padding block are zeros
+        float x[8];
+#pragma unroll
+        for (int kk = 0; kk < 8; kk++) x[kk] = v[kk] * sc;
+        vx_panel_store(panel, M, g, m, x);
+    }
+}
+
+extern "C" int vxh_swiglu_panel_norm(double *acc, int ld_acc, int M, int F, float thr, const double *ss_in,
+                                     int ss_K, double *clear, size_t n_clear, vxh_panel *p, vxh_stream s)
+{
+    int rc = vx_row_check(p, M, F, "swiglu_panel_norm");
+    if (rc) return rc;
+    if (ss_in && ss_K < 1) return vxh_fail(VXH_ERR_PARAM, "swiglu_panel_norm: norm length %d", ss_K);
+    if (n_clear && !clear) return vxh_fail(VXH_ERR_PARAM, "swiglu_panel_norm: clear range without a pointer");
+    const int chunks = (F + VX_CHUNK - 1) / VX_CHUNK;
+    p->M = M;
+    p->avx2 = 0;
+    p->rs_ld = chunks;
+    vx_swiglu_chunk_kernel<<<dim3(chunks, M), VX_SWC_THREADS, 0, vxh_hs(s)>>>(
+        acc, ld_acc, M, F, thr, ss_in, ss_K, (uint4 *)p->data, p->rscale, chunks, n_clear ? clear : nullptr,
+        (long)n_clear);
+    VXH_LAUNCHED();
+    return VXH_OK;
+}
+
 __global__ void vx_rmsnorm_kernel(const float *__restrict__ x, int ldx, int K,
                                   const float *__restrict__ w, float *__restrict__ out, int ld_out)
 {
@@ -421,8 +514,8 @@ extern "C" int vxh_gemm_acc_timed(const vxh_qmat *W, const vxh_panel *X, int M, 
     a.panel = (const uint4 *)X->data;
     a.corr = X->corr;
     a.rscale = X->rscale;
-    a.rs_ld = 1;
-    a.rs_chunk = 1 << 30;
+    a.rs_ld = X->rs_ld > 0 ? X->rs_ld : 1;
+    a.rs_chunk = X->rs_ld > 0 ? VX_CHUNK / 64 : 1 << 30;   // block pairs per scale chunk
     a.acc = acc;
     a.ld_acc = ld_acc;
     a.n_out = n_out;

@@ -111,7 +111,7 @@ struct vx_ppw_set {
 // Fused-epilogue arguments (vxh_fused.hip): the last workgroup to finish a
 // super-group of output rows runs the epilogue on its final sums.
 enum { VX_EPI_NONE = 0, VX_EPI_STORE = 1, VX_EPI_RESID = 2, VX_EPI_SWIGLU = 3, VX_EPI_ROPE = 4 };
-#define VX_CHUNK 1024   // panel columns per power-of-two scale chunk (fused path)
+#define VX_CHUNK 1024   // panel columns per power-of-two scale chunk (fused path, SwiGLU panel)
 
 #define VX_CNT_STRIDE 64   // words between arrival counters (256 bytes)
 

@@ -1002,13 +1002,22 @@ static vx_error forward_pro(vx_model *m, int M, int n_past, int logits_mode)
         p.clear = d->acc_x; p.n_clear = (size_t)M * dd;
         if ((e = pgemm(d, &Ld->wgu, &p, M, d->acc_gu, d->ld_gu, d->ld_gu, VX_PROF_GATEUP, 2 * d->F)))
             return e;
-        memset(&p, 0, sizeof(p));
-        p.kind = VXH_PRO_SWIGLU;
-        p.src = d->acc_gu; p.ld_src = d->ld_gu;
-        p.ss_in = SS(l, 1); p.ss_K = dd;
-        p.thr = d->opt.ffn_gate_threshold;
-        p.clear = d->acc_y; p.n_clear = (size_t)M * dd;
-        if ((e = pgemm(d, &Ld->wd, &p, M, d->acc_x, dd, dd, VX_PROF_DOWN, dd))) return e;
+        if (M > VXH_PRO_ATTN_MAX_ROWS) {
+            /* verify batches: the SwiGLU panel once per forward (each of the
+             * down GEMM's tile groups would rebuild its slice from the fp64
+             * gate/up sums); the panel launch clears acc_gu and acc_y */
+            TRY(vxh_swiglu_panel_norm(d->acc_gu, d->ld_gu, M, d->F, d->opt.ffn_gate_threshold, SS(l, 1), dd,
+                                      d->acc_y, (size_t)M * dd, &d->pan_f, s));
+            if ((e = gemm(d, &Ld->wd, &d->pan_f, M, d->acc_x, dd, dd, VX_PROF_DOWN, dd))) return e;
+        } else {
+            memset(&p, 0, sizeof(p));
+            p.kind = VXH_PRO_SWIGLU;
+            p.src = d->acc_gu; p.ld_src = d->ld_gu;
+            p.ss_in = SS(l, 1); p.ss_K = dd;
+            p.thr = d->opt.ffn_gate_threshold;
+            p.clear = d->acc_y; p.n_clear = (size_t)M * dd;
+            if ((e = pgemm(d, &Ld->wd, &p, M, d->acc_x, dd, dd, VX_PROF_DOWN, dd))) return e;
+        }
     }
     /* x += last down projection (clears acc_x) */
     TRY(vxh_acc_store(d->acc_x, dd, M, dd, d->x, dd, d->x, dd, s));
