@@ -340,6 +340,11 @@ def run_spec(args):
     print(json.dumps(line), flush=True)
 
 
+class _Panel(C.Structure):
+    _fields_ = [("data", C.c_void_p), ("corr", C.c_void_p), ("rscale", C.c_void_p), ("xs", C.c_void_p),
+                ("M", C.c_int), ("K", C.c_int), ("avx2", C.c_int), ("rs_ld", C.c_int)]
+
+
 class _QMat(C.Structure):
     _fields_ = [("type", C.c_int), ("n_rows", C.c_int), ("n_cols", C.c_int), ("n_pairs", C.c_int),
                 ("qs", C.c_void_p), ("d", C.c_void_p)]
@@ -365,6 +370,12 @@ def _bind_gemm(N, P):
     L.vxh_gemm_pro.argtypes = [vp, C.c_int, vp, vp, C.c_int, C.c_int, C.c_float, vp, vp, vp]
     L.vxh_acc_store.argtypes = [vp, C.c_int, C.c_int, C.c_int, vp, C.c_int, vp, C.c_int, vp]
     L.vxh_qmat_free.argtypes = [vp]
+    L.vxh_panel_alloc.argtypes = [vp, C.c_int, C.c_int]
+    L.vxh_panel_free.argtypes = [vp]
+    L.vxh_swiglu_panel_norm.argtypes = [vp, C.c_int, C.c_int, C.c_int, C.c_float, vp, C.c_int, vp, C.c_size_t,
+                                        vp, vp]
+    L.vxh_gemm_acc.argtypes = [vp, vp, C.c_int, vp, C.c_int, C.c_int, C.c_float, vp, C.c_int, C.c_float,
+                               C.c_int, vp]
     L.vxh_event_create.argtypes = [vp]
     L.vxh_event_destroy.argtypes = [vp]
     L.vxh_event_record.argtypes = [vp, vp]
@@ -410,10 +421,11 @@ def _time_loop(L, reps, body):
 
 def run_gemm(args):
     """Isolated verify GEMM kernels at M = k+1 on the 7B shapes, each with the
-    panel prologue the verify forward gives it (vxh_gemm_pro: residual add +
-    norm weight for QKV and gate/up, attention rows for the output
-    projection, SwiGLU for down, norm weight for the logits), weights rotated
-    over > 300 MB so the Infinity Cache does not serve them."""
+    input the verify forward gives it (vxh_gemm_pro: residual add + norm
+    weight for QKV and gate/up, attention rows for the output projection, norm
+    weight for the logits; down: a plain panel made once by
+    vxh_swiglu_panel_norm, then vxh_gemm_acc), weights rotated over > 300 MB so
+    the Infinity Cache does not serve them."""
     N, P = load_product()
     import ctypes as CC
     L = _bind_gemm(N, P)
@@ -452,8 +464,18 @@ def run_gemm(args):
         if kind == PRO_SWIGLU:
             pro.src, pro.ld_src, pro.ss_in, pro.ss_K, pro.thr = bufs[1].ptr, ld_src, bufs[5].ptr, 4096, 0.01
         acc = N.DevBuf(L, np.zeros(M * rows, np.float64))
+        panel = None
+        if kind == PRO_SWIGLU:
+            # the verify forward's down projection: SwiGLU panel once, then a plain-panel GEMM
+            panel = _Panel()
+            assert L.vxh_panel_alloc(CC.byref(panel), M, cols) == 0, L.vxh_last_error()
+            assert L.vxh_swiglu_panel_norm(bufs[1].ptr, ld_src, M, cols, 0.01, bufs[5].ptr, 4096, None, 0,
+                                           CC.byref(panel), None) == 0, L.vxh_last_error()
 
         def launch(q):
+            if panel is not None:
+                return L.vxh_gemm_acc(CC.byref(q), CC.byref(panel), M, acc.ptr, rows, rows, 1.0, None, 0, 0.0,
+                                      0, None)
             return L.vxh_gemm_pro(CC.byref(q), M, CC.byref(pro), acc.ptr, rows, rows, 1.0, None, None, None)
         for q in mats:
             assert launch(q) == 0, L.vxh_last_error()
@@ -468,12 +490,14 @@ def run_gemm(args):
         alg = mat_bytes + 4 * M * cols + 4 * M * rows
         gbs = alg / (avg_us * 1e-6) / 1e9
         results.append({"shape": f"{'Q4_0' if qt == 2 else 'Q8_0'} {rows}x{cols} M={M}",
-                        "prologue": {PRO_ROWS: "rows", PRO_RESID: "resid", PRO_SWIGLU: "swiglu"}[kind],
+                        "prologue": {PRO_ROWS: "rows", PRO_RESID: "resid", PRO_SWIGLU: "swiglu panel"}[kind],
                         "avg_us": round(avg_us, 2), "GB/s": round(gbs, 1),
                         "frac": round(gbs / PEAK_HBM_GBS, 4)})
         log(json.dumps(results[-1]))
         for b in bufs + [acc]:
             b.free()
+        if panel is not None:
+            L.vxh_panel_free(CC.byref(panel))
         for q in mats:
             L.vxh_qmat_free(CC.byref(q))
     print(json.dumps({"mode": "gemm", "M": M, "results": results}), flush=True)
