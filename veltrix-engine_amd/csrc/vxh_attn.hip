@@ -394,13 +394,28 @@ __device__ __forceinline__ void vx_attention_mfma_body(
     // of positions t0 + 16 pg + 4 r + s (dims 64 u + 4 n .. + 3) from the cache;
     // positions past the cache end read as zeros
     float4 kr[2][NJ], vr[2][4][NV4];
-    auto load_kv = [&]() {
+    // K first; at head_dim 128 V after the score MFMAs are issued (its
+    // latency overlaps the scores and the softmax, and K and V need not be
+    // live together, so 3 wavefronts fit a SIMD); at 64 (draft decode: too
+    // few wavefronts to hide a second round trip) V with K
+    auto load_k = [&]() {
 #pragma unroll
         for (int pg = 0; pg < 2; pg++) {
             const int pos = t0 + 16 * pg + n;
             const size_t off = (size_t)min(pos, n_ctx - 1) * kvd + g * HD + 4 * r;
 #pragma unroll
             for (int j = 0; j < NJ; j++) kr[pg][j] = *(const float4 *)(kc + off + 16 * j);
+        }
+#pragma unroll
+        for (int pg = 0; pg < 2; pg++) {
+            const bool ok = t0 + 16 * pg + n < n_ctx;
+#pragma unroll
+            for (int j = 0; j < NJ; j++) kr[pg][j] = vx_keep4(ok, kr[pg][j]);
+        }
+    };
+    auto load_v = [&]() {
+#pragma unroll
+        for (int pg = 0; pg < 2; pg++)
 #pragma unroll
             for (int st = 0; st < 4; st++) {
                 const int pv = t0 + 16 * pg + 4 * r + st;
@@ -408,21 +423,17 @@ __device__ __forceinline__ void vx_attention_mfma_body(
 #pragma unroll
                 for (int u = 0; u < NV4; u++) vr[pg][st][u] = *(const float4 *)(vc + ov + 64 * u);
             }
-        }
 #pragma unroll
-        for (int pg = 0; pg < 2; pg++) {
-            const bool ok = t0 + 16 * pg + n < n_ctx;
-#pragma unroll
-            for (int j = 0; j < NJ; j++) kr[pg][j] = vx_keep4(ok, kr[pg][j]);
+        for (int pg = 0; pg < 2; pg++)
 #pragma unroll
             for (int st = 0; st < 4; st++) {
                 const bool okv = t0 + 16 * pg + 4 * r + st < n_ctx;
 #pragma unroll
                 for (int u = 0; u < NV4; u++) vr[pg][st][u] = vx_keep4(okv, vr[pg][st][u]);
             }
-        }
     };
-    load_kv();
+    load_k();
+    if constexpr (HD == 64) load_v();
 
     // query n of this group: q vector (hl, m), its causal length cs
     const int qi = qg * 16 + n;
@@ -449,10 +460,19 @@ __device__ __forceinline__ void vx_attention_mfma_body(
     // row of this forward (at min(n_past + m, n_ctx - 1); only a one-row
     // forward is clamped) -- head g's new k/v rows too (query group 0 also
     // stores them into the cache); the wavefronts take them from LDS.
+    bool has_new_wg = false;   // QKV: this workgroup's chunks hold rows of this forward
+    __shared__ float4 s_new[QKV ? VX_ATT_MFMA_MAX_M * 2 * (HD / 4) : 1];   // [row][k, v][d4]
+    // new row of this forward at cache position pos, or -1 (rows sit at
+    // min(n_past + m, n_ctx - 1); only a one-row forward is clamped)
+    auto new_row = [&](int pos) -> int {
+        int mn = pos - n_past;
+        if (mn >= M || pos >= n_ctx) mn = -1;
+        if (mn < 0 && n_past >= n_ctx && pos == n_ctx - 1) mn = 0;
+        return mn;
+    };
     if constexpr (QKV) {
         constexpr int Q4 = HD / 4, QS = Q4 + 1;                      // float4 per row, padded stride
         __shared__ float4 s_q[16 * QS];
-        __shared__ float4 s_new[VX_ATT_MFMA_MAX_M * 2 * Q4];        // [row][k, v][d4]
         constexpr int QI = 16 * Q4 / ATT_THREADS;                  // q items per thread (1 or 2)
         {
             int row[QI], col[QI], pr[QI], rp[QI];
@@ -520,27 +540,15 @@ __device__ __forceinline__ void vx_attention_mfma_body(
 #pragma unroll
         for (int j = 0; j < NJ; j++) qv[j] = s_q[n * QS + 4 * j + r];
         if (has_new) {
-            auto new_row = [&](int pos) -> int {
-                int mn = pos - n_past;
-                if (mn >= M || pos >= n_ctx) mn = -1;
-                if (mn < 0 && n_past >= n_ctx && pos == n_ctx - 1) mn = 0;
-                return mn;
-            };
 #pragma unroll
             for (int pg = 0; pg < 2; pg++) {
                 const int mn = new_row(t0 + 16 * pg + n);
                 if (mn >= 0)
 #pragma unroll
                     for (int j = 0; j < NJ; j++) kr[pg][j] = s_new[(mn * 2) * Q4 + 4 * j + r];
-#pragma unroll
-                for (int st = 0; st < 4; st++) {
-                    const int mv = new_row(t0 + 16 * pg + 4 * r + st);
-                    if (mv >= 0)
-#pragma unroll
-                        for (int u = 0; u < NV4; u++) vr[pg][st][u] = s_new[(mv * 2 + 1) * Q4 + n + 16 * u];
-                }
             }
         }
+        has_new_wg = has_new;
     }
     if (ch >= n_chunks_w) return;
     if (!attend) return;
@@ -557,6 +565,18 @@ __device__ __forceinline__ void vx_attention_mfma_body(
             S[pg] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[pg][j].z, qv[j].z, S[pg], 0, 0, 0);
             S[pg] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[pg][j].w, qv[j].w, S[pg], 0, 0, 0);
         }
+    }
+    if constexpr (HD != 64) load_v();
+    if (QKV && has_new_wg) {
+#pragma unroll
+        for (int pg = 0; pg < 2; pg++)
+#pragma unroll
+            for (int st = 0; st < 4; st++) {
+                const int mv = new_row(t0 + 16 * pg + 4 * r + st);
+                if (mv >= 0)
+#pragma unroll
+                    for (int u = 0; u < NV4; u++) vr[pg][st][u] = s_new[(mv * 2 + 1) * (HD / 4) + n + 16 * u];
+            }
     }
     // chunk softmax statistics of query n (src/tensor.c:156-171 per chunk)
     float sc[2][4];
@@ -623,7 +643,7 @@ __global__ __launch_bounds__(ATT_THREADS) __attribute__((amdgpu_waves_per_eu(3))
 }
 
 template <int HD>
-__global__ __launch_bounds__(ATT_THREADS) __attribute__((amdgpu_waves_per_eu(HD == 64 ? 3 : 2))) void vx_attention_mfma_qkv_kernel(
+__global__ __launch_bounds__(ATT_THREADS) __attribute__((amdgpu_waves_per_eu(3))) void vx_attention_mfma_qkv_kernel(
     const float *__restrict__ q, int M, int n_past, int n_ctx, int n_heads, int n_kv, int cap,
     float *__restrict__ kc, float *__restrict__ vc, int n_chunks, int n_chunks_w, int n_qg,
     float *__restrict__ part, vx_qkv_args qa)
