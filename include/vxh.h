@@ -439,6 +439,12 @@ int vxh_row_stats(const float *L, int ldl, int R, int V, float T, float *stats, 
  * means all tokens. */
 int vxh_sample(const float *l, int V, float T, float top_p, const float *u_dev,
                int *token_out, float *nuc, vxh_stream s);
+/* vxh_sample that also leaves a copy of l[0..V) in keep (device, or NULL):
+ * the draft loop keeps each draft row for the verify decision without a
+ * separate copy launch (src/speculative.c:167 stores the draft's logits
+ * per drafted token). */
+int vxh_sample_keep(const float *l, int V, float T, float top_p, const float *u_dev,
+                    int *token_out, float *nuc, float *keep, vxh_stream s);
 /* Verify decisions for k drafts (src/speculative.c:186-233 on probabilities):
  * L: target logits [k+1][ldl] with their vxh_row_stats, D: draft logits
  * [k][ldd] with nucleus descriptors nuc[k][8], drafts[k], uniforms u[k+1]

@@ -326,6 +326,7 @@ def bind_vxh(L):
     L.vxh_download.argtypes = [vp, vp, C.c_size_t, vp]
     L.vxh_row_stats.argtypes = [vp, C.c_int, C.c_int, C.c_int, C.c_float, vp, vp]
     L.vxh_sample.argtypes = [vp, C.c_int, C.c_float, C.c_float, vp, vp, vp, vp]
+    L.vxh_sample_keep.argtypes = [vp, C.c_int, C.c_float, C.c_float, vp, vp, vp, vp, vp]
     L.vxh_accept.argtypes = [vp, C.c_int, C.c_int, vp, vp, C.c_int, C.c_int, vp, vp, C.c_int,
                              C.c_float, vp, vp, vp]
     L.vxh_stream_sync.argtypes = [vp]

@@ -93,6 +93,28 @@ def test_sampler_matches_oracle(P, V, T, top_p):
     assert ties <= 2
 
 
+@pytest.mark.parametrize("V,T,top_p", [(32000, 0.8, 1.0), (1001, 0.0, 1.0), (5000, 0.7, 0.5), (40000, 1.0, 1.0)])
+def test_sample_keep_copies_the_row_and_draws_like_sample(P, V, T, top_p):
+    """vxh_sample_keep = vxh_sample plus a copy of the row (register sampler:
+    the copy is stored as the row is loaded; other cases: a device copy)."""
+    print(f"sample_keep V={V} T={T} top_p={top_p}", flush=True)
+    rng = np.random.default_rng(V + 7)
+    l = rng.normal(0, 2.0, V).astype(np.float32)
+    dl, du = N.DevBuf(P, l), N.DevBuf(P, np.array([0.37], np.float32))
+    keep = N.DevBuf(P, np.full(V + 4, -7.0, np.float32))
+    bufs = [N.DevBuf(P, nbytes=4) for _ in range(2)] + [N.DevBuf(P, nbytes=32) for _ in range(2)]
+    assert P.vxh_sample(dl.ptr, V, T, top_p, du.ptr, bufs[0].ptr, bufs[2].ptr, None) == 0, P.vxh_last_error()
+    assert P.vxh_sample_keep(dl.ptr, V, T, top_p, du.ptr, bufs[1].ptr, bufs[3].ptr, keep.ptr, None) == 0, \
+        P.vxh_last_error()
+    assert P.vxh_stream_sync(None) == 0
+    got = keep.get(np.float32, V + 4)
+    assert np.array_equal(got[:V], l) and np.all(got[V:] == -7.0)
+    assert bufs[0].get(np.int32, 1)[0] == bufs[1].get(np.int32, 1)[0]
+    assert np.array_equal(bufs[2].get(np.uint32, 8), bufs[3].get(np.uint32, 8))
+    for b in [dl, du, keep] + bufs:
+        b.free()
+
+
 def run_accept(P, L, D, drafts, T, top_p, u):
     k = D.shape[0]
     V, Vd = L.shape[1], D.shape[1]

@@ -129,3 +129,38 @@ __device__ __forceinline__ float vx_wave_sum64(float v)
     v += vx_dpp<0x140>(v);
     return vx_sum_x32(vx_sum_x16(v));
 }
+
+// The same sum for fp64 values (each 32-bit half moved by the same DPP or
+// swap, so the halves stay paired); exact for integers below 2^53.
+template <int CTRL>
+__device__ __forceinline__ double vx_dpp_f64(double v)
+{
+    const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+    const int lo = (int)(unsigned)b, hi = (int)(unsigned)(b >> 32);
+    const unsigned nlo = (unsigned)__builtin_amdgcn_update_dpp(lo, lo, CTRL, 0xF, 0xF, false);
+    const unsigned nhi = (unsigned)__builtin_amdgcn_update_dpp(hi, hi, CTRL, 0xF, 0xF, false);
+    return __longlong_as_double((long long)(((unsigned long long)nhi << 32) | nlo));
+}
+
+template <bool X32>
+__device__ __forceinline__ double vx_sum_swap_f64(double v)
+{
+    const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+    const unsigned lo = (unsigned)b, hi = (unsigned)(b >> 32);
+    const auto rl = X32 ? __builtin_amdgcn_permlane32_swap(lo, lo, false, false)
+                        : __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+    const auto rh = X32 ? __builtin_amdgcn_permlane32_swap(hi, hi, false, false)
+                        : __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+    const double a = __longlong_as_double((long long)(((unsigned long long)rh[0] << 32) | rl[0]));
+    const double c = __longlong_as_double((long long)(((unsigned long long)rh[1] << 32) | rl[1]));
+    return a + c;
+}
+
+__device__ __forceinline__ double vx_wave_sum64_f64(double v)
+{
+    v += vx_dpp_f64<0xB1>(v);
+    v += vx_dpp_f64<0x4E>(v);
+    v += vx_dpp_f64<0x141>(v);
+    v += vx_dpp_f64<0x140>(v);
+    return vx_sum_swap_f64<true>(vx_sum_swap_f64<false>(v));
+}

@@ -12,17 +12,22 @@
 
 #define SB 1024   // threads per sampling workgroup
 
-// round(w * 2^32) as (uint64)(w * 2^32 + 0.5) in fp64, computed in fp32:
-// w * 2^32 is exact; below 2^23 adding 0.5 is exact too and truncation gives
-// the same floor, from 2^23 on the product is already an integer.  Masses of
-// 2^32 and more (w >= 1) take the fp64 expression itself.
+// round(w * 2^32) = floor(w * 2^32 + 0.5), exactly, in fp32 arithmetic, for
+// the probabilities and residual masses every caller passes (0 <= w <= 1):
+// x = w * 2^32 is exact; below 0.5 the result is 0; from 0.5 to 2^23 the sum
+// x + 0.5 is either exact (same binade as x) or lies in the next binade
+// below x's next integer, so truncation gives the floor; from 2^23 on x is
+// an integer.  w = 1 gives 2^32 (larger w saturate there); NaN gives 0.
 __device__ __forceinline__ uint64_t vx_fixed32(float w)
 {
-    if (!(w > 0.0f)) return 0ull;
-    float x = w * 4294967296.0f;
-    if (x >= 4294967296.0f) return (uint64_t)((double)w * 4294967296.0 + 0.5);
-    if (x < 8388608.0f) x += 0.5f;
-    return (uint64_t)(uint32_t)x;
+    // straight-line selects: unrolled over a thread's entries, early returns
+    // became a branch per entry
+    const float x = w * 4294967296.0f;
+    float r = x < 8388608.0f ? x + 0.5f : x;
+    r = x >= 0.5f ? r : 0.0f;
+    const bool top = x >= 4294967296.0f;
+    const uint32_t lo = top ? 0u : (uint32_t)fminf(r, 4294967040.0f);
+    return ((uint64_t)(top ? 1u : 0u) << 32) | lo;
 }
 
 // --- workgroup reductions (SB threads, 16 waves) ----------------------------
@@ -302,10 +307,10 @@ __global__ __launch_bounds__(SB) void vx_sample_kernel(const float *__restrict__
     }
 }
 
-// The sampler without a nucleus for V <= SB * SE: thread t owns the
-// contiguous entries [t*SE, t*SE + SE), loaded once; exponentials, masses and
-// the inverse-CDF prefix stay in registers (one wavefront-shuffle scan and
-// one LDS exchange instead of passes over the row).  Same arithmetic as
+// The sampler without a nucleus for V <= SB * SE: each thread loads its SE
+// entries once; exponentials and masses stay in registers, the inverse-CDF
+// search uses per-wavefront totals and one lane scan in the wavefront where
+// the threshold lands (no passes over the row).  Same arithmetic as
 // vx_sample_kernel with top_p = 1.
 #define SE 32
 
@@ -315,32 +320,71 @@ __device__ __forceinline__ uint64_t vx_shfl_up_u64(uint64_t v, int o)
     return ((uint64_t)hi << 32) | lo;
 }
 
+// Wave-blocked entries: wavefront w owns entries [2048 w, 2048 w + 2048)
+// (SB * SE = 32768 at most); its load j (0..7) covers entries 256 j ..
+// 256 j + 255 of that block, 4 consecutive ones per lane, so each load and
+// store of a wavefront is one contiguous KB (a thread owning 32 consecutive
+// entries made every float4 access of a wavefront touch 64 cache lines, and
+// the row's 128 KB thrashed the CU's L1).  In index order a wavefront's
+// entries run j-major, then lane, then the lane's 4 entries.
+#define SJ (SE / 4)
+
 __global__ __launch_bounds__(SB) void vx_sample_reg_kernel(const float *__restrict__ l, int V, float T,
                                                            const float *__restrict__ u,
                                                            int *__restrict__ token_out,
-                                                           float *__restrict__ nuc)
+                                                           float *__restrict__ nuc,
+                                                           float *__restrict__ keep)
 {
     __shared__ float redv[SB / 64];
     __shared__ int redi[SB / 64];
-    __shared__ uint64_t wsum[SB / 64];
+    __shared__ double wsum[SB / 64];
     __shared__ int res;
-    const int b = threadIdx.x * SE, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int b = wave * (64 * SE) + 4 * lane;   // entry (j, c) of this lane: b + 256 j + c
     float x[SE];
-    if (b + SE <= V) {
+    if (wave * (64 * SE) + 64 * SE <= V) {
 #pragma unroll
-        for (int j = 0; j < SE / 4; j++) {
-            const float4 v = *(const float4 *)(l + b + 4 * j);
+        for (int j = 0; j < SJ; j++) {
+            const float4 v = *(const float4 *)(l + b + 256 * j);
             x[4 * j] = v.x; x[4 * j + 1] = v.y; x[4 * j + 2] = v.z; x[4 * j + 3] = v.w;
         }
-    } else {
+        if (keep) {
 #pragma unroll
-        for (int j = 0; j < SE; j++) x[j] = b + j < V ? l[b + j] : 0.0f;
+            for (int j = 0; j < SJ; j++)
+                *(float4 *)(keep + b + 256 * j) = make_float4(x[4 * j], x[4 * j + 1], x[4 * j + 2], x[4 * j + 3]);
+        }
+    } else {
+        // the block holding entry V-1 and the ones after it: entries past V
+        // read as -inf, so they never win the argmax and their exp is 0
+#pragma unroll
+        for (int j = 0; j < SJ; j++)
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const int v = b + 256 * j + c;
+                const float t = l[min(v, V - 1)];
+                x[4 * j + c] = v < V ? t : -INFINITY;
+            }
+        if (keep) {
+#pragma unroll
+            for (int j = 0; j < SJ; j++)
+#pragma unroll
+                for (int c = 0; c < 4; c++)
+                    if (b + 256 * j + c < V) keep[b + 256 * j + c] = x[4 * j + c];
+        }
     }
     float bv = -INFINITY;
     int bi = 0x7fffffff;
 #pragma unroll
-    for (int j = 0; j < SE; j++)
-        if (b + j < V && (x[j] > bv || (x[j] == bv && b + j < bi))) { bv = x[j]; bi = b + j; }
+    for (int j = 0; j < SJ; j++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            // bitwise, not short-circuit: selects instead of a branch per entry
+            const int v = b + 256 * j + c;
+            const float t = x[4 * j + c];
+            const bool better = (v < V) & ((t > bv) | ((t == bv) & (v < bi)));
+            bv = better ? t : bv;
+            bi = better ? v : bi;
+        }
     float amv;
     bool amf;
     const int am = vx_wg_argmax(bv, bi, redv, redi, &amv, &amf);
@@ -356,45 +400,77 @@ __global__ __launch_bounds__(SB) void vx_sample_reg_kernel(const float *__restri
     float sum = 0.0f;
 #pragma unroll
     for (int j = 0; j < SE; j++) {
-        x[j] = b + j < V ? expf((x[j] - mx) / T) : 0.0f;
+        x[j] = expf((x[j] - mx) / T);
         sum += x[j];
     }
     sum = vx_wg_sum(sum, redv);
     const float inv = 1.0f / (sum + 1e-30f);
-    uint64_t St = 0;
+    // fixed-point masses; partial sums are integers far below 2^53, so the
+    // fp64 reductions are exact and order-free
+    uint64_t lt = 0;
 #pragma unroll
     for (int j = 0; j < SE; j++) {
         x[j] *= inv;                      // p_v = expf((l_v - max)/T) * inv
-        St += vx_fixed32(x[j]);
+        lt += vx_fixed32(x[j]);
     }
-    // exclusive prefix of the per-thread masses in index order
-    uint64_t incl = St;
-    for (int o = 1; o < 64; o <<= 1) {
-        const uint64_t y = vx_shfl_up_u64(incl, o);
-        if (lane >= o) incl += y;
-    }
-    if (lane == 63) wsum[wave] = incl;
+    const double wt = vx_wave_sum64_f64((double)lt);
+    if (lane == 0) wsum[wave] = wt;
     if (threadIdx.x == 0) res = am;
     __syncthreads();
-    uint64_t off = 0, S = 0;
+    double off = 0.0, Sd = 0.0;
     for (int w = 0; w < SB / 64; w++) {
         if (w < wave) off += wsum[w];
-        S += wsum[w];
+        Sd += wsum[w];
     }
+    const uint64_t S = (uint64_t)Sd;
     if (S > 0) {
         const uint64_t thr = vx_threshold(u[0], S);
-        const uint64_t before = off + incl - St;
-        if (before < thr && before + St >= thr) {
-            // first entry whose inclusive prefix reaches thr
-            uint64_t c = before;
-            int tok = b + SE - 1;
-            bool found = false;
+        const uint64_t before = (uint64_t)off;
+        if (before < thr && before + (uint64_t)wt >= thr) {
+            // the landing wavefront: which of its loads, then which lane,
+            // then which of the lane's 4 entries first reaches thr
+            uint64_t acc = before, acc_j = before;
+            int js = SJ - 1;
+            bool fj = false;
 #pragma unroll
-            for (int j = 0; j < SE; j++) {
-                c += vx_fixed32(x[j]);
-                if (!found && c >= thr) { tok = b + j; found = true; }
+            for (int j = 0; j < SJ; j++) {
+                uint64_t sj = 0;
+#pragma unroll
+                for (int c = 0; c < 4; c++) sj += vx_fixed32(x[4 * j + c]);
+                const uint64_t tj = (uint64_t)vx_wave_sum64_f64((double)sj);
+                const bool hit = !fj & (acc + tj >= thr);
+                js = hit ? j : js;
+                acc_j = hit ? acc : acc_j;
+                fj = fj | hit;
+                acc += tj;
             }
-            res = tok;
+            float p[4] = {x[0], x[1], x[2], x[3]};
+#pragma unroll
+            for (int j = 1; j < SJ; j++)
+#pragma unroll
+                for (int c = 0; c < 4; c++) p[c] = js == j ? x[4 * j + c] : p[c];
+            uint64_t s = 0;
+#pragma unroll
+            for (int c = 0; c < 4; c++) s += vx_fixed32(p[c]);
+            uint64_t incl = s;
+            for (int o = 1; o < 64; o <<= 1) {
+                const uint64_t y = vx_shfl_up_u64(incl, o);
+                if (lane >= o) incl += y;
+            }
+            const uint64_t bl = acc_j + incl - s;
+            if (bl < thr && bl + s >= thr) {
+                uint64_t c = bl;
+                int tok = b + 256 * js + 3;
+                bool found = false;
+#pragma unroll
+                for (int cc = 0; cc < 4; cc++) {
+                    c += vx_fixed32(p[cc]);
+                    const bool hit = !found & (c >= thr);
+                    tok = hit ? b + 256 * js + cc : tok;
+                    found = found | hit;
+                }
+                res = tok;
+            }
         }
     }
     __syncthreads();
@@ -406,29 +482,50 @@ __global__ __launch_bounds__(SB) void vx_sample_reg_kernel(const float *__restri
     }
 }
 
+extern "C" int vxh_sample_keep(const float *l, int V, float T, float top_p, const float *u_dev,
+                               int *token_out, float *nuc, float *keep, vxh_stream s)
+{
+    if (V <= 0) return vxh_fail(VXH_ERR_PARAM, "sample: V %d", V);
+    if (keep == l) keep = nullptr;
+    if (!(top_p < 1.0f) && V <= SB * SE && ((uintptr_t)l & 15) == 0 && ((uintptr_t)keep & 15) == 0) {
+        // the register sampler stores the row into keep as it loads it
+        vx_sample_reg_kernel<<<1, SB, 0, vxh_hs(s)>>>(l, V, T, u_dev, token_out, nuc, keep);
+    } else {
+        if (keep) VXH_CHECK(hipMemcpyAsync(keep, l, sizeof(float) * (size_t)V, hipMemcpyDeviceToDevice, vxh_hs(s)));
+        vx_sample_kernel<<<1, SB, 0, vxh_hs(s)>>>(l, V, T, top_p, u_dev, token_out, nuc);
+    }
+    VXH_LAUNCHED();
+    return VXH_OK;
+}
+
 extern "C" int vxh_sample(const float *l, int V, float T, float top_p, const float *u_dev,
                           int *token_out, float *nuc, vxh_stream s)
 {
-    if (V <= 0) return vxh_fail(VXH_ERR_PARAM, "sample: V %d", V);
-    if (!(top_p < 1.0f) && V <= SB * SE && ((uintptr_t)l & 15) == 0)
-        vx_sample_reg_kernel<<<1, SB, 0, vxh_hs(s)>>>(l, V, T, u_dev, token_out, nuc);
-    else
-        vx_sample_kernel<<<1, SB, 0, vxh_hs(s)>>>(l, V, T, top_p, u_dev, token_out, nuc);
-    VXH_LAUNCHED();
-    return VXH_OK;
+    return vxh_sample_keep(l, V, T, top_p, u_dev, token_out, nuc, nullptr, s);
 }
 
 // ---------------------------------------------------------------------------
 // verify decisions
 // ---------------------------------------------------------------------------
-// q_j(v) of the draft: the renormalised nucleus of softmax(D_j/T).
+// q_j(v) of the draft: the renormalised nucleus of softmax(D_j/T), from the
+// draft logit dv = D_j[v] and the row's nucleus descriptor.
+struct vx_nuc {
+    float mx, inv, tau, mass;
+    int tie;
+};
+__device__ __forceinline__ vx_nuc vx_nuc_load(const float *nuc)
+{
+    return {nuc[0], nuc[1], nuc[2], nuc[4], __float_as_int(nuc[3])};
+}
+__device__ __forceinline__ float vx_draft_q_of(float dv, const vx_nuc &n, int v, float T)
+{
+    const float p = expf((dv - n.mx) / T) * n.inv;
+    const bool in = (n.tau < 0.0f) | (p > n.tau) | ((p == n.tau) & (v <= n.tie));
+    return in ? p / n.mass : 0.0f;
+}
 __device__ __forceinline__ float vx_draft_q(const float *d, const float *nuc, int v, float T)
 {
-    float p = expf((d[v] - nuc[0]) / T) * nuc[1];
-    float tau = nuc[2];
-    int tie = __float_as_int(nuc[3]);
-    bool in = tau < 0.0f || p > tau || (p == tau && v <= tie);
-    return in ? p / nuc[4] : 0.0f;
+    return vx_draft_q_of(d[v], vx_nuc_load(nuc), v, T);
 }
 
 // One pass over the decided row: thread t sums the fixed-point masses of its
@@ -576,10 +673,9 @@ __global__ __launch_bounds__(SB) void vx_accept_kernel(const float *__restrict__
 
 // vx_accept_kernel for V <= SB * SE: the ratio tests of the k drafts run on
 // k lanes at once (the first rejection is the first failing lane, as in the
-// sequential scan), and thread t computes the probabilities of its
-// contiguous entries [t*SE, t*SE + SE) of the decided row once, keeping them
-// in registers for the mass, the inverse-CDF scan and the argmax fallback.
-// Same arithmetic as vx_accept_kernel.
+// sequential scan); the decided row is read once, wave-blocked and
+// coalesced, for its total mass, and only the wavefront where the inverse
+// CDF lands reads its entries again.  Same arithmetic as vx_accept_kernel.
 __global__ __launch_bounds__(SB) void vx_accept_reg_kernel(const float *__restrict__ L, int ldl, int V,
                                                            const float *__restrict__ stats,
                                                            const float *__restrict__ D, int ldd, int Vd,
@@ -589,7 +685,7 @@ __global__ __launch_bounds__(SB) void vx_accept_reg_kernel(const float *__restri
 {
     __shared__ float redv[SB / 64];
     __shared__ int redi[SB / 64];
-    __shared__ uint64_t wsum[SB / 64];
+    __shared__ double wsum[SB / 64];
     __shared__ int res;
     __shared__ int s_rej;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -619,66 +715,128 @@ __global__ __launch_bounds__(SB) void vx_accept_reg_kernel(const float *__restri
     const float *dj = D + (size_t)min(j, k - 1) * ldd;
     const float *nj = nuc + min(j, k - 1) * 8;
     const bool resample = j < k;
-    const int b = threadIdx.x * SE;
-    float w[SE];
+    const vx_nuc nq = vx_nuc_load(nj);
+    // wave-blocked entries as in vx_sample_reg_kernel: load j (0..SJ-1) of
+    // a lane covers entries b + 256 j .. b + 256 j + 3
+    const int b = wave * (64 * SE) + 4 * lane;
+    const bool vec = wave * (64 * SE) + 64 * SE <= min(V, Vd) &&
+                     (((uintptr_t)lj | (uintptr_t)dj) & 15) == 0;
+    // entries of load jj: the residual max(0, p - q) at a rejection, p for
+    // the bonus draw; 0 past V.  Straight-line loads with clamped addresses
+    // (a load inside a per-entry branch waits for itself); no per-entry
+    // array stays live, the one wavefront that needs entries again (landing
+    // search, argmax) recomputes them from L2.
+    auto entries4 = [&](int jj, float r[4]) {
+        const int v0 = b + 256 * jj;
+        float lv[4], dv[4];
+        if (vec) {
+            const float4 a4 = *(const float4 *)(lj + v0);
+            const float4 c4 = *(const float4 *)(dj + v0);
+            lv[0] = a4.x; lv[1] = a4.y; lv[2] = a4.z; lv[3] = a4.w;
+            dv[0] = c4.x; dv[1] = c4.y; dv[2] = c4.z; dv[3] = c4.w;
+        } else {
 #pragma unroll
-    for (int e = 0; e < SE; e++) {
-        const int v = b + e;
-        float r = 0.0f;
-        if (v < V) {
-            const float p = expf((lj[v] - mx) / T) * inv;
-            if (resample) {
-                const float q = v < Vd ? vx_draft_q(dj, nj, v, T) : 0.0f;
-                r = fmaxf(0.0f, p - q);
-            } else {
-                r = p;
+            for (int t = 0; t < 4; t++) {
+                lv[t] = lj[min(v0 + t, V - 1)];
+                dv[t] = dj[min(v0 + t, Vd - 1)];
             }
         }
-        w[e] = r;
-    }
-    uint64_t St = 0;
 #pragma unroll
-    for (int e = 0; e < SE; e++) St += vx_fixed32(w[e]);
-    uint64_t incl = St;
-    for (int o = 1; o < 64; o <<= 1) {
-        const uint64_t y = vx_shfl_up_u64(incl, o);
-        if (lane >= o) incl += y;
+        for (int t = 0; t < 4; t++) {
+            const int v = v0 + t;
+            const float p = expf((lv[t] - mx) / T) * inv;
+            const float q = v < Vd ? vx_draft_q_of(dv[t], nq, v, T) : 0.0f;
+            const float x = resample ? fmaxf(0.0f, p - q) : p;
+            r[t] = v < V ? x : 0.0f;
+        }
+    };
+    uint64_t lt = 0;
+#pragma unroll
+    for (int jj = 0; jj < SJ; jj++) {
+        float r[4];
+        entries4(jj, r);
+#pragma unroll
+        for (int t = 0; t < 4; t++) lt += vx_fixed32(r[t]);
     }
-    if (lane == 63) wsum[wave] = incl;
+    // fixed-point partial sums are integers far below 2^53: exact in fp64
+    const double wt = vx_wave_sum64_f64((double)lt);
+    if (lane == 0) wsum[wave] = wt;
     __syncthreads();
-    uint64_t off = 0, S = 0;
+    double off = 0.0, Sd = 0.0;
     for (int wv = 0; wv < SB / 64; wv++) {
         if (wv < wave) off += wsum[wv];
-        S += wsum[wv];
+        Sd += wsum[wv];
     }
+    const uint64_t S = (uint64_t)Sd;
     int tok;
     if (S == 0) {
         if (resample) {
             // no residual mass: argmax of the residual (first index on ties)
             float bv = -INFINITY;
             int bi = 0x7fffffff;
+            for (int jj = 0; jj < SJ; jj++) {
+                float r[4];
+                entries4(jj, r);
 #pragma unroll
-            for (int e = 0; e < SE; e++)
-                if (b + e < V && (w[e] > bv || (w[e] == bv && b + e < bi))) { bv = w[e]; bi = b + e; }
+                for (int t = 0; t < 4; t++) {
+                    const int v = b + 256 * jj + t;
+                    const bool better = (v < V) & ((r[t] > bv) | ((r[t] == bv) & (v < bi)));
+                    bv = better ? r[t] : bv;
+                    bi = better ? v : bi;
+                }
+            }
             tok = vx_wg_argmax(bv, bi, redv, redi);
         } else {
             tok = __float_as_int(stats[j * 3 + 2]);
         }
     } else {
         const uint64_t thr = vx_threshold(u[k], S);
-        const uint64_t before = off + incl - St;
+        const uint64_t before = (uint64_t)off;
         if (threadIdx.x == 0) res = V - 1;
         __syncthreads();
-        if (before < thr && before + St >= thr) {
-            uint64_t c = before;
-            int t = b + SE - 1;
-            bool found = false;
+        if (before < thr && before + (uint64_t)wt >= thr) {
+            // the landing wavefront: which load, then which lane, then
+            // which of the lane's 4 entries first reaches thr
+            uint64_t acc = before, acc_j = before;
+            int js = SJ - 1;
+            bool fj = false;
+            for (int jj = 0; jj < SJ; jj++) {
+                float r[4];
+                entries4(jj, r);
+                uint64_t sj = 0;
 #pragma unroll
-            for (int e = 0; e < SE; e++) {
-                c += vx_fixed32(w[e]);
-                if (!found && c >= thr) { t = b + e; found = true; }
+                for (int t = 0; t < 4; t++) sj += vx_fixed32(r[t]);
+                const uint64_t tj = (uint64_t)vx_wave_sum64_f64((double)sj);
+                const bool hit = !fj & (acc + tj >= thr);
+                js = hit ? jj : js;
+                acc_j = hit ? acc : acc_j;
+                fj = fj | hit;
+                acc += tj;
             }
-            res = t;
+            float r[4];
+            entries4(js, r);
+            uint64_t sl = 0;
+#pragma unroll
+            for (int t = 0; t < 4; t++) sl += vx_fixed32(r[t]);
+            uint64_t incl = sl;
+            for (int o = 1; o < 64; o <<= 1) {
+                const uint64_t y = vx_shfl_up_u64(incl, o);
+                if (lane >= o) incl += y;
+            }
+            const uint64_t bl = acc_j + incl - sl;
+            if (bl < thr && bl + sl >= thr) {
+                uint64_t c = bl;
+                int t_hit = b + 256 * js + 3;
+                bool found = false;
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    c += vx_fixed32(r[t]);
+                    const bool hit = !found & (c >= thr);
+                    t_hit = hit ? b + 256 * js + t : t_hit;
+                    found = found | hit;
+                }
+                res = t_hit;
+            }
         }
         __syncthreads();
         tok = res;

@@ -211,9 +211,8 @@ int vx_speculative_decode(vx_speculative_state *s, int *output, int max_tokens)
                     CHK(vxh_copy(dd->tok, s->dtok + i, sizeof(int), dd->stream));
                     CHKE(vx_dev_forward(dm, 1, n + i - 1, VX_LOGITS_LAST));
                 }
-                CHK(vxh_copy(s->D + (size_t)i * Vd, dd->logits, sizeof(float) * (size_t)Vd, dd->stream));
-                CHK(vxh_sample(s->D + (size_t)i * Vd, Vd, T, s->top_p, s->u_draft + i, s->dtok + 1 + i,
-                               s->nuc + 8 * i, dd->stream));
+                CHK(vxh_sample_keep(dd->logits, Vd, T, s->top_p, s->u_draft + i, s->dtok + 1 + i,
+                                    s->nuc + 8 * i, s->D + (size_t)i * Vd, dd->stream));
             }
             CHK(vxh_stream_sync(dd->stream));
         }
