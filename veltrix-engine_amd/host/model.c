@@ -1054,6 +1054,17 @@ static vx_error forward_pro(vx_model *m, int M, int n_past, int logits_mode)
  * next kernel consumes (and clears): q|k|v -> RoPE/KV write, attention
  * output projection and down projection -> the residual + RMSNorm panel of
  * the next block, gate/up -> the SwiGLU panel, logits -> a store. */
+vx_error vx_dev_forward_ids(vx_model *m, const int *ids, int M, int n_past, int logits_mode)
+{
+    vx_dev *d = vx_dev_of(m);
+    if (!d || !ids) return VX_ERR_PARAM;
+    int *own = d->tok;
+    d->tok = (int *)ids;   /* read by the embedding gather only */
+    vx_error e = vx_dev_forward(m, M, n_past, logits_mode);
+    d->tok = own;
+    return e;
+}
+
 vx_error vx_dev_forward(vx_model *m, int M, int n_past, int logits_mode)
 {
     vx_dev *d = vx_dev_of(m);

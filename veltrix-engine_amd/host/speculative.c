@@ -207,10 +207,7 @@ int vx_speculative_decode(vx_speculative_state *s, int *output, int max_tokens)
             for (int i = 0; i < kk; i++) s->uh[i] = vx_uniform(s->seed, 1, (uint64_t)round * k + i);
             CHK(vxh_upload(s->u_draft, s->uh, sizeof(float) * (size_t)kk, dd->stream));
             for (int i = 0; i < kk; i++) {
-                if (i > 0) {
-                    CHK(vxh_copy(dd->tok, s->dtok + i, sizeof(int), dd->stream));
-                    CHKE(vx_dev_forward(dm, 1, n + i - 1, VX_LOGITS_LAST));
-                }
+                if (i > 0) CHKE(vx_dev_forward_ids(dm, s->dtok + i, 1, n + i - 1, VX_LOGITS_LAST));
                 CHK(vxh_sample_keep(dd->logits, Vd, T, s->top_p, s->u_draft + i, s->dtok + 1 + i,
                                     s->nuc + 8 * i, s->D + (size_t)i * Vd, dd->stream));
             }
@@ -221,8 +218,7 @@ int vx_speculative_decode(vx_speculative_state *s, int *output, int max_tokens)
 
         /* verify: one target forward over [t0, d_0 .. d_{kk-1}] */
         CHK(vxh_upload(s->dtok, &t_last, sizeof(int), td->stream));
-        CHK(vxh_copy(td->tok, s->dtok, sizeof(int) * (size_t)(kk + 1), td->stream));
-        CHKE(vx_dev_forward(tm, kk + 1, n - 1, VX_LOGITS_ALL));
+        CHKE(vx_dev_forward_ids(tm, s->dtok, kk + 1, n - 1, VX_LOGITS_ALL));
         CHK(vxh_row_stats(td->logits, Vt, kk + 1, Vt, T, td->stats, td->stream));
         for (int j = 0; j < kk; j++) s->uh[j] = vx_uniform(s->seed, 2, (uint64_t)round * (k + 1) + j);
         /* the resample / bonus draw always uses the stream's slot k */

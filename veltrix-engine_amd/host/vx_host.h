@@ -118,6 +118,9 @@ typedef struct vx_dev {
  * logits land in dev->logits ([M][V] for ALL, row 0 for LAST).  Does not
  * touch cache_len. */
 vx_error vx_dev_forward(vx_model *m, int M, int n_past, int logits_mode);
+/* vx_dev_forward over M token ids already in device memory (ids[0..M)),
+ * instead of the model's own token buffer: no copy launch. */
+vx_error vx_dev_forward_ids(vx_model *m, const int *ids, int M, int n_past, int logits_mode);
 /* Host-token convenience: uploads tokens, runs all batches, advances
  * cache_len with the reference's clamp rule. */
 vx_error vx_dev_run_tokens(vx_model *m, const int *tokens, int n, int logits_mode,
