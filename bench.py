@@ -233,6 +233,15 @@ def run_spec(args):
     tm = synth_model(N, P, TARGET, 4096, 1001)
     dm = synth_model(N, P, DRAFT, 4096, 2002)
     log(f"models created in HBM: {time.perf_counter() - t0:.1f} s")
+    if args.kv_half:
+        # the flagged fp16 KV-cache mode of both models (not the headline
+        # configuration: the reference keeps its cache in fp32)
+        for m in (tm, dm):
+            opt = N.VxModelOptions()
+            P.vx_model_get_options(m, C.byref(opt))
+            opt.kv_half = 1
+            if P.vx_model_set_options(m, C.byref(opt)) != 0:
+                sys.exit("bench.py: fp16 KV cache refused: " + N.product_error())
     st = P.vx_speculative_create(dm, tm, args.k)
     if not st:
         sys.exit("bench.py: vx_speculative_create failed")
@@ -314,6 +323,7 @@ def run_spec(args):
                          f"k={args.k} drafts of a 22L d2048 32/4-head FFN5632 Q4_0 draft; prompt "
                          f"{args.prompt}, {args.tokens} tokens per step, T=0.8 top_p=1.0"),
             "k": args.k, "prompt": args.prompt, "tokens_per_step": args.tokens,
+            "kv_cache": "f16 (flagged mode)" if args.kv_half else "f32",
             "acceptance_rate": round(tot["accepted"] / max(tot["drafted"], 1), 4),
             "rounds_per_step": round(tot["rounds"] / args.steps, 1),
             "seeds": f"uniform seeds 4243..{4242 + args.steps}, one per step",
@@ -704,6 +714,8 @@ def main():
     ap.add_argument("--k", type=int, default=8)
     ap.add_argument("--mode", choices=["spec", "gemm", "configs"], default="spec")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kv-half", action="store_true",
+                    help="spec mode: both models with the flagged fp16 KV cache (not the headline)")
     ap.add_argument("--prof-every", type=int, default=7,
                     help="time every n-th verify GEMM of each class with kernel events")
     args = ap.parse_args()

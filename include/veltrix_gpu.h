@@ -52,6 +52,11 @@ typedef struct {
                                   (AVX2-lane mode always uses separate kernels)       */
     int pro_max_rows;          /* VX_FUSED_PROLOGUE: forwards of more rows use the
                                   separate row kernels                                 */
+    int kv_half;               /* 1: IEEE fp16 KV cache (flagged mode; the reference
+                                  keeps fp32); needs VX_FUSED_PROLOGUE, VX_Q4_EXACT,
+                                  pro_max_rows >= 16 and head_dim 64 or 128.  Changing
+                                  it drops the cache (cache_len 0); k_cache/v_cache
+                                  then hold halves                                    */
 } vx_model_options;
 
 #define VX_FUSED_NONE 0        /* separate row kernels (11 launches per layer)          */

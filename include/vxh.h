@@ -401,6 +401,25 @@ int vxh_attention_parts_qkv(double *qkv, int ld_qkv, const double *ss, int ss_K,
                             float *k_cache_layer, float *v_cache_layer, vxh_workspace *ws,
                             int *n_chunks, vxh_stream s);
 
+/* vxh_attention_qkv / vxh_attention_parts_qkv over an IEEE fp16 KV cache
+ * (k/v_cache_layer: [n_ctx][n_kv_heads * head_dim] halves, 8-byte aligned):
+ * the new rows are rounded to nearest even when stored, and this forward's
+ * own rows are attended to as rounded, so a batch and the same rows one at
+ * a time see the same keys and values.  A flagged mode (the reference keeps
+ * fp32, src/model.c:291-296, :404-411), for head_dim 64 or 128 and at most
+ * VXH_ATTN_QKV_FAST_ROWS rows; it halves the attention's cache bytes. */
+int vxh_attention_qkv_f16(double *qkv, int ld_qkv, const double *ss, int ss_K, const float *bq,
+                          const float *bk, const float *bv, const float *cos_tab, const float *sin_tab,
+                          int n_pos, int M, int n_past, int n_ctx, int n_heads, int n_kv_heads,
+                          int head_dim, int cap, uint16_t *k_cache_layer, uint16_t *v_cache_layer,
+                          float *out, int ld_out, vxh_workspace *ws, vxh_stream s);
+int vxh_attention_parts_qkv_f16(double *qkv, int ld_qkv, const double *ss, int ss_K, const float *bq,
+                                const float *bk, const float *bv, const float *cos_tab,
+                                const float *sin_tab, int n_pos, int M, int n_past, int n_ctx,
+                                int n_heads, int n_kv_heads, int head_dim, int cap,
+                                uint16_t *k_cache_layer, uint16_t *v_cache_layer, vxh_workspace *ws,
+                                int *n_chunks, vxh_stream s);
+
 /* vxh_attention whose second launch also builds the output projection's
  * x-panel p (K = n_heads * head_dim, one scale per row): the last head of
  * each row to finish reads the row back and writes its panel.  row_counters:

@@ -433,6 +433,27 @@ static void apply_norm(float *x, float *tmp, const float *w, int n, float *ones)
  * pos = cache_len (clamped to n_ctx-1), then every query head h reads kv head
  * h*n_kv/n_heads over positions [0, min(pos+1, cap)), cap = 4096 in the
  * reference (src/model.c:304-305). */
+/* binary16: 10 fraction bits, normal exponents -14..15, subnormal quantum
+ * 2^-24, largest finite 65504; values from 65520 on round to infinity.
+ * Scaling by powers of two is exact, nearbyint rounds ties to even. */
+float or_round_half(float x)
+{
+    if (x != x) return x;
+    double a = fabs((double)x);
+    if (a == 0.0) return x;
+    double q;
+    if (a < 0x1p-14) {
+        q = 0x1p-24;
+    } else {
+        int e;
+        frexp(a, &e);                /* a = f * 2^e, f in [0.5, 1) */
+        q = ldexp(1.0, e - 1 - 10);
+    }
+    double r = nearbyint(a / q) * q;
+    if (r > 65504.0) r = INFINITY;
+    return (float)(x < 0 ? -r : r);
+}
+
 static void attention(or_model *m, const float *q, const float *k, const float *v,
                       float *out, int layer, float *scores)
 {
@@ -445,6 +466,12 @@ static void attention(or_model *m, const float *q, const float *k, const float *
     size_t loff = (size_t)layer * (size_t)max_ctx * kvd;
     memcpy(m->k_cache + loff + (size_t)pos * kvd, k, sizeof(float) * (size_t)kvd);
     memcpy(m->v_cache + loff + (size_t)pos * kvd, v, sizeof(float) * (size_t)kvd);
+    if (m->kv_half)
+        for (int i = 0; i < kvd; i++) {
+            float *kr = m->k_cache + loff + (size_t)pos * kvd, *vr = m->v_cache + loff + (size_t)pos * kvd;
+            kr[i] = or_round_half(kr[i]);
+            vr[i] = or_round_half(vr[i]);
+        }
     memset(out, 0, sizeof(float) * (size_t)nh * hd);
     int cs = cache_size;
     if (m->attn_cap > 0 && cs > m->attn_cap) cs = m->attn_cap;

@@ -84,7 +84,14 @@ typedef struct {
     const float *const *bq, *const *bk, *const *bv;   /* optional F32 biases      */
     float *k_cache, *v_cache;   /* [n_layers][n_ctx][kv_dim], caller-owned        */
     int cache_len;
+    int kv_half;                /* 1: rows rounded to IEEE fp16 (nearest even) as
+                                   they are stored -- the GPU engine's flagged fp16
+                                   KV mode; 0 (the reference): fp32                 */
 } or_model;
+
+/* x rounded to the nearest IEEE binary16 value (ties to even), as fp32:
+ * overflow gives +-inf, NaN stays NaN. */
+float or_round_half(float x);
 
 /* Sequential single-token forwards over tokens[0..n); writes the last token's
  * logits (src/model.c:391-628).  Returns 0 or a negative error. */

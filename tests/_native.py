@@ -77,6 +77,7 @@ class OrModel(C.Structure):
         ("attn_norm", C.c_void_p), ("ffn_norm", C.c_void_p),
         ("bq", C.c_void_p), ("bk", C.c_void_p), ("bv", C.c_void_p),
         ("k_cache", C.c_void_p), ("v_cache", C.c_void_p), ("cache_len", C.c_int),
+        ("kv_half", C.c_int),
     ]
 
 
@@ -90,6 +91,8 @@ def oracle():
     if "oracle" not in _libs:
         L = C.CDLL(ORACLE_SO)
         L.or_fp16_to_fp32.restype = C.c_float
+        L.or_round_half.argtypes = [C.c_float]
+        L.or_round_half.restype = C.c_float
         L.or_fp16_to_fp32.argtypes = [C.c_uint16]
         L.or_fp32_to_fp16.restype = C.c_uint16
         L.or_fp32_to_fp16.argtypes = [C.c_float]
@@ -225,7 +228,7 @@ def max_violation(a, b, atol=1e-4, rtol=1e-3):
 # --------------------------------------------------------------------------
 class VxModelOptions(C.Structure):
     _fields_ = [("q4_kernel", C.c_int), ("attn_cap", C.c_int), ("ffn_gate_threshold", C.c_float),
-                ("fused", C.c_int), ("pro_max_rows", C.c_int)]
+                ("fused", C.c_int), ("pro_max_rows", C.c_int), ("kv_half", C.c_int)]
 
 
 class VxSynthSpec(C.Structure):

@@ -30,7 +30,7 @@ class OracleModel:
 
     def __init__(self, weights, n_layers, n_embd, n_heads, n_kv_heads, n_ff, n_vocab, n_ctx,
                  rope_theta=10000.0, q4_mode=0, attn_cap=4096, attn_o_inplace=0, gate_thr=0.01,
-                 wscale=1.0):
+                 wscale=1.0, kv_half=0):
         self.keep = []
         hd = n_embd // n_heads
         kvd = n_kv_heads * hd
@@ -39,6 +39,7 @@ class OracleModel:
         m.n_head_dim, m.n_ff, m.n_vocab, m.n_ctx = hd, n_ff, n_vocab, n_ctx
         m.rope_theta, m.q4_mode, m.attn_cap, m.attn_o_inplace = rope_theta, q4_mode, attn_cap, attn_o_inplace
         m.gate_thr, m.wscale = gate_thr, wscale
+        m.kv_half = kv_half
 
         def W(name):
             a = weights.get(name)

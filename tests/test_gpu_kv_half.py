@@ -1,0 +1,98 @@
+"""The flagged fp16 KV-cache mode (vx_model_options.kv_half) against the
+oracle with the same rounding (or_model.kv_half: each stored K/V row rounded
+to the nearest binary16, ties to even): a verify batch after a GPU prefill,
+teacher-forced, at head_dim 64 (draft-shaped, the attention-in-attn_o path
+for one row) and 128 (target-shaped), to the same tolerance as the fp32
+cache.  The cache read back holds only binary16 values, and the mode is
+refused where a forward would take a kernel without it."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import _native as N
+from _native import close, max_violation
+from _oracle_model import OracleModel
+from test_gpu_configs import prefill, read_weights, synth
+
+pytestmark = pytest.mark.gpu
+O = N.oracle()
+
+
+@pytest.fixture(scope="module")
+def P():
+    if not N.product_available():
+        pytest.fail("product library not built")
+    L = N.bind_vxh(N.product())
+    assert L.vxh_init() == 0, L.vxh_last_error()
+    return L
+
+
+def set_kv_half(P, mp, on, **over):
+    opt = N.VxModelOptions()
+    P.vx_model_get_options(mp, C.byref(opt))
+    opt.kv_half = on
+    for k, v in over.items():
+        setattr(opt, k, v)
+    return P.vx_model_set_options(mp, C.byref(opt))
+
+
+@pytest.mark.parametrize("d,h,kv", [(256, 4, 2), (512, 4, 2)])
+def test_kv_half_verify_matches_oracle(P, d, h, kv):
+    L, F, V, n_ctx, n_past, k = 2, 512, 512, 256, 100, 4
+    hd = d // h
+    kvd = kv * hd
+    print(f"kv_half verify: d{d} {h}/{kv} heads (head_dim {hd}), {n_past} prefilled, k={k}", flush=True)
+    mp = synth(P, L, d, h, kv, F, V, n_ctx, seed=77 + d, thr=0.0)
+    try:
+        assert set_kv_half(P, mp, 1) == 0, N.product_error()
+        rng = np.random.default_rng(d)
+        toks = rng.integers(0, V, n_past + k + 1).astype(np.int32)
+        prefill(P, mp, toks[:n_past], V)
+        # one-row forward (attention combined inside attn_o), then roll back
+        one = prefill(P, mp, toks[n_past:n_past + 1], V)
+        P.vx_model_kv_truncate(mp, n_past)
+        got = np.zeros((k + 1, V), np.float32)
+        assert P.vx_model_verify(mp, toks[n_past:], k + 1, got) == 0, N.product_error()
+        P.vx_model_kv_truncate(mp, n_past)
+        w = read_weights(P, mp, L, d, kvd, F, V, 2, 2)
+        om = OracleModel(w, L, d, h, kv, F, V, n_ctx=n_ctx, attn_cap=4096, gate_thr=0.0, kv_half=1)
+        kc = om.k_cache.reshape(L, n_ctx, kvd)
+        vc = om.v_cache.reshape(L, n_ctx, kvd)
+        for l in range(L):
+            kk = np.zeros((n_past, kvd), np.float32)
+            vv = np.zeros((n_past, kvd), np.float32)
+            assert P.vx_model_read_kv(mp, l, n_past, kk, vv) == 0, N.product_error()
+            # the cache holds binary16 values only
+            assert np.array_equal(kk, kk.astype(np.float16).astype(np.float32))
+            assert np.array_equal(vv, vv.astype(np.float16).astype(np.float32))
+            assert np.abs(kk).max() > 0 and np.abs(vv).max() > 0
+            kc[l, :n_past] = kk
+            vc[l, :n_past] = vv
+    finally:
+        P.vx_model_destroy(mp)
+    om.cache_len = n_past
+    ref = np.zeros((k + 1, V), np.float32)
+    assert O.or_forward_all(om.ptr, toks[n_past:], k + 1, ref) == 0
+    diff = np.abs(got.astype(np.float64) - ref)
+    print(f"max |diff| {diff.max():.3e}; one-row forward vs verify row 0 {np.abs(one - got[0]).max():.3e}")
+    assert close(got, ref), max_violation(got, ref)
+    assert close(one, ref[0]), max_violation(one, ref[0])
+
+
+def test_kv_half_refused_where_unsupported(P):
+    mp = synth(P, 1, 256, 4, 2, 512, 512, 64, seed=9)
+    try:
+        # forwards of more rows would take the separate row kernels (fp32 cache only)
+        assert set_kv_half(P, mp, 1, pro_max_rows=1) != 0
+        assert set_kv_half(P, mp, 1, fused=0) != 0
+        assert set_kv_half(P, mp, 2) != 0
+        assert set_kv_half(P, mp, 1) == 0, N.product_error()
+        assert set_kv_half(P, mp, 0) == 0, N.product_error()
+    finally:
+        P.vx_model_destroy(mp)
+    mp = synth(P, 1, 384, 4, 2, 512, 512, 64, seed=9)   # head_dim 96
+    try:
+        assert set_kv_half(P, mp, 1) != 0
+    finally:
+        P.vx_model_destroy(mp)

@@ -368,7 +368,45 @@ __device__ __forceinline__ float4 vx_keep4(bool ok, float4 v)
     return make_float4(ok ? v.x : 0.0f, ok ? v.y : 0.0f, ok ? v.z : 0.0f, ok ? v.w : 0.0f);
 }
 
-template <bool QKV, int HD>
+// KV cache rows in fp32 (KH = false, the reference's cache) or IEEE fp16
+// (KH = true, a flagged mode: round to nearest even on store, exact widening
+// on load).  i is an element index, a multiple of 4.
+template <bool KH>
+__device__ __forceinline__ float4 vx_kv_load4(const float *base, size_t i)
+{
+    if constexpr (KH) {
+        const uint2 h = *(const uint2 *)((const uint16_t *)base + i);
+        return make_float4(vx_half_bits_to_float(h.x & 0xFFFFu), vx_half_bits_to_float(h.x >> 16),
+                           vx_half_bits_to_float(h.y & 0xFFFFu), vx_half_bits_to_float(h.y >> 16));
+    } else {
+        return *(const float4 *)(base + i);
+    }
+}
+__device__ __forceinline__ uint32_t vx_half_bits(float x)
+{
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);   // round to nearest even
+}
+// the value a KV row element holds after a store and a load
+template <bool KH>
+__device__ __forceinline__ float4 vx_kv_round4(float4 v)
+{
+    if constexpr (KH)
+        return make_float4(vx_half_bits_to_float(vx_half_bits(v.x)), vx_half_bits_to_float(vx_half_bits(v.y)),
+                           vx_half_bits_to_float(vx_half_bits(v.z)), vx_half_bits_to_float(vx_half_bits(v.w)));
+    else
+        return v;
+}
+template <bool KH>
+__device__ __forceinline__ void vx_kv_store4(float *base, size_t i, float4 v)
+{
+    if constexpr (KH)
+        *(uint2 *)((uint16_t *)base + i) = make_uint2(vx_half_bits(v.x) | (vx_half_bits(v.y) << 16),
+                                                      vx_half_bits(v.z) | (vx_half_bits(v.w) << 16));
+    else
+        *(float4 *)(base + i) = v;
+}
+
+template <bool QKV, int HD, bool KH = false>
 __device__ __forceinline__ void vx_attention_mfma_body(
     const float *__restrict__ q, int M, int n_past, int n_ctx, int n_heads, int n_kv, int cap,
     float *__restrict__ kc, float *__restrict__ vc, int n_chunks, int n_chunks_w, int n_qg,
@@ -404,7 +442,7 @@ __device__ __forceinline__ void vx_attention_mfma_body(
             const int pos = t0 + 16 * pg + n;
             const size_t off = (size_t)min(pos, n_ctx - 1) * kvd + g * HD + 4 * r;
 #pragma unroll
-            for (int j = 0; j < NJ; j++) kr[pg][j] = *(const float4 *)(kc + off + 16 * j);
+            for (int j = 0; j < NJ; j++) kr[pg][j] = vx_kv_load4<KH>(kc, off + 16 * j);
         }
 #pragma unroll
         for (int pg = 0; pg < 2; pg++) {
@@ -421,7 +459,7 @@ __device__ __forceinline__ void vx_attention_mfma_body(
                 const int pv = t0 + 16 * pg + 4 * r + st;
                 const size_t ov = (size_t)min(pv, n_ctx - 1) * kvd + g * HD + 4 * n;
 #pragma unroll
-                for (int u = 0; u < NV4; u++) vr[pg][st][u] = *(const float4 *)(vc + ov + 64 * u);
+                for (int u = 0; u < NV4; u++) vr[pg][st][u] = vx_kv_load4<KH>(vc, ov + 64 * u);
             }
 #pragma unroll
         for (int pg = 0; pg < 2; pg++)
@@ -528,10 +566,11 @@ __device__ __forceinline__ void vx_attention_mfma_body(
                 for (int u = 0; u < 2; u++) {
                     const int it = it0 + u * ATT_THREADS;
                     if (it >= M * 2 * Q4) continue;
-                    s_new[it] = o[u];
+                    // the new rows as the cache holds them (fp16 mode: rounded)
+                    s_new[it] = vx_kv_round4<KH>(o[u]);
                     if (qg == 0) {
                         const int kind = (it / Q4) % 2, pos = min(n_past + row[u], n_ctx - 1);
-                        *(float4 *)((kind ? vc : kc) + (size_t)pos * kvd + el[u]) = o[u];
+                        vx_kv_store4<KH>(kind ? vc : kc, (size_t)pos * kvd + el[u], o[u]);
                     }
                 }
             }
@@ -642,13 +681,13 @@ __global__ __launch_bounds__(ATT_THREADS) __attribute__((amdgpu_waves_per_eu(3))
                                       n_qg, part, qa);
 }
 
-template <int HD>
+template <int HD, bool KH = false>
 __global__ __launch_bounds__(ATT_THREADS) __attribute__((amdgpu_waves_per_eu(3))) void vx_attention_mfma_qkv_kernel(
     const float *__restrict__ q, int M, int n_past, int n_ctx, int n_heads, int n_kv, int cap,
     float *__restrict__ kc, float *__restrict__ vc, int n_chunks, int n_chunks_w, int n_qg,
     float *__restrict__ part, vx_qkv_args qa)
 {
-    vx_attention_mfma_body<true, HD>(q, M, n_past, n_ctx, n_heads, n_kv, cap, kc, vc, n_chunks, n_chunks_w,
+    vx_attention_mfma_body<true, HD, KH>(q, M, n_past, n_ctx, n_heads, n_kv, cap, kc, vc, n_chunks, n_chunks_w,
                                      n_qg, part, qa);
 }
 
@@ -839,8 +878,11 @@ static int vx_attention_run(const float *q, const vx_qkv_args *qa, long n_clr, i
                             int n_ctx, int n_heads, int n_kv_heads, int head_dim, int cap, float *kc,
                             float *vc, float *out, int ld_out, vxh_workspace *ws,
                             unsigned *row_counters, vxh_xpanel *xp, int parts_only, int *n_chunks_out,
-                            vxh_stream s)
+                            vxh_stream s, int kv_half = 0)
 {
+    if (kv_half && (!qa || (head_dim != 64 && head_dim != 128) || M > VX_ATT_MFMA_MAX_M))
+        return vxh_fail(VXH_ERR_UNSUPPORTED, "attention: an fp16 KV cache needs the q|k|v kernel, head_dim "
+                        "64 or 128 and at most %d rows (head_dim %d, %d rows)", VX_ATT_MFMA_MAX_M, head_dim, M);
     if (M < 1 || n_kv_heads < 1 || n_heads % n_kv_heads)
         return vxh_fail(VXH_ERR_PARAM, "attention: M %d heads %d kv %d", M, n_heads, n_kv_heads);
     if (head_dim % 4 || head_dim > ATT_MAX_HD)
@@ -868,7 +910,15 @@ static int vx_attention_run(const float *q, const vx_qkv_args *qa, long n_clr, i
         const int nqg = (QM + 15) / 16, ncg = (n_chunks_w + 3) / 4;
         const int grid = n_kv_heads * nqg * ncg;
         const vx_qkv_args &A = qa ? *qa : none;
-        if (head_dim == 64 && qa)
+        if (kv_half && head_dim == 64)
+            vx_attention_mfma_qkv_kernel<64, true><<<grid, ATT_THREADS, 0, vxh_hs(s)>>>(
+                nullptr, M, n_past, n_ctx, n_heads, n_kv_heads, cap, kc, vc, n_chunks, n_chunks_w, nqg,
+                ws->part, A);
+        else if (kv_half)
+            vx_attention_mfma_qkv_kernel<128, true><<<grid, ATT_THREADS, 0, vxh_hs(s)>>>(
+                nullptr, M, n_past, n_ctx, n_heads, n_kv_heads, cap, kc, vc, n_chunks, n_chunks_w, nqg,
+                ws->part, A);
+        else if (head_dim == 64 && qa)
             vx_attention_mfma_qkv_kernel<64><<<grid, ATT_THREADS, 0, vxh_hs(s)>>>(
                 nullptr, M, n_past, n_ctx, n_heads, n_kv_heads, cap, kc, vc, n_chunks, n_chunks_w, nqg,
                 ws->part, A);
@@ -921,7 +971,7 @@ static int vx_attention_qkv(double *qkv, int ld_qkv, const double *ss, int ss_K,
                             const float *bk, const float *bv, const float *cos_tab, const float *sin_tab,
                             int n_pos, int M, int n_past, int n_ctx, int n_heads, int n_kv_heads,
                             int head_dim, int cap, float *kc, float *vc, float *out, int ld_out,
-                            vxh_workspace *ws, int *n_chunks_out, vxh_stream s)
+                            vxh_workspace *ws, int *n_chunks_out, vxh_stream s, int kv_half = 0)
 {
     if (!qkv || ((uintptr_t)qkv & 15) || ld_qkv % 2 || M < 1 || n_kv_heads < 1 ||
         ld_qkv < (n_heads + 2 * n_kv_heads) * head_dim)
@@ -943,7 +993,7 @@ static int vx_attention_qkv(double *qkv, int ld_qkv, const double *ss, int ss_K,
     qa.sn = sin_tab;
     return vx_attention_run(nullptr, &qa, (long)M * ld_qkv, M, n_past, n_ctx, n_heads, n_kv_heads,
                             head_dim, cap, kc, vc, out, ld_out, ws, nullptr, nullptr, n_chunks_out != nullptr,
-                            n_chunks_out, s);
+                            n_chunks_out, s, kv_half);
 }
 
 extern "C" int vxh_attention_qkv(double *qkv, int ld_qkv, const double *ss, int ss_K, const float *bq,
@@ -966,6 +1016,32 @@ extern "C" int vxh_attention_parts_qkv(double *qkv, int ld_qkv, const double *ss
     if (!n_chunks) return vxh_fail(VXH_ERR_PARAM, "attention_parts_qkv: n_chunks output missing");
     return vx_attention_qkv(qkv, ld_qkv, ss, ss_K, bq, bk, bv, cos_tab, sin_tab, n_pos, M, n_past, n_ctx,
                             n_heads, n_kv_heads, head_dim, cap, kc, vc, nullptr, 0, ws, n_chunks, s);
+}
+
+extern "C" int vxh_attention_qkv_f16(double *qkv, int ld_qkv, const double *ss, int ss_K, const float *bq,
+                                     const float *bk, const float *bv, const float *cos_tab,
+                                     const float *sin_tab, int n_pos, int M, int n_past, int n_ctx,
+                                     int n_heads, int n_kv_heads, int head_dim, int cap, uint16_t *kc,
+                                     uint16_t *vc, float *out, int ld_out, vxh_workspace *ws, vxh_stream s)
+{
+    if (((uintptr_t)kc | (uintptr_t)vc) & 7) return vxh_fail(VXH_ERR_PARAM, "attention_qkv_f16: cache alignment");
+    return vx_attention_qkv(qkv, ld_qkv, ss, ss_K, bq, bk, bv, cos_tab, sin_tab, n_pos, M, n_past, n_ctx,
+                            n_heads, n_kv_heads, head_dim, cap, (float *)kc, (float *)vc, out, ld_out, ws,
+                            nullptr, s, 1);
+}
+
+extern "C" int vxh_attention_parts_qkv_f16(double *qkv, int ld_qkv, const double *ss, int ss_K,
+                                           const float *bq, const float *bk, const float *bv,
+                                           const float *cos_tab, const float *sin_tab, int n_pos, int M,
+                                           int n_past, int n_ctx, int n_heads, int n_kv_heads, int head_dim,
+                                           int cap, uint16_t *kc, uint16_t *vc, vxh_workspace *ws,
+                                           int *n_chunks, vxh_stream s)
+{
+    if (!n_chunks) return vxh_fail(VXH_ERR_PARAM, "attention_parts_qkv_f16: n_chunks output missing");
+    if (((uintptr_t)kc | (uintptr_t)vc) & 7) return vxh_fail(VXH_ERR_PARAM, "attention_parts_qkv_f16: cache alignment");
+    return vx_attention_qkv(qkv, ld_qkv, ss, ss_K, bq, bk, bv, cos_tab, sin_tab, n_pos, M, n_past, n_ctx,
+                            n_heads, n_kv_heads, head_dim, cap, (float *)kc, (float *)vc, nullptr, 0, ws,
+                            n_chunks, s, 1);
 }
 
 extern "C" int vxh_attention_xpanel(const float *q, int M, int n_past, int n_ctx, int n_heads,

@@ -293,10 +293,11 @@ vx_error vx_dev_ensure_kv(vx_model *m)
         return VX_OK;
     }
     size_t per = (size_t)(d->n_layers > 0 ? d->n_layers : 1) * n_ctx * d->kvd;
-    TRY(vxh_malloc((void **)&m->k_cache, per * sizeof(float)));
-    TRY(vxh_malloc((void **)&m->v_cache, per * sizeof(float)));
-    TRY(vxh_fill_f32(m->k_cache, 0.0f, per, d->stream));
-    TRY(vxh_fill_f32(m->v_cache, 0.0f, per, d->stream));
+    const size_t esz = d->opt.kv_half ? 2 : sizeof(float);   /* kvd is even: whole floats */
+    TRY(vxh_malloc((void **)&m->k_cache, per * esz));
+    TRY(vxh_malloc((void **)&m->v_cache, per * esz));
+    TRY(vxh_fill_f32(m->k_cache, 0.0f, per * esz / sizeof(float), d->stream));
+    TRY(vxh_fill_f32(m->v_cache, 0.0f, per * esz / sizeof(float), d->stream));
     d->n_ctx_alloc = n_ctx;
     /* RoPE angle table for positions 0..n_ctx, computed like the reference
      * (src/tensor.c:182-187) */
@@ -641,7 +642,29 @@ vx_error vx_model_set_options(vx_model *m, const vx_model_options *opt)
     if (opt->attn_cap < 0) return VX_ERR_PARAM;
     if (opt->fused < VX_FUSED_NONE || opt->fused > VX_FUSED_PROLOGUE || opt->pro_max_rows < 0)
         return VX_ERR_PARAM;
+    if (opt->kv_half != 0 && opt->kv_half != 1) return VX_ERR_PARAM;
+    if (opt->kv_half) {
+        /* every forward must take the q|k|v attention kernel, the only one
+         * with an fp16 cache */
+        int has_o = 1;
+        for (int l = 0; l < d->n_layers; l++) has_o &= d->layers[l].has_o;
+        if (opt->fused != VX_FUSED_PROLOGUE || opt->q4_kernel != VX_Q4_EXACT || opt->pro_max_rows < VX_MAX_BATCH ||
+            (d->hd != 64 && d->hd != 128) || !has_o) {
+            vx_set_error("fp16 KV cache: needs the prologue path, exact Q4_0, pro_max_rows >= %d and "
+                         "head_dim 64 or 128", VX_MAX_BATCH);
+            return VX_ERR_UNSUPPORTED;
+        }
+    }
     int cap_changed = opt->attn_cap != d->opt.attn_cap;
+    int kv_changed = opt->kv_half != d->opt.kv_half;
+    if (kv_changed && m->k_cache) {
+        /* a cache of the other element type: dropped, allocated again by the next forward */
+        TRY(vxh_stream_sync(d->stream));
+        vxh_free(m->k_cache);
+        vxh_free(m->v_cache);
+        m->k_cache = m->v_cache = NULL;
+        m->cache_len = 0;
+    }
     d->opt = *opt;
     if (cap_changed && m->k_cache) return dev_alloc_workspace(d, d->n_ctx_alloc, d->opt.attn_cap);
     return VX_OK;
@@ -952,8 +975,10 @@ static vx_error forward_pro(vx_model *m, int M, int n_past, int logits_mode)
     vxh_pro p;
     for (int l = 0; l < L; l++) {
         vx_dev_layer *Ld = &d->layers[l];
-        float *kc = m->k_cache + (size_t)l * n_ctx * kvd;
-        float *vc = m->v_cache + (size_t)l * n_ctx * kvd;
+        const int kvh = d->opt.kv_half;
+        const size_t kv_off = (size_t)l * n_ctx * kvd;
+        float *kc = m->k_cache + kv_off, *vc = m->v_cache + kv_off;
+        uint16_t *kh = (uint16_t *)m->k_cache + kv_off, *vh = (uint16_t *)m->v_cache + kv_off;
         memset(&p, 0, sizeof(p));
         p.kind = VXH_PRO_RESID;
         p.x = d->x; p.ldx = dd;
@@ -968,21 +993,33 @@ static vx_error forward_pro(vx_model *m, int M, int n_past, int logits_mode)
         if (attn_in_o) {
             /* partials of the attention, combined by the output projection */
             int n_chunks = 0;
-            TRY(vxh_attention_parts_qkv(d->acc_qkv, d->ld_qkv, SS(l, 0), dd, Ld->bq, Ld->bk, Ld->bv,
-                                        d->rope_cos, d->rope_sin, d->n_pos, M, n_past, n_ctx, d->n_heads,
-                                        d->n_kv, d->hd, d->opt.attn_cap, kc, vc, &d->ws, &n_chunks, s));
+            if (kvh)
+                TRY(vxh_attention_parts_qkv_f16(d->acc_qkv, d->ld_qkv, SS(l, 0), dd, Ld->bq, Ld->bk, Ld->bv,
+                                                d->rope_cos, d->rope_sin, d->n_pos, M, n_past, n_ctx,
+                                                d->n_heads, d->n_kv, d->hd, d->opt.attn_cap, kh, vh, &d->ws,
+                                                &n_chunks, s));
+            else
+                TRY(vxh_attention_parts_qkv(d->acc_qkv, d->ld_qkv, SS(l, 0), dd, Ld->bq, Ld->bk, Ld->bv,
+                                            d->rope_cos, d->rope_sin, d->n_pos, M, n_past, n_ctx, d->n_heads,
+                                            d->n_kv, d->hd, d->opt.attn_cap, kc, vc, &d->ws, &n_chunks, s));
             p.kind = VXH_PRO_ATTN;
             p.part = d->ws.part; p.n_chunks = n_chunks;
             p.n_heads = d->n_heads; p.n_kv_heads = d->n_kv; p.head_dim = d->hd;
             p.clear = d->acc_qkv; p.n_clear = (size_t)M * d->ld_qkv;
         } else if (M <= VXH_ATTN_QKV_FAST_ROWS && (d->hd == 64 || d->hd == 128)) {
             /* RoPE and the new k/v rows inside the attention's first launch */
-            TRY(vxh_attention_qkv(d->acc_qkv, d->ld_qkv, SS(l, 0), dd, Ld->bq, Ld->bk, Ld->bv, d->rope_cos,
-                                  d->rope_sin, d->n_pos, M, n_past, n_ctx, d->n_heads, d->n_kv, d->hd,
-                                  d->opt.attn_cap, kc, vc, d->att, dd, &d->ws, s));
+            if (kvh)
+                TRY(vxh_attention_qkv_f16(d->acc_qkv, d->ld_qkv, SS(l, 0), dd, Ld->bq, Ld->bk, Ld->bv,
+                                          d->rope_cos, d->rope_sin, d->n_pos, M, n_past, n_ctx, d->n_heads,
+                                          d->n_kv, d->hd, d->opt.attn_cap, kh, vh, d->att, dd, &d->ws, s));
+            else
+                TRY(vxh_attention_qkv(d->acc_qkv, d->ld_qkv, SS(l, 0), dd, Ld->bq, Ld->bk, Ld->bv,
+                                      d->rope_cos, d->rope_sin, d->n_pos, M, n_past, n_ctx, d->n_heads,
+                                      d->n_kv, d->hd, d->opt.attn_cap, kc, vc, d->att, dd, &d->ws, s));
             p.kind = VXH_PRO_ROWS;
             p.x = d->att; p.ldx = dd;
         } else {
+            if (kvh) return VX_ERR_UNSUPPORTED;   /* excluded by vx_model_set_options */
             TRY(vxh_rope_kv_norm(d->acc_qkv, d->ld_qkv, M, n_past, n_ctx, d->n_heads, d->n_kv, d->hd,
                                  Ld->bq, Ld->bk, Ld->bv, d->rope_cos, d->rope_sin, d->n_pos, SS(l, 0), dd,
                                  d->q, kc, vc, s));
@@ -1070,6 +1107,7 @@ vx_error vx_dev_forward(vx_model *m, int M, int n_past, int logits_mode)
     vx_dev *d = vx_dev_of(m);
     if (M < 1 || M > VX_MAX_BATCH) return VX_ERR_PARAM;
     if (pro_ok(d, M)) return forward_pro(m, M, n_past, logits_mode);
+    if (d->opt.kv_half) return VX_ERR_UNSUPPORTED;   /* fp16 caches: prologue path only */
     if (fused_ok(d)) return forward_fused(m, M, n_past, logits_mode);
     const int dd = d->d, kvd = d->kvd, F = d->F, V = d->V, n_ctx = d->n_ctx_alloc;
     const int avx2 = d->opt.q4_kernel == VX_Q4_AVX2_LANES;
@@ -1248,7 +1286,23 @@ vx_error vx_model_read_kv(const vx_model *m, int layer, int n, float *k, float *
     if (!d || !m->k_cache || layer < 0 || layer >= d->n_layers || n < 0 || n > d->n_ctx_alloc)
         return VX_ERR_PARAM;
     size_t off = (size_t)layer * d->n_ctx_alloc * d->kvd;
-    size_t bytes = sizeof(float) * (size_t)n * d->kvd;
+    size_t cnt = (size_t)n * d->kvd;
+    if (d->opt.kv_half) {
+        /* halves widened exactly */
+        uint16_t *h = (uint16_t *)malloc(2 * (cnt ? cnt : 1));
+        if (!h) return VX_ERR_MEMORY;
+        vx_error e = VX_OK;
+        for (int w = 0; w < 2 && e == VX_OK; w++) {
+            float *dst = w ? v : k;
+            if (!dst) continue;
+            const uint16_t *src = (const uint16_t *)(w ? m->v_cache : m->k_cache) + off;
+            if (vxh_download(h, src, 2 * cnt, d->stream)) e = vx_from_vxh(-1);
+            for (size_t i = 0; e == VX_OK && i < cnt; i++) dst[i] = vx_fp16_to_fp32(h[i]);
+        }
+        free(h);
+        return e;
+    }
+    size_t bytes = sizeof(float) * cnt;
     if (k) TRY(vxh_download(k, m->k_cache + off, bytes, d->stream));
     if (v) TRY(vxh_download(v, m->v_cache + off, bytes, d->stream));
     return VX_OK;
