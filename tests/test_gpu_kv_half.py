@@ -96,3 +96,38 @@ def test_kv_half_refused_where_unsupported(P):
         assert set_kv_half(P, mp, 1) != 0
     finally:
         P.vx_model_destroy(mp)
+
+
+def test_kv_half_speculative_greedy_equals_target_greedy(P):
+    """Greedy speculative decoding with both caches in fp16 emits the target's
+    own greedy sequence (target-only forwards with the same fp16 cache), up
+    to the first near-tie of the target's logits."""
+    V, n_gen = 512, 32
+    print("kv_half speculative greedy: 2L target / 1L draft, d256 4/2 heads", flush=True)
+    tm = synth(P, 2, 256, 4, 2, 512, V, 256, seed=11, thr=0.0)
+    dm = synth(P, 1, 256, 4, 2, 512, V, 256, seed=12, thr=0.0)
+    tg = synth(P, 2, 256, 4, 2, 512, V, 256, seed=11, thr=0.0)
+    st = None
+    try:
+        for m in (tm, dm, tg):
+            assert set_kv_half(P, m, 1) == 0, N.product_error()
+        st = P.vx_speculative_create(dm, tm, 4)
+        assert st
+        P.vx_speculative_set_temp(st, 0.0, 1.0)
+        prompt = np.random.default_rng(3).integers(0, V, 12).astype(np.int32)
+        out = np.zeros(n_gen, np.int32)
+        assert P.vx_speculative_generate(st, prompt.copy(), len(prompt), out, n_gen) == n_gen, N.product_error()
+        lg = np.zeros(V, np.float32)
+        assert P.vx_model_forward(tg, prompt, len(prompt), lg) == 0, N.product_error()
+        for i in range(n_gen):
+            top2 = np.sort(lg)[-2:]
+            if top2[1] - top2[0] < 1e-4:
+                break   # certified tie: the sequences may part here
+            t = int(np.argmax(lg))
+            assert out[i] == t, (i, out[:i + 1])
+            assert P.vx_model_forward(tg, np.array([t], np.int32), 1, lg) == 0, N.product_error()
+    finally:
+        if st:
+            P.vx_speculative_destroy(st)
+        for m in (tm, dm, tg):
+            P.vx_model_destroy(m)
