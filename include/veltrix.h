@@ -177,6 +177,10 @@ void vx_model_destroy(vx_model *model);
 vx_error vx_model_forward(vx_model *model, const int *tokens, int n_tokens, float *logits);
 void vx_model_kv_truncate(vx_model *model, int length);
 void vx_set_compute_level(vx_compute_level level);
+/* include/veltrix.h:180 of the reference declares it and src/ defines it
+ * nowhere; here it is defined and ignored (meta-learning is not on the
+ * verify path). */
+void vx_enable_metalearn(bool enable);
 void vx_set_n_threads(int n);
 void vx_set_forward_timing_enabled(int enabled);
 void vx_print_forward_timing(void);

@@ -517,6 +517,38 @@ static void embed(const or_model *m, int token, float *x, float *tmp)
     memcpy(x, tmp + inblk, sizeof(float) * (size_t)stride);
 }
 
+/* Test hook: the FFN column of token ti, layer l whose |silu(g)| is closest to
+ * the skip threshold, and that distance. */
+static void gate_log(const or_model *m, const float *g, int F, int ti, int l)
+{
+    float best = INFINITY;
+    int bi = -1;
+    for (int i = 0; i < F; i++) {
+        float dist = fabsf(fabsf(g[i]) - m->gate_thr);
+        if (dist < best) { best = dist; bi = i; }
+    }
+    size_t at = (size_t)ti * m->n_layers + l;
+    if (m->gate_near) m->gate_near[at] = best;
+    if (m->gate_near_idx) m->gate_near_idx[at] = bi;
+}
+
+/* Test hook: invert the skip decision of column flip_col: a skipped up row is
+ * computed (the same row product as an unskipped one), a computed one is zero. */
+static void gate_flip(const or_model *m, const or_mat *w, const float *xn, const float *g, float *u,
+                      int F, int d, float *tmp)
+{
+    int i = m->flip_col;
+    if (!(fabsf(g[i]) < m->gate_thr)) { u[i] = 0.0f; return; }
+    if (!w->data) return;
+    or_mat row = *w;
+    size_t bsz = w->type == OR_TYPE_Q4_0 ? 18 : (w->type == OR_TYPE_Q8_0 ? 34 : 0);
+    if (bsz) row.data = (const uint8_t *)w->data + (size_t)i * ((size_t)(d + 31) / 32) * bsz;
+    else row.data = (const float *)w->data + (size_t)i * d;
+    row.rows = 1;
+    apply_mat(m, &row, xn, &u[i], 1, d, NULL, 0, 0, tmp);
+    (void)F;
+}
+
 static int forward_impl(or_model *m, const int *tokens, int n, float *logits, int all)
 {
     int d = m->n_embd, hd = m->n_head_dim, nh = m->n_heads, nkv = m->n_kv_heads;
@@ -599,6 +631,9 @@ static int forward_impl(or_model *m, const int *tokens, int n, float *logits, in
             apply_mat(m, &m->wg[l], xn, g, F, d, NULL, 0, 0, tmp);
             or_silu(g, F);
             apply_mat(m, &m->wu[l], xn, u, F, d, g, m->gate_thr, 0, tmp);
+            if (m->gate_near || m->gate_near_idx) gate_log(m, g, F, ti, l);
+            if (m->flip && m->flip_tok == ti && m->flip_layer == l && m->flip_col >= 0 && m->flip_col < F)
+                gate_flip(m, &m->wu[l], xn, g, u, F, d, tmp);
             for (int i = 0; i < F; i++) g[i] = g[i] * u[i];
             /* the down projection's tail is an unwritten pad in the reference
              * (src/model.c:432-433); it is read as zeros here */

@@ -87,6 +87,14 @@ typedef struct {
     int kv_half;                /* 1: rows rounded to IEEE fp16 (nearest even) as
                                    they are stored -- the GPU engine's flagged fp16
                                    KV mode; 0 (the reference): fp32                 */
+    /* Test hooks of the FFN gate-skip |silu(g_i)| < gate_thr (src/model.c:582-585;
+     * the reference has no such hooks).  They let a test prove that a logit
+     * difference comes from one skip decision that sits at the threshold. */
+    float *gate_near;           /* optional [n][n_layers] (n = tokens of the call):
+                                   min over FFN columns i of ||silu(g_i)| - gate_thr| */
+    int *gate_near_idx;         /* optional [n][n_layers]: the column i of that minimum */
+    int flip;                   /* 1: invert the skip decision of one column:          */
+    int flip_tok, flip_layer, flip_col;   /* token index within the call, layer, column */
 } or_model;
 
 /* x rounded to the nearest IEEE binary16 value (ties to even), as fp32:

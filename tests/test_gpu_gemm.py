@@ -141,4 +141,6 @@ def test_gemm_zero_and_one_hot(P):
     assert np.array_equal(Y[2].astype(np.float64), vals[:, 255])
     W["qs"][:] = 0x88
     X = rng.normal(0, 1, (2, cols)).astype(np.float32)
-    assert P.vx_gemm_q4_0(N._ptr(W), X, cols, Y[:2].copy(), 2, rows, cols, 0) == 0
+    out = np.full((2, rows), 7.0, np.float32)
+    assert P.vx_gemm_q4_0(N._ptr(W), X, cols, out, 2, rows, cols, 0) == 0
+    assert np.all(out == 0.0), np.abs(out).max()

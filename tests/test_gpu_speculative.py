@@ -8,8 +8,10 @@ Sampled (T > 0): every round is replayed on the oracle with the same seeded
 uniforms: the draft tokens must be the oracle sampler's draws from the draft
 model's logits, and the emitted tokens the oracle's acceptance decisions on the
 target's logits (teacher-forced over the committed sequence).  A divergence is
-accepted only as a certified tie (test_gpu_accept.py), after which the replay
-stops.
+accepted only as a certified tie: a uniform within 1e-5 of the acceptance
+ratio, or a draw whose CDF threshold sits within 1e-6 of the boundary between
+two neighbouring tokens.  The replay then follows the GPU's choice; an
+uncertified divergence fails.
 """
 import ctypes as C
 
@@ -19,6 +21,7 @@ import pytest
 import _native as N
 from _gguf import llama_gguf
 from _oracle_model import OracleModel
+from test_gpu_accept import near_boundary
 
 pytestmark = pytest.mark.gpu
 O = N.oracle()
@@ -164,13 +167,14 @@ def test_sampled_replay_matches_oracle(P, models, T, top_p):
 
     committed = list(prompt)
     emitted_total = []
-    ties = 0
+    ties = []
     for r in range(stats.rounds):
         n0 = len(committed)
         drafts = [int(t) for t in tr_d[r * k:(r + 1) * k] if t >= 0]
         kk = len(drafts)
         seq = committed + drafts
-        # draft model: logits for positions n0-1 .. n0-2+kk (teacher forced)
+        # draft model: logits for positions n0-1 .. n0-2+kk (teacher forced
+        # over the GPU's drafts, so a certified divergence does not stop the replay)
         Q = np.zeros((max(kk, 1), V), np.float32)
         if kk:
             dl = oracle_logits(draw, dsh, seq[:n0 - 1 + kk])
@@ -179,12 +183,9 @@ def test_sampled_replay_matches_oracle(P, models, T, top_p):
                 tok = O.or_sample_top_p(np.ascontiguousarray(dl[n0 - 1 + j]), V, T, top_p, float(u),
                                         Q[j].ctypes.data_as(C.c_void_p))
                 if tok != drafts[j]:
-                    ties += 1
-                    break
-            else:
-                tok = None
-            if tok is not None and tok != drafts[j]:
-                break   # certified divergence (checked in test_gpu_accept); stop replay
+                    assert certified_draw(Q[j], u, tok, drafts[j]), ("uncertified draft divergence", r, j,
+                                                                     tok, drafts[j])
+                    ties.append(("draft", r, j))
         tl = oracle_logits(traw, tsh, seq)[n0 - 1:n0 + kk]
         u = np.array([uniform(seed, 2, r * (k + 1) + j) for j in range(kk)] +
                      [uniform(seed, 2, r * (k + 1) + k)], np.float32)
@@ -193,13 +194,109 @@ def test_sampled_replay_matches_oracle(P, models, T, top_p):
         ne = O.or_accept_sampled(np.ascontiguousarray(tl.ravel()), V, np.ascontiguousarray(Q[:max(kk, 1)].ravel()),
                                  V, np.array(drafts + [0], np.int32), kk, T, u, o, C.byref(na))
         got = [int(t) for t in tr_e[r * (k + 1):(r + 1) * (k + 1)] if t >= 0]
-        if list(o[:ne]) != got:
-            ties += 1
-            break
-        assert na.value == tr_a[r]
+        if list(o[:ne]) != got or na.value != tr_a[r]:
+            assert certified_accept(tl, Q, drafts, T, u, got, int(tr_a[r]), list(o[:ne]), na.value), \
+                ("uncertified accept divergence", r, got, list(o[:ne]))
+            ties.append(("accept", r))
         committed += got
         emitted_total += got
-    print(f"rounds {stats.rounds}, accepted {stats.accepted}/{stats.drafted}, divergences {ties}")
-    assert ties <= 1
-    assert emitted_total == list(out[:len(emitted_total)])
-    assert len(emitted_total) >= n_gen // 2
+    print(f"rounds {stats.rounds}, accepted {stats.accepted}/{stats.drafted}, certified divergences {ties}")
+    assert len(ties) <= 2
+    assert len(emitted_total) >= n_gen
+    assert emitted_total[:n_gen] == list(out)
+
+
+def adjacent_in_support(w, a, b):
+    """a and b both carry mass and no token between them does."""
+    lo, hi = min(a, b), max(a, b)
+    return w[a] > 0 and w[b] > 0 and not np.any(w[lo + 1:hi] > 0)
+
+
+def certified_draw(w, u, tok_oracle, tok_gpu):
+    """A draw that differs only across one CDF boundary: the threshold of u sits
+    within 1e-6 of a prefix boundary (fp32 expf differences between the GPU and
+    the host libm move it) and the two tokens are neighbours in the support."""
+    w = np.asarray(w, np.float64)
+    return near_boundary(w, u) and adjacent_in_support(w, tok_oracle, tok_gpu)
+
+
+def certified_accept(tl, Q, drafts, T, u, got, na_g, want, na_o):
+    """Certificate for the first decision where the GPU round and the oracle
+    round differ: the ratio test (|u_j - alpha_j| < 1e-5), or the residual /
+    bonus draw across one CDF boundary."""
+    kk = len(drafts)
+    j = min(na_g, na_o)
+    V = tl.shape[1]
+    p = np.zeros(V, np.float32)
+    O.or_softmax_temp(np.ascontiguousarray(tl[j]), V, T, p)
+    if j < kk and na_g != na_o:
+        alpha = min(1.0, float(p[drafts[j]]) / max(float(Q[j][drafts[j]]), 1e-10))
+        return abs(float(u[j]) - alpha) < 1e-5
+    if j < kk:
+        w = np.maximum(0.0, p.astype(np.float64) - Q[j])
+    else:
+        w = p.astype(np.float64)
+    return len(got) == len(want) and got[:-1] == want[:-1] and certified_draw(w, float(u[kk]), want[-1], got[-1])
+
+
+def test_decode_after_a_dropped_cache_fails_before_launching(P, tmp_path):
+    """Changing kv_half drops a model's KV cache (and the prefilled rows with
+    it): decode must refuse with an error instead of running on a missing or
+    fresh cache."""
+    path = str(tmp_path / "hd64.gguf")
+    llama_gguf(path, np.random.default_rng(8), 1, 256, 4, 2, 256, 256, std=0.08)   # head_dim 64
+    tm, dm = load(P, path), load(P, path)
+    st = P.vx_speculative_create(dm, tm, 4)
+    try:
+        P.vx_speculative_set_temp(st, 0.0, 1.0)
+        prompt = np.arange(6, dtype=np.int32)
+        assert P.vx_speculative_prefill(st, prompt, 6) == 6
+        opt = N.VxModelOptions()
+        P.vx_model_get_options(tm, C.byref(opt))
+        opt.kv_half = 1
+        assert P.vx_model_set_options(tm, C.byref(opt)) == 0, N.product_error()
+        assert not tm.contents.k_cache
+        out = np.zeros(8, np.int32)
+        assert P.vx_speculative_decode(st, out, 8) == 0
+        assert "prefill again" in N.product_error()
+        # prefill again: decoding works on the new (fp16) cache
+        assert P.vx_speculative_prefill(st, prompt, 6) == 6
+        assert P.vx_speculative_decode(st, out, 8) == 8, N.product_error()
+    finally:
+        P.vx_speculative_destroy(st)
+        P.vx_model_destroy(tm)
+        P.vx_model_destroy(dm)
+
+
+def test_draft_context_smaller_than_target(P, models):
+    """The loop is bounded by the target's context only (src/speculative.c:244,
+    :257): once the draft's cache is full, rounds are target-only, and greedy
+    output still equals target-only greedy decoding."""
+    (tpath, traw, tsh), (dpath, draw, dsh) = models
+    V = tsh[5]
+    tm, dm = load(P, tpath), load(P, dpath)
+    dm.contents.config.n_ctx = 14          # 10 prompt positions + 4
+    st = P.vx_speculative_create(dm, tm, 4)
+    n_gen = 20
+    prompt = np.random.default_rng(15).integers(0, V, 10).astype(np.int32)
+    try:
+        P.vx_speculative_set_temp(st, 0.0, 1.0)
+        out = np.zeros(n_gen, np.int32)
+        assert P.vx_speculative_generate(st, prompt.copy(), len(prompt), out, n_gen) == n_gen, N.product_error()
+        stats = N.VxSpecStats()
+        P.vx_speculative_get_stats(st, C.byref(stats))
+        assert stats.drafted < 4 * stats.rounds      # some rounds ran without drafts
+        tg = load(P, tpath)
+        lg = np.zeros(V, np.float32)
+        assert P.vx_model_forward(tg, prompt, len(prompt), lg) == 0
+        ref = []
+        for _ in range(n_gen):
+            t = int(np.argmax(lg))
+            ref.append(t)
+            assert P.vx_model_forward(tg, np.array([t], np.int32), 1, lg) == 0
+        P.vx_model_destroy(tg)
+        assert list(out) == ref
+    finally:
+        P.vx_speculative_destroy(st)
+        P.vx_model_destroy(tm)
+        P.vx_model_destroy(dm)

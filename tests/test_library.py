@@ -157,3 +157,18 @@ def test_compute_entry_points_fail_loudly_without_gpu(P, tmp_path):
     llama_gguf(path, rng, 1, 64, 2, 1, 128, 50)
     mp = C.POINTER(N.VxModelDev)()
     assert P.vx_model_create(path.encode(), C.byref(mp)) != 0
+
+
+def test_integration_snippet_compiles_and_links(P, tmp_path):
+    """The C caller in INTEGRATION.md, written against the reference API,
+    compiles unchanged against include/ and links against the library."""
+    doc = open(os.path.join(N.REPO, "INTEGRATION.md")).read()
+    blocks = re.findall(r"```c\n(.*?)```", doc, flags=re.S)
+    assert blocks, "no C block in INTEGRATION.md"
+    src = tmp_path / "app.c"
+    src.write_text(blocks[0])
+    libdir = os.path.dirname(N.PRODUCT_SO)
+    r = subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", "-I", os.path.join(N.REPO, "include"),
+                        str(src), "-o", str(tmp_path / "app"), "-L", libdir, "-lveltrix_amd",
+                        "-Wl,-rpath," + libdir], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr

@@ -78,6 +78,7 @@ uint64_t vx_splitmix64(uint64_t x)
 }
 
 void vx_set_compute_level(vx_compute_level level) { g_level = level; }
+void vx_enable_metalearn(bool enable) { (void)enable; }   /* accepted, ignored */
 void vx_set_n_threads(int n) { (void)n; }   /* host threads do not matter here */
 
 void vx_set_forward_timing_enabled(int enabled)
@@ -299,6 +300,7 @@ vx_error vx_dev_ensure_kv(vx_model *m)
     TRY(vxh_fill_f32(m->k_cache, 0.0f, per * esz / sizeof(float), d->stream));
     TRY(vxh_fill_f32(m->v_cache, 0.0f, per * esz / sizeof(float), d->stream));
     d->n_ctx_alloc = n_ctx;
+    d->kv_gen++;
     /* RoPE angle table for positions 0..n_ctx, computed like the reference
      * (src/tensor.c:182-187) */
     int half = d->hd / 2;
@@ -315,6 +317,9 @@ vx_error vx_dev_ensure_kv(vx_model *m)
             sn[(size_t)p * half + i] = sinf(ang);
         }
     }
+    /* a cache dropped by vx_model_set_options kept its tables */
+    if (d->rope_cos) { vxh_free(d->rope_cos); d->rope_cos = NULL; }
+    if (d->rope_sin) { vxh_free(d->rope_sin); d->rope_sin = NULL; }
     vx_error e = upload_f32(d, &d->rope_cos, cs, d->n_pos * half);
     if (e == VX_OK) e = upload_f32(d, &d->rope_sin, sn, d->n_pos * half);
     free(cs);
@@ -664,6 +669,7 @@ vx_error vx_model_set_options(vx_model *m, const vx_model_options *opt)
         vxh_free(m->v_cache);
         m->k_cache = m->v_cache = NULL;
         m->cache_len = 0;
+        d->kv_gen++;
     }
     d->opt = *opt;
     if (cap_changed && m->k_cache) return dev_alloc_workspace(d, d->n_ctx_alloc, d->opt.attn_cap);
@@ -1106,6 +1112,11 @@ vx_error vx_dev_forward(vx_model *m, int M, int n_past, int logits_mode)
 {
     vx_dev *d = vx_dev_of(m);
     if (M < 1 || M > VX_MAX_BATCH) return VX_ERR_PARAM;
+    if (!m->k_cache || !m->v_cache) {
+        /* nothing to attend to or store into: fail before any launch */
+        vx_set_error("forward without a KV cache (dropped by an option change?)");
+        return VX_ERR_PARAM;
+    }
     if (pro_ok(d, M)) return forward_pro(m, M, n_past, logits_mode);
     if (d->opt.kv_half) return VX_ERR_UNSUPPORTED;   /* fp16 caches: prologue path only */
     if (fused_ok(d)) return forward_fused(m, M, n_past, logits_mode);

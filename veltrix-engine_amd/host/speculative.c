@@ -50,6 +50,7 @@ struct vx_speculative_state {
     int *committed;
     int cap;
     int n_prompt;         /* 0 = not prefilled */
+    unsigned gen_t, gen_d;   /* the models' cache generations at prefill */
 };
 
 float vx_uniform(uint64_t seed, uint64_t stream, uint64_t index)
@@ -163,6 +164,8 @@ int vx_speculative_prefill(vx_speculative_state *s, const int *prompt, int promp
         if (vx_dev_run_tokens(dm, s->committed, prompt_len - 1, VX_LOGITS_NONE, NULL) != VX_OK) return 0;
     }
     s->st.prefill_ms = vx_now_ms() - t0;
+    s->gen_t = vx_dev_of(tm)->kv_gen;
+    s->gen_d = vx_dev_of(dm)->kv_gen;
     s->n_prompt = prompt_len;
     return prompt_len;
 }
@@ -172,6 +175,11 @@ int vx_speculative_decode(vx_speculative_state *s, int *output, int max_tokens)
     if (!s || !output || max_tokens < 1 || s->n_prompt < 1) return 0;
     vx_model *tm = s->target, *dm = s->draft;
     vx_dev *td = vx_dev_of(tm), *dd = vx_dev_of(dm);
+    if (!tm->k_cache || !dm->k_cache || td->kv_gen != s->gen_t || dd->kv_gen != s->gen_d) {
+        /* an option change dropped a cache after prefill: its rows are gone */
+        vx_set_error("a model's KV cache changed since vx_speculative_prefill; prefill again");
+        return 0;
+    }
     const int k = s->k, Vd = s->Vd, Vt = s->Vt;
     const float T = s->temperature;
     int generated = 0;
@@ -189,12 +197,16 @@ int vx_speculative_decode(vx_speculative_state *s, int *output, int max_tokens)
 
     for (int round = 0; generated < max_tokens; round++) {
         /* drafts this round: the round emits up to kk+1 tokens, and positions
-         * n-1 .. n-1+kk must fit both caches */
+         * n-1 .. n-1+kk must fit the target's cache.  The loop is bounded by
+         * the target's context only (src/speculative.c:244, :257); once the
+         * draft's cache is full the rounds are target-only (kk = 0: the
+         * target's own draw at position n-1) */
         int kk = k;
         if (kk > max_tokens - generated - 1) kk = max_tokens - generated - 1;
         if (kk > tctx - n) kk = tctx - n;
         if (kk > dctx - n) kk = dctx - n;
-        if (n - 1 >= tctx || kk < 0) break;
+        if (n - 1 >= tctx) break;
+        if (kk < 0) kk = 0;
         double ta = vx_now_ms();
         int t_last = committed[n - 1];
         if (kk > 0) {

@@ -69,6 +69,7 @@ typedef struct vx_dev {
     int has_out_norm;
     /* KV cache and RoPE tables, allocated on first use */
     int n_ctx_alloc;
+    unsigned kv_gen;                   /* bumped whenever the cache is allocated or dropped */
     float *rope_cos, *rope_sin;
     int n_pos;
     /* activations, VX_MAX_BATCH rows */
