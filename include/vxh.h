@@ -238,6 +238,20 @@ size_t vxh_gemm_workspace_elems(int n_rows, int M);
 int vxh_gemm(const vxh_qmat *W, const vxh_panel *X, int M, const vxh_epilogue *ep,
              vxh_workspace *ws, int path, vxh_stream s);
 
+/* vxh_gemm without a workspace and without any allocation: no counterpart in
+ * the reference; for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The fp64 accumulator is a static device array of VXH_NOALLOC_ACC_ELEMS
+ * doubles (4 MiB) that each GPU the library runs on holds until the process
+ * ends; calls needing more (vxh_gemm_workspace_elems(W->n_rows, M) above it)
+ * fail with VXH_ERR_PARAM before launching anything.  Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (other streams,
+ * other threads) race and must not be issued.  The part a call uses is
+ * cleared by a fill kernel at its start.  Same results as vxh_gemm. */
+#define VXH_NOALLOC_ACC_ELEMS (1 << 19)
+int vxh_gemm_noalloc(const vxh_qmat *W, const vxh_panel *X, int M, const vxh_epilogue *ep, int path,
+                     vxh_stream s);
+
 /* ---- GEMM that builds its own panel ------------------------------------------
  * vxh_gemm_acc_timed whose workgroups build their K slice of the panel from
  * the source rows, so that no row kernel runs between two GEMMs of the
