@@ -402,6 +402,11 @@ __global__ __launch_bounds__(256) void vx_gemm_kernel(vx_gemm_args a)
     constexpr int NS = vx_mcfg<M>::NS;
     constexpr int R1 = vx_mcfg<M>::R1;
     constexpr int WPP = QT == 2 ? 1 : 2;   // 16-byte weight loads per lane per block pair
+    // two accumulator sets per block pair for verify batches read from a
+    // panel or plain rows; the residual/SwiGLU prologues keep one (their
+    // preloaded rows already cost registers: a second set lowered occupancy
+    // and slowed 22016x4096 at M = 9 from 21.1 to 23.8 us)
+    constexpr bool DUAL = M >= 5 && (PRO == VX_PRO_PANEL || PRO == VX_PRO_ROWS);
     constexpr int UNITS = PPW * 8 * NS;    // panel units of a full slice
     constexpr int UPT = (UNITS + 255) / 256;
     __shared__ uint4 lds[UPT * 256];
@@ -561,7 +566,49 @@ __global__ __launch_bounds__(256) void vx_gemm_kernel(vx_gemm_args a)
             for (int q = 0; q < WPP; q++) w[i % VX_RING][q] = wp[((size_t)pi * WPP + q) * 64];
             sc[i % VX_RING] = sp[(size_t)pi * 32];
         }
-        if (i < np) {
+        if (DUAL && i < np) {
+            // Both blocks of the pair issue their MFMAs into separate
+            // accumulator sets before either result is read, so one block's
+            // MFMA latency overlaps the other's reads and FMAs (one shared
+            // set serialises MFMA -> wait -> reads per block).
+            vx_half8 b[2][2], av[2][2];
+#pragma unroll
+            for (int blk = 0; blk < 2; blk++) {
+                const int bl = 2 * i + blk;
+                if (QT == 2) {
+                    b[blk][0] = vx_unpack_q4(blk ? wv[0].z : wv[0].x, magic);
+                    b[blk][1] = vx_unpack_q4(blk ? wv[0].w : wv[0].y, magic);
+                } else {
+                    b[blk][0] = vx_unpack_q8(wv[blk].x, wv[blk].y, magic);
+                    b[blk][1] = vx_unpack_q8(wv[blk].z, wv[blk].w, magic);
+                }
+                av[blk][0] = __builtin_bit_cast(vx_half8, lds[((bl * 2 + 0) * 2 + h) * NS + slot]);
+                av[blk][1] = __builtin_bit_cast(vx_half8, lds[((bl * 2 + 1) * 2 + h) * NS + slot]);
+            }
+            vx_f32x16 D0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[0][0], b[0][0], zero16, 0, 0, 0);
+            vx_f32x16 D1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[1][0], b[1][0], zero16, 0, 0, 0);
+            D0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[0][1], b[0][1], D0, 0, 0, 0);
+            D1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[1][1], b[1][1], D1, 0, 0, 0);
+#pragma unroll
+            for (int blk = 0; blk < 2; blk++) {
+                const int bl = 2 * i + blk;
+                const vx_f32x16 &D = blk ? D1 : D0;
+                const float d = vx_half_bits_to_float((sv >> (16 * blk)) & 0xFFFFu);
+#pragma unroll
+                for (int r = 0; r < R1; r++) {
+                    float dh = D[r];
+                    if (AVX2) {
+                        const int m = 8 * (r / 4) + 4 * h + (r % 4);
+                        dh = fmaf(-8.0f, m < M ? lcorr[bl * M + m] : 0.0f, dh);
+                    }
+                    acc[r] = fmaf(d, dh, acc[r]);
+                    acc[r + 8] = fmaf(d, D[r + 8], acc[r + 8]);
+                }
+            }
+        }
+        if (!DUAL && i < np) {
+            // one accumulator set, block by block (fewer registers: the M <= 4
+            // decode GEMMs run more wavefronts per SIMD with it)
 #pragma unroll
             for (int blk = 0; blk < 2; blk++) {
                 const int bl = 2 * i + blk;
@@ -589,6 +636,13 @@ __global__ __launch_bounds__(256) void vx_gemm_kernel(vx_gemm_args a)
                     acc[r + 8] = fmaf(d, D[r + 8], acc[r + 8]);
                 }
             }
+        }
+        // Keep this pair's accumulation here: without it the compiler sinks
+        // every result read and FMA below the last MFMA of the unrolled loop
+        // and holds all accumulator sets live at once.
+        if constexpr (DUAL) {
+#pragma unroll
+            for (int r = 0; r < R1; r++) asm volatile("" : "+v"(acc[r]), "+v"(acc[r + 8]));
         }
     }
 
@@ -673,8 +727,19 @@ static int vx_launch_gemm(const vxh_qmat *W, vx_gemm_args &a, hipStream_t st, hi
     const long groups = (W->n_rows / 32 + 3) / 4;
     const int cand[3] = {S::v0, S::v1, S::v2};
     int pick = S::n - 1;
-    for (int i = 0; i < S::n; i++)
-        if (groups * ((W->n_pairs + cand[i] - 1) / cand[i]) <= S::target) { pick = i; break; }
+    if (QT == 2 && M >= 5 && M <= 12 && EPI == VX_EPI_NONE && (PRO == VX_PRO_PANEL || PRO == VX_PRO_ROWS)) {
+        // verify batches (Q4_0) from a plain panel or rows: the 16-pair slice
+        // whenever it still gives every CU more than one workgroup (measured
+        // on MI355X at M = 9: 4096x11008 and 32000x4096 4-10% faster than 8
+        // pairs; 4096x4096 keeps 8 -- 128 workgroups leave half the CUs
+        // idle).  Residual prologues keep 8: twice the slice per workgroup
+        // costs them more than the longer stream saves (12288x4096 12.7 ->
+        // 15.4 us).
+        pick = groups * ((W->n_pairs + 15) / 16) >= 340 ? 1 : 0;
+    } else {
+        for (int i = 0; i < S::n; i++)
+            if (groups * ((W->n_pairs + cand[i] - 1) / cand[i]) <= S::target) { pick = i; break; }
+    }
     if (pick == 0) return vx_launch_ppw<QT, M, AVX2, S::v0, EPI, PRO>(W, a, st, e0, e1);
     if (pick == 1) return vx_launch_ppw<QT, M, AVX2, S::v1, EPI, PRO>(W, a, st, e0, e1);
     return vx_launch_ppw<QT, M, AVX2, S::v2, EPI, PRO>(W, a, st, e0, e1);
