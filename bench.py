@@ -14,10 +14,13 @@ several acceptance traces of the same workload).  The value is the
 emitted-token throughput of the timed steps (accepted drafts + the resampled
 or bonus token of every round).
 
+value: tok/s of the timed steps, run clean (no instrumentation).
+
 roofline: the verify dequant-GEMMs of the target (M = k+1 rows), timed with
-HIP events recorded on the target's stream around every GEMM launch inside
-the timed steps; achieved = algorithmic bytes (Q4_0 weight blocks + fp32
-activations in + fp32 results out) / event time.
+HIP events that the dispatch records on the target's stream around every 7th
+GEMM launch of each class, in a separate instrumented pass of the same
+workload after the timed steps; achieved = algorithmic bytes (Q4_0 weight
+blocks + fp32 activations in + fp32 results out) / event time.
 
 cpu_baseline: the reference engine's own x86 build (oracle/_ref, built from
 its sources by oracle/Makefile) on this host's cores: single-token forwards
@@ -30,7 +33,13 @@ configs: the isolated Q4_0/Q8_0 GEMMs at M = 1, 5, 9 (4096x4096, 11008x4096,
 (k=4, greedy) and of a 28L d3584 V152064 model at 8192 positions (k=8, T=1),
 each beside the reference's x86 build.
 
-Usage: python bench.py [--gpus 1] [--steps 5] [--warmup 1] [--mode spec|gemm|configs]
+--mode paths: the MFMA kernel against the dot-product kernel (v_dot2_f32_f16,
+no MFMA) on plain panels, at M = k+1 (verify shapes) and M = 1 (draft shapes).
+
+--mode traffic --fetch F.csv --write W.csv: HBM bytes per verify GEMM launch
+from two rocprofv3 counter runs of --mode gemm (FETCH_SIZE, WRITE_SIZE).
+
+Usage: python bench.py [--gpus 1] [--steps 5] [--warmup 1] [--mode spec|gemm|configs|paths|traffic]
 """
 import argparse
 import ctypes as C
@@ -146,7 +155,10 @@ def _gguf_stream(path, shape, rng, emb_type=2):
             f.write(b"\0" * ((-len(data)) % 32))
 
 
-def _ref_forward_ms(N, R, path, n_tok, ctx):
+def _ref_forward_ms(N, R, path, n_tok, ctx, thread_counts):
+    """Best of n_tok single-token forwards at context ctx for each thread
+    count (tests/benchmark.c:21-50 takes the best of 5); the model is larger
+    than the last-level cache, so every forward streams it from DRAM."""
     mp = C.POINTER(N.VxModel)()
     rc = R.vx_model_create(path.encode(), C.byref(mp))
     if rc != 0:
@@ -155,16 +167,29 @@ def _ref_forward_ms(N, R, path, n_tok, ctx):
         V = mp.contents.config.n_vocab
         lg = np.zeros(V, np.float32)
         R.vx_model_forward(mp, np.array([1], np.int32), 1, lg)     # allocates the KV cache
-        mp.contents.cache_len = ctx
-        times = []
-        for i in range(n_tok):
-            t0 = time.perf_counter()
-            R.vx_model_forward(mp, np.array([(7 * i + 3) % V], np.int32), 1, lg)
-            times.append(time.perf_counter() - t0)
-            mp.contents.cache_len = ctx                         # same context for every sample
-        return 1e3 * float(np.median(times))
+        best = {}
+        for th in thread_counts:
+            R.vx_set_n_threads(th)
+            times = []
+            for i in range(n_tok):
+                mp.contents.cache_len = ctx                     # same context for every sample
+                t0 = time.perf_counter()
+                R.vx_model_forward(mp, np.array([(7 * i + 3) % V], np.int32), 1, lg)
+                times.append(time.perf_counter() - t0)
+            best[th] = 1e3 * float(np.min(times))
+        return best
     finally:
         R.vx_model_destroy(mp)
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def _tmpdir(need):
@@ -178,36 +203,47 @@ def _tmpdir(need):
     raise RuntimeError(f"no directory with {need / 1e9:.0f} GB free for the reference's GGUF files")
 
 
-def cpu_baseline(N, stats_emitted, stats_drafted, ctx, n_target=3, n_draft=8):
+def cpu_baseline(N, stats_emitted, stats_drafted, ctx, n_trials=5):
+    """The reference's x86 build on this host: best of n_trials single-token
+    forwards of each model at context ctx, with all threads and with one,
+    turned into tok/s for the GPU run's acceptance trace (the reference
+    verifies one draft token per forward, src/speculative.c:186-207)."""
     if not N.ref_available("avx2"):
         return None
     R = N.ref("avx2")
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    R.vx_set_n_threads(threads)
     rng = np.random.default_rng(99)
     tmpdir = _tmpdir(6e9)
     t_start = time.perf_counter()
+    counts = sorted({threads, 1}, reverse=True)
     with tempfile.TemporaryDirectory(dir=tmpdir) as td:
         tp, dp = os.path.join(td, "target.gguf"), os.path.join(td, "draft.gguf")
         _gguf_stream(tp, TARGET, rng)
-        t_target = _ref_forward_ms(N, R, tp, n_target, ctx)
+        t_target = _ref_forward_ms(N, R, tp, n_trials, ctx, counts)
         os.remove(tp)
         _gguf_stream(dp, DRAFT, rng)
-        t_draft = _ref_forward_ms(N, R, dp, n_draft, ctx)
-    cpu_ms = stats_drafted * t_draft + stats_emitted * t_target
-    log(f"cpu baseline: target forward {t_target:.1f} ms, draft forward {t_draft:.1f} ms "
-        f"({threads} threads, {time.perf_counter() - t_start:.1f} s)")
+        t_draft = _ref_forward_ms(N, R, dp, n_trials, ctx, counts)
+    R.vx_set_n_threads(threads)
+
+    def tok_s(th):
+        return 1e3 * stats_emitted / (stats_drafted * t_draft[th] + stats_emitted * t_target[th])
+    cpu = _cpu_model()
+    log(f"cpu baseline ({cpu}): target forward {t_target} ms, draft forward {t_draft} ms by thread count "
+        f"({time.perf_counter() - t_start:.1f} s)")
     return {
-        "value": round(1e3 * stats_emitted / cpu_ms, 3),
+        "value": round(tok_s(threads), 3),
         "unit": "tok/s",
         "cores": threads,
         "kind": "reference",
-        "sample": (f"reference x86 build (oracle/_ref/libvxref_avx2.so, -Ofast -mavx2 -mfma -fopenmp), "
-                   f"{threads} threads: median of {n_target} target and {n_draft} draft single-token "
-                   f"forwards at context {ctx} on same-shape random Q4_0 GGUFs (target "
-                   f"{t_target:.1f} ms, draft {t_draft:.1f} ms); tok/s = emitted / (drafted*t_draft + "
-                   f"emitted*t_target) for the GPU run's acceptance trace ({stats_drafted} drafted, "
-                   f"{stats_emitted} emitted over the timed steps)"),
+        "value_1_thread": round(tok_s(1), 3),
+        "cpu_model": cpu,
+        "sample": (f"reference x86 build (oracle/_ref/libvxref_avx2.so, -Ofast -mavx2 -mfma -fopenmp) on "
+                   f"{cpu}: best of {n_trials} single-token forwards of same-shape random Q4_0 GGUFs at "
+                   f"context {ctx}, {threads} threads (target {t_target[threads]:.1f} ms, draft "
+                   f"{t_draft[threads]:.1f} ms) and 1 thread (target {t_target[1]:.1f} ms, draft "
+                   f"{t_draft[1]:.1f} ms); tok/s = emitted / (drafted*t_draft + emitted*t_target) for the "
+                   f"GPU run's acceptance trace ({stats_drafted} drafted, {stats_emitted} emitted over the "
+                   f"timed steps)"),
     }
 
 
@@ -258,33 +294,41 @@ def run_spec(args):
     for _ in range(args.warmup):
         if P.vx_speculative_decode(st, out, args.tokens) != args.tokens:
             sys.exit("bench.py: decode failed: " + N.product_error())
-    # kernel-execution events around every --prof-every-th verify GEMM of each
-    # class (7: a stride that walks through the 32 layers): a launch with
-    # events costs ~18 us of host time, enough to starve the GPU when every
-    # verify GEMM carries them (174.7 vs 186.3 tok/s)
-    P.vx_model_set_profiling(tm, args.prof_every)
-    P.vxh_device_sync()
     # every timed step decodes from the prefilled state with uniforms of its
     # own seed: the acceptance trace of two unrelated random models moves
     # with any rounding change, so the figure averages several traces
-    tot = dict(rounds=0, accepted=0, drafted=0, emitted=0, verify_ms=0.0, draft_ms=0.0)
     stats = N.VxSpecStats()
-    elapsed = 0.0
-    for i in range(args.steps):
-        P.vx_speculative_set_seed(st, 4243 + i)
-        t0 = time.perf_counter()
-        n = P.vx_speculative_decode(st, out, args.tokens)
-        P.vxh_device_sync()
-        elapsed += time.perf_counter() - t0
-        if n != args.tokens:
-            sys.exit("bench.py: decode failed: " + N.product_error())
-        P.vx_speculative_get_stats(st, C.byref(stats))
-        for key in tot:
-            tot[key] += getattr(stats, key)
+
+    def decode_steps(seeds):
+        tot = dict(rounds=0, accepted=0, drafted=0, emitted=0, verify_ms=0.0, draft_ms=0.0)
+        elapsed = 0.0
+        for seed in seeds:
+            P.vx_speculative_set_seed(st, seed)
+            t0 = time.perf_counter()
+            n = P.vx_speculative_decode(st, out, args.tokens)
+            P.vxh_device_sync()
+            elapsed += time.perf_counter() - t0
+            if n != args.tokens:
+                sys.exit("bench.py: decode failed: " + N.product_error())
+            P.vx_speculative_get_stats(st, C.byref(stats))
+            for key in tot:
+                tot[key] += getattr(stats, key)
+        return tot, elapsed
+    # the headline: a clean pass, no instrumentation
+    P.vxh_device_sync()
+    tot, elapsed = decode_steps([4243 + i for i in range(args.steps)])
+    value = args.steps * args.tokens / elapsed
+    # the roofline: a separate pass of the same workload with kernel-execution
+    # events around every --prof-every-th verify GEMM of each class (7: a
+    # stride that walks through the 32 layers; a launch with events costs
+    # ~18 us of host time, so this pass is not the one timed above)
+    P.vx_model_set_profiling(tm, args.prof_every)
+    P.vxh_device_sync()
+    tot_p, elapsed_p = decode_steps([4243 + i for i in range(args.prof_steps)])
     prof = (N.VxGemmProfile * 5)()
     P.vx_model_get_profile(tm, prof)
     P.vx_model_set_profiling(tm, 0)
-    value = args.steps * args.tokens / elapsed
+    log(f"instrumented pass: {args.prof_steps * args.tokens / elapsed_p:.1f} tok/s over {args.prof_steps} steps")
     names = ["qkv", "attn_out", "gate_up", "down", "output"]
     ms = sum(p.ms for p in prof)
     byt = sum(p.bytes for p in prof)
@@ -340,7 +384,8 @@ def run_spec(args):
             "frac": round(achieved / PEAK_HBM_GBS, 4),
             "traffic": read_traffic(),
             "kernel": (f"vx_gemm_kernel (Q4_0, M={args.k + 1}), every {args.prof_every}th verify GEMM launch "
-                       f"of each class (kernel-execution events)"),
+                       f"of each class (kernel-execution events), in a separate instrumented pass of "
+                       f"{args.prof_steps} steps after the timed ones"),
             "launches": launches,
             "avg_launch_us": round(1e3 * ms / max(launches, 1), 3),
             "bytes_per_launch": round(byt / max(launches, 1)),
@@ -513,6 +558,115 @@ def run_gemm(args):
     print(json.dumps({"mode": "gemm", "M": M, "results": results}), flush=True)
 
 
+
+def run_paths(args):
+    """The MFMA kernel against the dot-product kernel (VXH_PATH_DOT) on the
+    same plain panels: the target's verify GEMMs at M = k+1 and the draft's
+    decode GEMMs at M = 1, weights rotated over > 300 MB.  Times are device
+    time per launch between events (run under rocprofv3 --kernel-trace for
+    the kernels' own durations)."""
+    N, P = load_product()
+    import ctypes as CC
+    L = _bind_gemm(N, P)
+    L.vxh_prep_panel.argtypes = [CC.c_void_p, CC.c_void_p, CC.c_int, CC.c_int, CC.c_int, CC.c_int,
+                                 CC.c_void_p, CC.c_int, CC.c_void_p]
+    rng = np.random.default_rng(3)
+    cases = [(args.k + 1, r, c) for r, c in ((4096, 4096), (12288, 4096), (4096, 11008), (22016, 4096),
+                                             (32000, 4096))]
+    cases += [(1, r, c) for r, c in ((2560, 2048), (2048, 2048), (11264, 2048), (2048, 5632), (32000, 2048))]
+    results = []
+    for M, rows, cols in cases:
+        mats, mat_bytes = _rotated_mats(N, L, 2, rows, cols)
+        x = N.DevBuf(L, rng.normal(0, 1, (M, cols)).astype(np.float32))
+        pan = _Panel()
+        assert L.vxh_panel_alloc(CC.byref(pan), M, cols) == 0, L.vxh_last_error()
+        assert L.vxh_prep_panel(CC.byref(pan), x.ptr, cols, M, cols, 0, None, 0, None) == 0, L.vxh_last_error()
+        acc = N.DevBuf(L, np.zeros(M * rows, np.float64))
+        row = {"shape": f"Q4_0 {rows}x{cols} M={M}"}
+        for name, path in (("mfma", 1), ("dot", 2)):
+            def one_pass():
+                for q in mats:
+                    L.vxh_gemm_acc(CC.byref(q), CC.byref(pan), M, acc.ptr, rows, rows, 1.0, None, 0, 0.0, path, None)
+            assert L.vxh_gemm_acc(CC.byref(mats[0]), CC.byref(pan), M, acc.ptr, rows, rows, 1.0, None, 0, 0.0,
+                                  path, None) == 0, L.vxh_last_error()
+            reps = args.steps * 10
+            ms = _time_loop(L, reps, one_pass)
+            us = 1e3 * ms / (reps * len(mats))
+            row[name + "_us"] = round(us, 2)
+            row[name + "_GB/s"] = round((mat_bytes + 4 * M * cols + 4 * M * rows) / (us * 1e-6) / 1e9, 1)
+        row["mfma_speedup"] = round(row["dot_us"] / row["mfma_us"], 2)
+        log(json.dumps(row))
+        results.append(row)
+        x.free()
+        acc.free()
+        L.vxh_panel_free(CC.byref(pan))
+        for q in mats:
+            L.vxh_qmat_free(CC.byref(q))
+    print(json.dumps({"mode": "paths", "results": results}), flush=True)
+
+
+# ---------------------------------------------------------------------------
+# HBM traffic per verify GEMM from rocprofv3 counters (no GPU needed)
+# ---------------------------------------------------------------------------
+GEMM_SHAPES = [("Q4_0 4096x4096", 4096, 4096, 18), ("Q4_0 12288x4096", 12288, 4096, 18),
+               ("Q4_0 4096x11008", 4096, 11008, 18), ("Q4_0 22016x4096", 22016, 4096, 18),
+               ("Q4_0 32000x4096", 32000, 4096, 18), ("Q8_0 11008x4096", 11008, 4096, 34),
+               ("Q8_0 4096x11008", 4096, 11008, 34)]
+VERIFY_MIX = {"Q4_0 12288x4096": 32, "Q4_0 4096x4096": 32, "Q4_0 22016x4096": 32,
+              "Q4_0 4096x11008": 32, "Q4_0 32000x4096": 1}
+
+
+def run_traffic(args):
+    """Post-processes two `rocprofv3 --pmc` runs of `--mode gemm` (one with
+    FETCH_SIZE, one with WRITE_SIZE; KiB per dispatch) into HBM bytes per
+    launch of each verify GEMM.  Each counter is scaled by what it reads for
+    the 256 MiB device-to-device calibration copy that --mode gemm runs
+    first; GEMM dispatches are grouped by (kernel, grid size), one group per
+    shape in the order --mode gemm runs them.  The verify-step figure is the
+    launch-weighted mean over one target forward at M = k+1: 32 layers x
+    (QKV, O, gate/up, down) + the output projection."""
+    import csv
+    from collections import OrderedDict
+    M = args.k + 1
+    cal_bytes = 256 << 20
+
+    def load(path, counter):
+        groups, cal = OrderedDict(), []
+        with open(path) as f:
+            for d in csv.DictReader(f):
+                if d.get("Counter_Name") != counter:
+                    continue
+                name, v = d["Kernel_Name"], float(d["Counter_Value"]) * 1024.0
+                if name.startswith("__amd_rocclr_copyBuffer") and v > cal_bytes / 2:
+                    cal.append(v)
+                elif name.startswith("void vx_gemm_kernel"):
+                    groups.setdefault((name.split("(")[0], d["Grid_Size"]), []).append(v)
+        return groups, cal
+    fetch, fcal = load(args.fetch, "FETCH_SIZE")
+    write, wcal = load(args.write, "WRITE_SIZE")
+    ff = cal_bytes / (sum(fcal) / len(fcal))
+    wf = cal_bytes / (sum(wcal) / len(wcal))
+    print(f"calibration: copy of {cal_bytes} B reads FETCH {sum(fcal) / len(fcal):.0f} B (factor {ff:.4f}), "
+          f"WRITE {sum(wcal) / len(wcal):.0f} B (factor {wf:.4f})")
+    keys = list(fetch.keys())
+    if len(keys) != len(GEMM_SHAPES):
+        sys.exit(f"expected {len(GEMM_SHAPES)} GEMM groups, found {len(keys)}: {keys}")
+    per, alg = {}, {}
+    print(f"{'shape (M=%d)' % M:18s} {'kernel':40s} {'launches':>8s} {'alg MB':>8s} {'fetch MB':>9s} "
+          f"{'write MB':>9s} {'traffic/alg':>11s}")
+    for (shape, r, c, bpb), key in zip(GEMM_SHAPES, keys):
+        fv = sum(fetch[key]) / len(fetch[key]) * ff
+        wv = sum(write.get(key, [0.0])) / max(1, len(write.get(key, []))) * wf
+        alg[shape] = r * c // 32 * bpb + 4 * M * c + 4 * M * r
+        per[shape] = fv + wv
+        print(f"{shape:18s} {key[0][5:45]:40s} {len(fetch[key]):8d} {alg[shape] / 1e6:8.2f} {fv / 1e6:9.2f} "
+              f"{wv / 1e6:9.2f} {(fv + wv) / alg[shape]:11.3f}")
+    n = sum(VERIFY_MIX.values())
+    t = sum(per[s] * c for s, c in VERIFY_MIX.items()) / n
+    a = sum(alg[s] * c for s, c in VERIFY_MIX.items()) / n
+    print(f"verify mix (32 x QKV/O/gate-up/down + output, M={M}): algorithmic {a:.0f} B/launch")
+    print(f"traffic_bytes_per_launch: {t:.0f}")
+
 # ---------------------------------------------------------------------------
 # the other benchmark configurations: isolated GEMMs and single verify steps
 # ---------------------------------------------------------------------------
@@ -673,9 +827,9 @@ def _configs_verify(N, P, L, name, shape, ctx, k, T, emb_type, reps, R, threads)
                 path = os.path.join(td, "m.gguf")
                 t0 = time.perf_counter()
                 _gguf_stream(path, shape, np.random.default_rng(98), emb_type)
-                t_tok = _ref_forward_ms(N, R, path, 2, ctx)
+                t_tok = _ref_forward_ms(N, R, path, 2, ctx, [threads])[threads]
             r["cpu_ref_ms"] = round((k + 1) * t_tok, 1)
-            r["cpu_ref_sample"] = (f"reference x86 build, {threads} threads: median of 2 single-token forwards at "
+            r["cpu_ref_sample"] = (f"reference x86 build, {threads} threads: best of 2 single-token forwards at "
                                    f"cache position {ctx} ({t_tok:.1f} ms; the reference holds 4096 positions "
                                    f"and clamps later ones to the last slot, attending 4096 either way), "
                                    f"times k+1 = {k + 1} (it verifies one token per forward)")
@@ -712,10 +866,14 @@ def main():
     ap.add_argument("--tokens", type=int, default=256)
     ap.add_argument("--prompt", type=int, default=2048)
     ap.add_argument("--k", type=int, default=8)
-    ap.add_argument("--mode", choices=["spec", "gemm", "configs"], default="spec")
+    ap.add_argument("--mode", choices=["spec", "gemm", "configs", "traffic", "paths"], default="spec")
+    ap.add_argument("--fetch", help="traffic mode: counter CSV of the FETCH_SIZE run")
+    ap.add_argument("--write", help="traffic mode: counter CSV of the WRITE_SIZE run")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kv-half", action="store_true",
                     help="spec mode: both models with the flagged fp16 KV cache (not the headline)")
+    ap.add_argument("--prof-steps", type=int, default=2,
+                    help="steps of the separate instrumented pass that measures the roofline")
     ap.add_argument("--prof-every", type=int, default=7,
                     help="time every n-th verify GEMM of each class with kernel events")
     args = ap.parse_args()
@@ -724,7 +882,11 @@ def main():
         print(f"bench.py: this engine runs the verify path on ONE GPU; --gpus {args.gpus} "
               f"(WORLD_SIZE {ws}) is not supported -- run with --gpus 1", file=sys.stderr)
         sys.exit(2)
-    if args.mode == "gemm":
+    if args.mode == "traffic":
+        run_traffic(args)
+    elif args.mode == "paths":
+        run_paths(args)
+    elif args.mode == "gemm":
         run_gemm(args)
     elif args.mode == "configs":
         run_configs(args)

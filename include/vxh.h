@@ -185,6 +185,9 @@ int vxh_swiglu_panel_norm(double *acc, int ld_acc, int M, int F, float thr, cons
  * vxh_resid_rmsnorm_panel, vxh_swiglu_panel) round the accumulator to fp32
  * and clear it, so an accumulator that starts zeroed stays zeroed between
  * uses. */
+/* path: VXH_PATH_AUTO and VXH_PATH_MFMA take the MFMA kernel; VXH_PATH_DOT
+ * the same GEMM with v_dot2_f32_f16 per activation row instead of MFMA
+ * (exact Q4_0/Q8_0 panels; kept to measure the MFMA kernel against). */
 enum { VXH_PATH_AUTO = 0, VXH_PATH_MFMA = 1, VXH_PATH_DOT = 2 };
 
 int vxh_gemm_acc(const vxh_qmat *W, const vxh_panel *X, int M, double *acc, int ld_acc,

@@ -144,3 +144,69 @@ def test_gemm_zero_and_one_hot(P):
     out = np.full((2, rows), 7.0, np.float32)
     assert P.vx_gemm_q4_0(N._ptr(W), X, cols, out, 2, rows, cols, 0) == 0
     assert np.all(out == 0.0), np.abs(out).max()
+
+
+class _QMat(C.Structure):
+    _fields_ = [("type", C.c_int), ("n_rows", C.c_int), ("n_cols", C.c_int), ("n_pairs", C.c_int),
+                ("qs", C.c_void_p), ("d", C.c_void_p)]
+
+
+class _Panel(C.Structure):
+    _fields_ = [("data", C.c_void_p), ("corr", C.c_void_p), ("rscale", C.c_void_p), ("xs", C.c_void_p),
+                ("M", C.c_int), ("K", C.c_int), ("avx2", C.c_int), ("rs_ld", C.c_int)]
+
+
+@pytest.mark.parametrize("typ,rows,cols,M", [(2, 2560, 2048, 1), (2, 4096, 4096, 9), (2, 4096, 11008, 5),
+                                             (8, 2048, 5632, 1), (8, 1024, 4096, 9), (2, 96, 160, 16)])
+def test_dot_path_matches_oracle(P, typ, rows, cols, M):
+    """VXH_PATH_DOT (v_dot2_f32_f16, no MFMA) on the same panel as the MFMA
+    kernel: against the oracle GEMV at the fp32 bar."""
+    vp = C.c_void_p
+    L = N.bind_vxh(P)
+    L.vxh_qmat_alloc.argtypes = [vp, C.c_int, C.c_int, C.c_int]
+    L.vxh_qmat_set_rows.argtypes = [vp, vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, vp]
+    L.vxh_qmat_free.argtypes = [vp]
+    L.vxh_panel_alloc.argtypes = [vp, C.c_int, C.c_int]
+    L.vxh_panel_free.argtypes = [vp]
+    L.vxh_prep_panel.argtypes = [vp, vp, C.c_int, C.c_int, C.c_int, C.c_int, vp, C.c_int, vp]
+    L.vxh_gemm_acc.argtypes = [vp, vp, C.c_int, vp, C.c_int, C.c_int, C.c_float, vp, C.c_int, C.c_float, C.c_int, vp]
+    L.vxh_acc_store.argtypes = [vp, C.c_int, C.c_int, C.c_int, vp, C.c_int, vp, C.c_int, vp]
+    print(f"dot path {'Q4_0' if typ == 2 else 'Q8_0'} {rows}x{cols} M={M}", flush=True)
+    rng = np.random.default_rng(rows + cols + M + typ)
+    W = N.rand_q4_0(rng, rows, cols) if typ == 2 else N.rand_q8_0(rng, rows, cols)
+    X = rng.normal(0, 1, (M, cols)).astype(np.float32)
+    rows_p = (rows + 31) // 32 * 32
+    q = _QMat()
+    assert L.vxh_qmat_alloc(C.byref(q), typ, rows_p, cols) == 0, L.vxh_last_error()
+    assert L.vxh_qmat_set_rows(C.byref(q), N._ptr(W), 0, rows, rows, 0, 0, None) == 0, L.vxh_last_error()
+    pan = _Panel()
+    assert L.vxh_panel_alloc(C.byref(pan), M, cols) == 0
+    dx = N.DevBuf(L, X)
+    acc = N.DevBuf(L, np.zeros(M * rows_p, np.float64))
+    dy = N.DevBuf(L, nbytes=4 * M * rows)
+    try:
+        assert L.vxh_prep_panel(C.byref(pan), dx.ptr, cols, M, cols, 0, None, 0, None) == 0
+        assert L.vxh_gemm_acc(C.byref(q), C.byref(pan), M, acc.ptr, rows_p, rows, 1.0, None, 0, 0.0, 2, None) == 0, \
+            L.vxh_last_error()
+        assert L.vxh_acc_store(acc.ptr, rows_p, M, rows, dy.ptr, rows, None, 0, None) == 0
+        assert L.vxh_stream_sync(None) == 0
+        Y = dy.get(np.float32, M * rows).reshape(M, rows)
+    finally:
+        for b in (dx, acc, dy):
+            b.free()
+        L.vxh_panel_free(C.byref(pan))
+        L.vxh_qmat_free(C.byref(q))
+    ref = np.zeros((M, rows), np.float32)
+    if typ == 2:
+        for m in range(M):
+            O.or_gemv_q4_0(N._ptr(W), np.ascontiguousarray(X[m]), ref[m], rows, cols)
+        exact = X.astype(np.float64) @ N.q4_values(W).T
+    else:
+        A = np.zeros(rows * cols, np.float32)
+        O.or_dequantize_row_q8_0(N._ptr(W), A, rows * cols, 1.0)
+        for m in range(M):
+            O.or_gemv_f32(ref[m], A.reshape(rows, cols), np.ascontiguousarray(X[m]), rows, cols)
+        exact = X.astype(np.float64) @ N.q8_values(W).T
+    ok, nfb = N.parity(Y, ref, exact)
+    print(f"max |d| {np.abs(Y.astype(np.float64) - ref).max():.2e}; elements on the exact-value fallback: {nfb}")
+    assert ok, N.max_violation(Y, ref)

@@ -494,6 +494,172 @@ extern "C" int vxh_rmsnorm(const float *x, int ldx, int M, int K, const float *w
     return VXH_OK;
 }
 
+// ---------------------------------------------------------------------------
+// dot-product path (VXH_PATH_DOT): the same GEMM without MFMA
+// ---------------------------------------------------------------------------
+// Same workgroup shape, K slices, weight stream and LDS panel slice as
+// vx_gemm_kernel.  Lane (j, h) of a wavefront takes row j of its tile and the
+// K half h (elements 16h..16h+15) of both blocks of every pair: the nibbles
+// or bytes unpack to exact fp16 (s - 8, resp. q) as on the MFMA path, and
+// every activation row m accumulates d * sum (w * x_hi + w * x_lo) with
+// v_dot2_f32_f16 from the panel's hi and lo parts.  The two K halves of a row
+// meet with one lane swap before the fp64 atomic add.  Exists to measure the
+// MFMA path against (src/simd/avx2.c:311-370 is a dot product per row).
+#define VX_DOT_PPW 8
+
+__device__ __forceinline__ float vx_dot8(const vx_half8 &w, const vx_half8 &x, float t)
+{
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const vx_half2 a = {w[2 * q], w[2 * q + 1]};
+        const vx_half2 b = {x[2 * q], x[2 * q + 1]};
+        t = __builtin_amdgcn_fdot2(a, b, t, false);
+    }
+    return t;
+}
+
+template <int QT, int M>
+__global__ __launch_bounds__(256) void vx_gemm_dot_kernel(vx_gemm_args a)
+{
+    constexpr int PPW = VX_DOT_PPW;
+    constexpr int NS = 2 * M;
+    constexpr int WPP = QT == 2 ? 1 : 2;
+    constexpr int UNITS = PPW * 8 * NS;
+    constexpr int UPT = (UNITS + 255) / 256;
+    __shared__ uint4 lds[UPT * 256];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int grp = blockIdx.x / a.n_splits, split = blockIdx.x % a.n_splits;
+    const int T = grp * 4 + wave;
+    const bool tile_ok = T < a.n_tiles;
+    const int Tc = tile_ok ? T : 0;
+    const int p0 = split * PPW;
+    const int np = min(PPW, a.n_pairs - p0);
+    const int units = np * 8 * NS;
+    const int c = lane & 31, h = lane >> 5;
+    const uint32_t magic = 0x64006400u;
+    uint4 pv[UPT];
+    const uint4 *psrc = a.panel + (size_t)p0 * 8 * NS;
+#pragma unroll
+    for (int j = 0; j < UPT; j++) pv[j] = psrc[min(j * 256 + (int)threadIdx.x, units - 1)];
+    const uint4 *wp = a.wq + ((size_t)Tc * a.n_pairs + p0) * WPP * 64 + lane;
+    const uint32_t *sp = a.wd + ((size_t)Tc * a.n_pairs + p0) * 32 + c;
+    uint4 w[VX_RING][WPP];
+    uint32_t sc[VX_RING];
+#pragma unroll
+    for (int i = 0; i < VX_RING; i++) {
+        const int pi = min(i, np - 1);
+#pragma unroll
+        for (int q = 0; q < WPP; q++) w[i][q] = wp[((size_t)pi * WPP + q) * 64];
+        sc[i] = sp[(size_t)pi * 32];
+    }
+#pragma unroll
+    for (int j = 0; j < UPT; j++) lds[j * 256 + threadIdx.x] = pv[j];
+    __syncthreads();
+    float acc[M];
+#pragma unroll
+    for (int m = 0; m < M; m++) acc[m] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PPW; i++) {
+        uint4 wv[WPP];
+#pragma unroll
+        for (int q = 0; q < WPP; q++) wv[q] = w[i % VX_RING][q];
+        const uint32_t sv = sc[i % VX_RING];
+        if (i + VX_RING < PPW) {
+            const int pi = min(i + VX_RING, np - 1);
+#pragma unroll
+            for (int q = 0; q < WPP; q++) w[i % VX_RING][q] = wp[((size_t)pi * WPP + q) * 64];
+            sc[i % VX_RING] = sp[(size_t)pi * 32];
+        }
+        if (i < np) {
+#pragma unroll
+            for (int blk = 0; blk < 2; blk++) {
+                const int bl = 2 * i + blk;
+                vx_half8 b0, b1;
+                if (QT == 2) {
+                    b0 = vx_unpack_q4(blk ? wv[0].z : wv[0].x, magic);
+                    b1 = vx_unpack_q4(blk ? wv[0].w : wv[0].y, magic);
+                } else {
+                    b0 = vx_unpack_q8(wv[blk].x, wv[blk].y, magic);
+                    b1 = vx_unpack_q8(wv[blk].z, wv[blk].w, magic);
+                }
+                const float d = vx_half_bits_to_float((sv >> (16 * blk)) & 0xFFFFu);
+                const uint4 *u0 = lds + ((bl * 2 + 0) * 2 + h) * NS, *u1 = lds + ((bl * 2 + 1) * 2 + h) * NS;
+#pragma unroll
+                for (int m = 0; m < M; m++) {
+                    float t = 0.0f;
+                    t = vx_dot8(b0, __builtin_bit_cast(vx_half8, u0[m]), t);
+                    t = vx_dot8(b0, __builtin_bit_cast(vx_half8, u0[M + m]), t);
+                    t = vx_dot8(b1, __builtin_bit_cast(vx_half8, u1[m]), t);
+                    t = vx_dot8(b1, __builtin_bit_cast(vx_half8, u1[M + m]), t);
+                    acc[m] = fmaf(d, t, acc[m]);
+                }
+            }
+        }
+    }
+    // row j's two K halves live in lanes j and j + 32
+#pragma unroll
+    for (int m = 0; m < M; m++) acc[m] = vx_sum_x32(acc[m]);
+    const int n = T * 32 + c;
+    if (h == 0 && tile_ok && n < a.n_out) {
+        const int chunk = p0 / a.rs_chunk;
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            if (a.gate && fabsf(a.gate[(size_t)m * a.ld_gate + n]) < a.thr) continue;
+            const float osc = a.rscale[m * a.rs_ld + chunk] * a.scale;
+            __hip_atomic_fetch_add(&a.acc[(size_t)m * a.ld_acc + n], (double)(acc[m] * osc), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+template <int QT, int M>
+static int vx_launch_dot(const vxh_qmat *W, vx_gemm_args &a, hipStream_t st, hipEvent_t e0, hipEvent_t e1)
+{
+    a.n_tiles = W->n_rows / 32;
+    a.n_pairs = W->n_pairs;
+    a.n_splits = (W->n_pairs + VX_DOT_PPW - 1) / VX_DOT_PPW;
+    if (a.rs_ld > 1 && a.rs_chunk % VX_DOT_PPW)
+        return vxh_fail(VXH_ERR_PARAM, "gemm: K slice of %d pairs crosses a %d-pair scale chunk", VX_DOT_PPW,
+                        a.rs_chunk);
+    const int groups = (a.n_tiles + 3) / 4;
+    if (e0 || e1)
+        hipExtLaunchKernelGGL(vx_gemm_dot_kernel<QT, M>, dim3(groups * a.n_splits), dim3(256), 0, st, e0, e1, 0,
+                              a);
+    else
+        vx_gemm_dot_kernel<QT, M><<<groups * a.n_splits, 256, 0, st>>>(a);
+    VXH_LAUNCHED();
+    return VXH_OK;
+}
+
+template <int M>
+static int vx_dot_m(const vxh_qmat *W, vx_gemm_args &a, hipStream_t st, hipEvent_t e0, hipEvent_t e1)
+{
+    return W->type == 2 ? vx_launch_dot<2, M>(W, a, st, e0, e1) : vx_launch_dot<8, M>(W, a, st, e0, e1);
+}
+
+static int vx_dot_dispatch(const vxh_qmat *W, int M, vx_gemm_args &a, hipStream_t st, hipEvent_t e0,
+                           hipEvent_t e1)
+{
+    switch (M) {
+    case 1: return vx_dot_m<1>(W, a, st, e0, e1);
+    case 2: return vx_dot_m<2>(W, a, st, e0, e1);
+    case 3: return vx_dot_m<3>(W, a, st, e0, e1);
+    case 4: return vx_dot_m<4>(W, a, st, e0, e1);
+    case 5: return vx_dot_m<5>(W, a, st, e0, e1);
+    case 6: return vx_dot_m<6>(W, a, st, e0, e1);
+    case 7: return vx_dot_m<7>(W, a, st, e0, e1);
+    case 8: return vx_dot_m<8>(W, a, st, e0, e1);
+    case 9: return vx_dot_m<9>(W, a, st, e0, e1);
+    case 10: return vx_dot_m<10>(W, a, st, e0, e1);
+    case 11: return vx_dot_m<11>(W, a, st, e0, e1);
+    case 12: return vx_dot_m<12>(W, a, st, e0, e1);
+    case 13: return vx_dot_m<13>(W, a, st, e0, e1);
+    case 14: return vx_dot_m<14>(W, a, st, e0, e1);
+    case 15: return vx_dot_m<15>(W, a, st, e0, e1);
+    default: return vx_dot_m<16>(W, a, st, e0, e1);
+    }
+}
+
 extern "C" int vxh_gemm_acc_timed(const vxh_qmat *W, const vxh_panel *X, int M, double *acc,
                                   int ld_acc, int n_out, float scale, const float *gate, int ld_gate,
                                   float thr, int path, vxh_event start, vxh_event stop, vxh_stream s)
@@ -504,8 +670,8 @@ extern "C" int vxh_gemm_acc_timed(const vxh_qmat *W, const vxh_panel *X, int M, 
         return vxh_fail(VXH_ERR_PARAM, "gemm: W has K %d, panel %d", W->n_cols, X->K);
     if (n_out < 0 || n_out > W->n_rows || (n_out > ld_acc && M > 1))
         return vxh_fail(VXH_ERR_PARAM, "gemm: n_out %d (rows %d, ld %d)", n_out, W->n_rows, ld_acc);
-    if (path == VXH_PATH_DOT)
-        return vxh_fail(VXH_ERR_UNSUPPORTED, "dot-product path not built for this shape");
+    if (path == VXH_PATH_DOT && X->avx2)
+        return vxh_fail(VXH_ERR_UNSUPPORTED, "dot-product path: exact Q4_0/Q8_0 panels only");
     if (n_out == 0) return VXH_OK;
     vx_gemm_args a;
     memset(&a, 0, sizeof(a));
@@ -523,6 +689,7 @@ extern "C" int vxh_gemm_acc_timed(const vxh_qmat *W, const vxh_panel *X, int M, 
     a.gate = gate;
     a.ld_gate = ld_gate;
     a.thr = thr;
+    if (path == VXH_PATH_DOT) return vx_dot_dispatch(W, M, a, vxh_hs(s), (hipEvent_t)start, (hipEvent_t)stop);
     return vx_dispatch<VX_EPI_NONE>(W, M, X->avx2, a, vxh_hs(s), (hipEvent_t)start, (hipEvent_t)stop);
 }
 
