@@ -57,6 +57,10 @@ typedef struct {
                                   pro_max_rows >= 16 and head_dim 64 or 128.  Changing
                                   it drops the cache (cache_len 0); k_cache/v_cache
                                   then hold halves                                    */
+    int prefill_min_rows;      /* prompt chunks of at least this many rows whose
+                                  positions fit the context run as one large-M
+                                  batch (up to 512 rows; exact Q4_0 kernel, fp32
+                                  cache); 0 = never.  Default 48               */
 } vx_model_options;
 
 #define VX_FUSED_NONE 0        /* separate row kernels (11 launches per layer)          */

@@ -361,6 +361,28 @@ int vxh_gemm_fused(const vxh_qmat *W, const vxh_xpanel *X, int M, double *acc, i
                    int n_out, float scale, const vxh_fepi *e, vxh_event start, vxh_event stop,
                    vxh_stream s);
 
+/* ---- prompt prefill at large M ---------------------------------------------------
+ * The reference runs a prompt one token per forward (src/speculative.c:100-107,
+ * src/model.c:450-616); these run a chunk of prompt rows as one batch.
+ *
+ * vxh_gemm_rows: Y[m][n] = (R ? R[m][n] : 0) + scale * sum_k X[m][k] W[n][k]
+ * for m < M (any M >= 1), n < n_out, from fp32 rows X[M][ldx] (16-byte
+ * aligned, ldx % 4 == 0, K = W->n_cols).  Compute-bound MFMA tiles of 64 rows
+ * x 128 columns; weights enter as the exact fp16 pair d*q = hi + lo and the
+ * activations as fp16 hi + lo, summed over all of K in fp32 (within the fp32
+ * GEMV's rounding of src/quantize.c:728-750).  Y may alias R. */
+int vxh_gemm_rows(const vxh_qmat *W, const float *X, int ldx, int M, float *Y, int ldy, int n_out,
+                  const float *R, int ldr, float scale, vxh_stream s);
+/* vxh_rope_kv for fp32 q|k|v rows qkv[M][ld_qkv] (no deferred norm, not
+ * cleared): rotated q to q_out[M][ldq], k and v into the cache rows. */
+int vxh_rope_kv_rows(const float *qkv, int ld_qkv, int M, int n_past, int n_ctx, int n_heads,
+                     int n_kv_heads, int head_dim, const float *bq, const float *bk, const float *bv,
+                     const float *cos_tab, const float *sin_tab, int n_pos, float *q_out, int ldq,
+                     float *k_cache_layer, float *v_cache_layer, vxh_stream s);
+/* h[m][i] = |silu(g)| < thr ? 0 : silu(g) * u for the tile-interleaved gate/up
+ * rows gu[M][ld_gu] (gate at 32(i/16) + i%16, up 16 further; src/model.c:582-585). */
+int vxh_swiglu_rows(const float *gu, int ld_gu, int M, int F, float thr, float *h, int ldh, vxh_stream s);
+
 /* ---- attention block ---------------------------------------------------------
  * RoPE + KV write (src/tensor.c:173-271 portable branch, src/model.c:291-296):
  * qkv[m] = [q | k | v] (+ optional F32 biases), read from the fp64 GEMM

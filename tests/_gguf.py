@@ -95,7 +95,7 @@ def fp32_to_fp16_trunc(f):
 
 def llama_gguf(path, rng, n_layers, n_embd, n_heads, n_kv_heads, n_ff, n_vocab,
                rope_theta=10000.0, std=0.02, with_attn_output=True, norm_random=False,
-               emb_type=GGML_Q4_0, out_type=GGML_Q4_0, with_output=True):
+               emb_type=GGML_Q4_0, out_type=GGML_Q4_0, with_output=True, matrix_type=GGML_Q4_0):
     """Write a random-init Llama-style model (weights N(0, std) quantised with
     the reference quantiser, norms F32).  Returns dict of the raw arrays."""
     hd = n_embd // n_heads
@@ -130,15 +130,15 @@ def llama_gguf(path, rng, n_layers, n_embd, n_heads, n_kv_heads, n_ff, n_vocab,
     qmat("token_embd.weight", n_vocab, n_embd, emb_type)
     for l in range(n_layers):
         norm(f"blk.{l}.attn_norm.weight", n_embd)
-        qmat(f"blk.{l}.attn_q.weight", n_embd, n_embd)
-        qmat(f"blk.{l}.attn_k.weight", kvd, n_embd)
-        qmat(f"blk.{l}.attn_v.weight", kvd, n_embd)
+        qmat(f"blk.{l}.attn_q.weight", n_embd, n_embd, matrix_type)
+        qmat(f"blk.{l}.attn_k.weight", kvd, n_embd, matrix_type)
+        qmat(f"blk.{l}.attn_v.weight", kvd, n_embd, matrix_type)
         if with_attn_output:
-            qmat(f"blk.{l}.attn_output.weight", n_embd, n_embd)
+            qmat(f"blk.{l}.attn_output.weight", n_embd, n_embd, matrix_type)
         norm(f"blk.{l}.ffn_norm.weight", n_embd)
-        qmat(f"blk.{l}.ffn_gate.weight", n_ff, n_embd)
-        qmat(f"blk.{l}.ffn_up.weight", n_ff, n_embd)
-        qmat(f"blk.{l}.ffn_down.weight", n_embd, n_ff)
+        qmat(f"blk.{l}.ffn_gate.weight", n_ff, n_embd, matrix_type)
+        qmat(f"blk.{l}.ffn_up.weight", n_ff, n_embd, matrix_type)
+        qmat(f"blk.{l}.ffn_down.weight", n_embd, n_ff, matrix_type)
     norm("output_norm.weight", n_embd)
     if with_output:
         qmat("output.weight", n_vocab, n_embd, out_type)

@@ -230,7 +230,8 @@ def max_violation(a, b, atol=1e-4, rtol=1e-3):
 # --------------------------------------------------------------------------
 class VxModelOptions(C.Structure):
     _fields_ = [("q4_kernel", C.c_int), ("attn_cap", C.c_int), ("ffn_gate_threshold", C.c_float),
-                ("fused", C.c_int), ("pro_max_rows", C.c_int), ("kv_half", C.c_int)]
+                ("fused", C.c_int), ("pro_max_rows", C.c_int), ("kv_half", C.c_int),
+                ("prefill_min_rows", C.c_int)]
 
 
 class VxSynthSpec(C.Structure):

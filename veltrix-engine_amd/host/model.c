@@ -180,6 +180,9 @@ static void dev_free(vx_dev *d)
     vxh_free(d->stats); vxh_free(d->acc_out);
     vxh_free(d->ss); vxh_free(d->hrows); vxh_free(d->cnt); vxh_free(d->cnt_row);
     vxh_free(d->x2); vxh_free(d->acc_y);
+    vxh_free(d->pf_tok); vxh_free(d->pf_x); vxh_free(d->pf_xn); vxh_free(d->pf_qkv);
+    vxh_free(d->pf_q); vxh_free(d->pf_att); vxh_free(d->pf_gu); vxh_free(d->pf_h);
+    vxh_workspace_free(&d->pf_ws);
     vxh_panel_free(&d->pan_d);
     vxh_panel_free(&d->pan_f);
     vxh_xpanel_free(&d->xp_att);
@@ -212,6 +215,7 @@ static vx_error dev_alloc_common(vx_model *m)
     d->opt.ffn_gate_threshold = 0.01f;
     d->opt.fused = VX_FUSED_PROLOGUE;
     d->opt.pro_max_rows = VX_MAX_BATCH;
+    d->opt.prefill_min_rows = 48;
     if (d->d % 32 || d->F % 32 || d->F <= 0 || d->d <= 0 || d->n_heads * d->hd != d->d ||
         d->hd % 2 || d->n_kv <= 0 || d->n_heads % d->n_kv) {
         vx_set_error("unsupported shape: n_embd %d n_ff %d heads %d/%d head_dim %d", d->d, d->F,
@@ -648,6 +652,7 @@ vx_error vx_model_set_options(vx_model *m, const vx_model_options *opt)
     if (opt->fused < VX_FUSED_NONE || opt->fused > VX_FUSED_PROLOGUE || opt->pro_max_rows < 0)
         return VX_ERR_PARAM;
     if (opt->kv_half != 0 && opt->kv_half != 1) return VX_ERR_PARAM;
+    if (opt->prefill_min_rows < 0) return VX_ERR_PARAM;
     if (opt->kv_half) {
         /* every forward must take the q|k|v attention kernel, the only one
          * with an fp16 cache */
@@ -672,6 +677,15 @@ vx_error vx_model_set_options(vx_model *m, const vx_model_options *opt)
         d->kv_gen++;
     }
     d->opt = *opt;
+    if (cap_changed && d->pf_ready) {
+        /* the prefill attention workspace is sized for the cap: rebuilt on next use */
+        TRY(vxh_stream_sync(d->stream));
+        vxh_workspace_free(&d->pf_ws);
+        vxh_free(d->pf_tok); vxh_free(d->pf_x); vxh_free(d->pf_xn); vxh_free(d->pf_qkv);
+        vxh_free(d->pf_q); vxh_free(d->pf_att); vxh_free(d->pf_gu); vxh_free(d->pf_h);
+        d->pf_tok = NULL; d->pf_x = d->pf_xn = d->pf_qkv = d->pf_q = d->pf_att = d->pf_gu = d->pf_h = NULL;
+        d->pf_ready = 0;
+    }
     if (cap_changed && m->k_cache) return dev_alloc_workspace(d, d->n_ctx_alloc, d->opt.attn_cap);
     return VX_OK;
 }
@@ -1187,6 +1201,90 @@ vx_error vx_dev_forward(vx_model *m, int M, int n_past, int logits_mode)
     return VX_OK;
 }
 
+/* --------------------------------------------------------------------------- */
+/* large-M prompt prefill                                                        */
+/* --------------------------------------------------------------------------- */
+/* The large-M path covers the exact Q4_0/Q8_0 arithmetic with an fp32 cache;
+ * the AVX2-lane mode and the fp16 cache stay on the batched forward. */
+static int pf_ok(const vx_dev *d)
+{
+    return d->opt.prefill_min_rows > 0 && d->opt.q4_kernel == VX_Q4_EXACT && !d->opt.kv_half &&
+           d->hd % 4 == 0 && d->hd <= 128;
+}
+
+static vx_error pf_alloc(vx_dev *d)
+{
+    if (d->pf_ready) return VX_OK;
+    const size_t R = VX_PF_ROWS;
+    TRY(vxh_malloc((void **)&d->pf_tok, sizeof(int) * R));
+    TRY(vxh_malloc((void **)&d->pf_x, sizeof(float) * R * d->d));
+    TRY(vxh_malloc((void **)&d->pf_xn, sizeof(float) * R * d->d));
+    TRY(vxh_malloc((void **)&d->pf_qkv, sizeof(float) * R * d->ld_qkv));
+    TRY(vxh_malloc((void **)&d->pf_q, sizeof(float) * R * d->d));
+    TRY(vxh_malloc((void **)&d->pf_att, sizeof(float) * R * d->d));
+    TRY(vxh_malloc((void **)&d->pf_gu, sizeof(float) * R * d->ld_gu));
+    TRY(vxh_malloc((void **)&d->pf_h, sizeof(float) * R * d->F));
+    size_t an = vxh_attention_workspace_floats(VX_PF_ROWS, d->n_ctx_alloc, d->opt.attn_cap, d->n_heads, d->n_kv,
+                                               d->hd);
+    TRY(vxh_workspace_alloc(&d->pf_ws, 32, an));
+    d->pf_ready = 1;
+    return VX_OK;
+}
+
+/* M <= VX_PF_ROWS prompt rows at positions n_past .. n_past+M-1 (all below
+ * n_ctx) as one batch: per layer RMSNorm rows, the large-M GEMMs, RoPE + KV
+ * store, causal attention over the cache, SwiGLU (src/model.c:514-594).
+ * With last_logits the last row's logits land in d->logits row 0. */
+static vx_error forward_prefill(vx_model *m, const int *tokens, int M, int n_past, int last_logits)
+{
+    vx_dev *d = vx_dev_of(m);
+    const int dd = d->d, kvd = d->kvd, n_ctx = d->n_ctx_alloc;
+    vxh_stream s = d->stream;
+    vx_error e = pf_alloc(d);
+    if (e != VX_OK) return e;
+    TRY(vxh_upload(d->pf_tok, tokens, sizeof(int) * (size_t)M, s));
+    if (d->has_embd) TRY(vxh_qmat_gather_rows(&d->embd, d->pf_tok, M, vx_get_synthetic_weight_scale(), d->pf_x, dd, s));
+    else TRY(vxh_fill_f32(d->pf_x, 0.0f, (size_t)M * dd, s));
+    for (int l = 0; l < d->n_layers; l++) {
+        vx_dev_layer *Ld = &d->layers[l];
+        float *kc = m->k_cache + (size_t)l * n_ctx * kvd, *vc = m->v_cache + (size_t)l * n_ctx * kvd;
+        TRY(vxh_rmsnorm(d->pf_x, dd, M, dd, Ld->attn_norm, d->pf_xn, dd, s));
+        TRY(vxh_gemm_rows(&Ld->wqkv, d->pf_xn, dd, M, d->pf_qkv, d->ld_qkv, dd + 2 * kvd, NULL, 0,
+                          scale_for(d, Ld->wqkv.type), s));
+        TRY(vxh_rope_kv_rows(d->pf_qkv, d->ld_qkv, M, n_past, n_ctx, d->n_heads, d->n_kv, d->hd, Ld->bq, Ld->bk,
+                             Ld->bv, d->rope_cos, d->rope_sin, d->n_pos, d->pf_q, dd, kc, vc, s));
+        TRY(vxh_attention(d->pf_q, M, n_past, n_ctx, d->n_heads, d->n_kv, d->hd, d->opt.attn_cap, kc, vc,
+                          d->pf_att, dd, &d->pf_ws, s));
+        if (Ld->has_o)
+            TRY(vxh_gemm_rows(&Ld->wo, d->pf_att, dd, M, d->pf_x, dd, dd, d->pf_x, dd, scale_for(d, Ld->wo.type), s));
+        else
+            TRY(vxh_add_rows(d->pf_x, dd, d->pf_att, dd, M, dd, s));
+        TRY(vxh_rmsnorm(d->pf_x, dd, M, dd, Ld->ffn_norm, d->pf_xn, dd, s));
+        TRY(vxh_gemm_rows(&Ld->wgu, d->pf_xn, dd, M, d->pf_gu, d->ld_gu, d->ld_gu, NULL, 0,
+                          scale_for(d, Ld->wgu.type), s));
+        TRY(vxh_swiglu_rows(d->pf_gu, d->ld_gu, M, d->F, d->opt.ffn_gate_threshold, d->pf_h, d->F, s));
+        TRY(vxh_gemm_rows(&Ld->wd, d->pf_h, d->F, M, d->pf_x, dd, dd, d->pf_x, dd, scale_for(d, Ld->wd.type), s));
+    }
+    if (!last_logits) return VX_OK;
+    /* the last row's logits through the decode GEMM (src/model.c:598-615) */
+    if (d->acc_dirty && (e = zero_acc(d)) != VX_OK) return e;
+    const float *src = d->pf_x + (size_t)(M - 1) * dd;
+    const int V = d->V, orows = d->has_out ? d->out_rows : 0;
+    if (orows < V) TRY(vxh_fill_rows(d->logits, V, 1, orows, V - orows, -1e30f, s));
+    if (d->has_out) {
+        if (d->has_out_norm)
+            TRY(vxh_rmsnorm_panel(src, dd, 1, dd, d->out_norm, 0, NULL, 4, &d->pan_d, NULL, 0, s));
+        else
+            TRY(vxh_prep_panel(&d->pan_d, src, dd, 1, dd, 0, NULL, 4, s));
+        d->acc_dirty = 1;
+        if ((e = gemm(d, &d->out, &d->pan_d, 1, d->acc_lg, d->ld_lg, orows, VX_PROF_OUTPUT, orows)) != VX_OK)
+            return e;
+        TRY(vxh_acc_store(d->acc_lg, d->ld_lg, 1, orows, d->logits, V, NULL, 0, s));
+        d->acc_dirty = 0;
+    }
+    return VX_OK;
+}
+
 /* Runs n host tokens from cache_len on, with the reference's position clamp
  * (src/model.c:279-286): positions that fit run in batches of up to 16,
  * overflowing tokens one at a time on the last slot. */
@@ -1205,6 +1303,20 @@ vx_error vx_dev_run_tokens(vx_model *m, const int *tokens, int n, int logits_mod
     while (i < n) {
         int c = m->cache_len;
         if (c < 0) c = 0;
+        /* long prompts: chunks of up to VX_PF_ROWS rows as one large-M batch */
+        if (logits_mode != VX_LOGITS_ALL && pf_ok(d) && n - i >= d->opt.prefill_min_rows && c < n_ctx) {
+            int P = n - i;
+            if (P > VX_PF_ROWS) P = VX_PF_ROWS;
+            if (P > n_ctx - c) P = n_ctx - c;
+            if (P >= d->opt.prefill_min_rows) {
+                const int last = i + P == n && logits_mode == VX_LOGITS_LAST;
+                if ((e = forward_prefill(m, tokens + i, P, c, last)) != VX_OK) return e;
+                if (last) TRY(vxh_download(logits_host, d->logits, sizeof(float) * (size_t)V, d->stream));
+                m->cache_len = c + P;
+                i += P;
+                continue;
+            }
+        }
         int M, next_len;
         if (c < n_ctx) {
             M = n - i;

@@ -14,6 +14,7 @@
 #include "vxh.h"
 
 #define VX_MAX_BATCH 16
+#define VX_PF_ROWS 512             /* rows of one large-M prefill chunk */
 #define VX_N_COUNTERS (64 * 2048)  /* GEMM arrival counters, 64 words apart */
 
 /* ---- errors ----------------------------------------------------------------- */
@@ -101,6 +102,14 @@ typedef struct vx_dev {
      * accumulator (acc_x holds the down projection's) */
     float *x2;
     double *acc_y;
+    /* large-M prompt prefill (allocated on first use): token ids, the
+     * residual rows, normed rows, q|k|v rows, rotated q, attention rows,
+     * gate/up rows, SwiGLU rows, each [VX_PF_ROWS][...] fp32, and the
+     * attention workspace for that many rows */
+    int pf_ready;
+    int *pf_tok;
+    float *pf_x, *pf_xn, *pf_qkv, *pf_q, *pf_att, *pf_gu, *pf_h;
+    vxh_workspace pf_ws;
     /* GEMM profiling (vx_model_set_profiling) */
     int prof_on;                       /* 0: off; n: every n-th launch per class   */
     int prof_tick[VX_PROF_N];
