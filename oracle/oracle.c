@@ -532,12 +532,11 @@ static void gate_log(const or_model *m, const float *g, int F, int ti, int l)
     if (m->gate_near_idx) m->gate_near_idx[at] = bi;
 }
 
-/* Test hook: invert the skip decision of column flip_col: a skipped up row is
+/* Test hook: invert the skip decision of column i: a skipped up row is
  * computed (the same row product as an unskipped one), a computed one is zero. */
 static void gate_flip(const or_model *m, const or_mat *w, const float *xn, const float *g, float *u,
-                      int F, int d, float *tmp)
+                      int F, int d, float *tmp, int i)
 {
-    int i = m->flip_col;
     if (!(fabsf(g[i]) < m->gate_thr)) { u[i] = 0.0f; return; }
     if (!w->data) return;
     or_mat row = *w;
@@ -632,8 +631,9 @@ static int forward_impl(or_model *m, const int *tokens, int n, float *logits, in
             or_silu(g, F);
             apply_mat(m, &m->wu[l], xn, u, F, d, g, m->gate_thr, 0, tmp);
             if (m->gate_near || m->gate_near_idx) gate_log(m, g, F, ti, l);
-            if (m->flip && m->flip_tok == ti && m->flip_layer == l && m->flip_col >= 0 && m->flip_col < F)
-                gate_flip(m, &m->wu[l], xn, g, u, F, d, tmp);
+            for (int f = 0; f < m->flip && f < OR_MAX_FLIPS; f++)
+                if (m->flip_tok[f] == ti && m->flip_layer[f] == l && m->flip_col[f] >= 0 && m->flip_col[f] < F)
+                    gate_flip(m, &m->wu[l], xn, g, u, F, d, tmp, m->flip_col[f]);
             for (int i = 0; i < F; i++) g[i] = g[i] * u[i];
             /* the down projection's tail is an unwritten pad in the reference
              * (src/model.c:432-433); it is read as zeros here */

@@ -66,6 +66,8 @@ typedef struct {
     int rows, cols;    /* rows = ne[1], cols = ne[0]     */
 } or_mat;
 
+#define OR_MAX_FLIPS 4
+
 typedef struct {
     int n_layers, n_heads, n_kv_heads, n_embd, n_head_dim, n_ff, n_vocab, n_ctx;
     float rope_theta;
@@ -93,8 +95,10 @@ typedef struct {
     float *gate_near;           /* optional [n][n_layers] (n = tokens of the call):
                                    min over FFN columns i of ||silu(g_i)| - gate_thr| */
     int *gate_near_idx;         /* optional [n][n_layers]: the column i of that minimum */
-    int flip;                   /* 1: invert the skip decision of one column:          */
-    int flip_tok, flip_layer, flip_col;   /* token index within the call, layer, column */
+    int flip;                   /* number of inverted skip decisions (0..OR_MAX_FLIPS), */
+    int flip_tok[OR_MAX_FLIPS];   /* each at token index within the call, layer, column */
+    int flip_layer[OR_MAX_FLIPS];
+    int flip_col[OR_MAX_FLIPS];
 } or_model;
 
 /* x rounded to the nearest IEEE binary16 value (ties to even), as fp32:

@@ -79,7 +79,7 @@ class OrModel(C.Structure):
         ("k_cache", C.c_void_p), ("v_cache", C.c_void_p), ("cache_len", C.c_int),
         ("kv_half", C.c_int),
         ("gate_near", C.c_void_p), ("gate_near_idx", C.c_void_p), ("flip", C.c_int),
-        ("flip_tok", C.c_int), ("flip_layer", C.c_int), ("flip_col", C.c_int),
+        ("flip_tok", C.c_int * 4), ("flip_layer", C.c_int * 4), ("flip_col", C.c_int * 4),
     ]
 
 

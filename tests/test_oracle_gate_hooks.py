@@ -7,7 +7,7 @@ the threshold, and the flip reruns the oracle with exactly that decision
 inverted.  The checks below tie both hooks to independent computations:
 
 * flip of a computed column == the same model with that up row's weights
-  zeroed (bit-exact);
+  zeroed (bit-exact), and two flips == two zeroed rows;
 * flip of a skipped column == a model with no skipping whose other up rows
   are zeroed (bit-exact);
 * the logged column and distance == numpy float64 of the first layer's gate.
@@ -42,7 +42,10 @@ def run(raw, tok, thr, flip=None, log=False):
         om.m.gate_near = near.ctypes.data
         om.m.gate_near_idx = idx.ctypes.data
     if flip is not None:
-        om.m.flip, om.m.flip_tok, om.m.flip_layer, om.m.flip_col = 1, 0, 0, flip
+        cols = [flip] if np.isscalar(flip) else list(flip)
+        om.m.flip = len(cols)
+        for f, col in enumerate(cols):
+            om.m.flip_tok[f], om.m.flip_layer[f], om.m.flip_col[f] = 0, 0, col
     out = np.zeros(s["n_vocab"], np.float32)
     assert O.or_forward(om.ptr, np.array([tok], np.int32), 1, out) == 0
     return out, near, idx
@@ -60,6 +63,21 @@ def test_flip_of_computed_column_equals_zeroed_up_row(tmp_path):
     assert np.array_equal(got, want)
     base, _, _ = run(raw, 5, 0.0)
     assert not np.array_equal(base, got)
+
+
+def test_two_flips_equal_two_zeroed_up_rows(tmp_path):
+    raw = model(tmp_path)
+    cols = [17, 60]
+    got, _, _ = run(raw, 5, 0.0, flip=cols)
+    z = dict(raw)
+    up = raw["blk.0.ffn_up.weight"].copy()
+    for col in cols:
+        up[col]["d"] = 0
+    z["blk.0.ffn_up.weight"] = up
+    want, _, _ = run(z, 5, 0.0)
+    assert np.array_equal(got, want)
+    one, _, _ = run(raw, 5, 0.0, flip=cols[0])
+    assert not np.array_equal(one, got)
 
 
 def test_flip_of_skipped_column_equals_single_unskipped_row(tmp_path):

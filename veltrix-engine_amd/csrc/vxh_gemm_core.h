@@ -646,18 +646,44 @@ __global__ __launch_bounds__(256) void vx_gemm_kernel(vx_gemm_args a)
         }
     }
 
-    // 3. this slice's contribution, added in fp64
+    // 3. this slice's contribution, added in fp64.  Every load of the flush
+    // (row scales, sums of squares, gate values) is issued before any of it
+    // is used: with the loads inside the per-row branches each row waited
+    // for its own round trip (at M = 9 five in a row; measured on MI355X,
+    // 4096x4096 8.46 -> 6.56 us, 22016x4096 18.59 -> 16.90 us).
     const int n = T * 32 + c;
-    if (tile_ok && n < a.n_out) {
-        const int chunk = p0 / a.rs_chunk;
+    const bool out_ok = tile_ok && n < a.n_out;
+    const int chunk = p0 / a.rs_chunk;
+    float osc[R1];
+#pragma unroll
+    for (int r = 0; r < R1; r++) {
+        const int m = min(8 * (r / 4) + 4 * h + (r % 4), M - 1);
+        osc[r] = (PANEL ? a.rscale[m * a.rs_ld + chunk] : lrs[m]) * a.scale;
+    }
+    if (a.ss) {
+        double ssv[R1];
+#pragma unroll
+        for (int r = 0; r < R1; r++) ssv[r] = a.ss[min(8 * (r / 4) + 4 * h + (r % 4), M - 1)];
+#pragma unroll
+        for (int r = 0; r < R1; r++) osc[r] *= vx_rms_inv((float)ssv[r], a.ss_K);
+    }
+    bool keep[R1];
+#pragma unroll
+    for (int r = 0; r < R1; r++) keep[r] = 8 * (r / 4) + 4 * h + (r % 4) < M;
+    if (a.gate && out_ok) {
+        float gv[R1];
+#pragma unroll
+        for (int r = 0; r < R1; r++)
+            gv[r] = a.gate[(size_t)min(8 * (r / 4) + 4 * h + (r % 4), M - 1) * a.ld_gate + n];
+#pragma unroll
+        for (int r = 0; r < R1; r++) keep[r] = keep[r] && !(fabsf(gv[r]) < a.thr);
+    }
+    if (out_ok) {
 #pragma unroll
         for (int r = 0; r < R1; r++) {
+            if (!keep[r]) continue;
             const int m = 8 * (r / 4) + 4 * h + (r % 4);
-            if (m >= M) continue;
-            if (a.gate && fabsf(a.gate[(size_t)m * a.ld_gate + n]) < a.thr) continue;
-            float osc = (PANEL ? a.rscale[m * a.rs_ld + chunk] : lrs[m]) * a.scale;
-            if (a.ss) osc *= vx_rms_inv((float)a.ss[m], a.ss_K);
-            const float v = (acc[r] + acc[r + 8]) * osc;
+            const float v = (acc[r] + acc[r + 8]) * osc[r];
             __hip_atomic_fetch_add(&a.acc[(size_t)m * a.ld_acc + n], (double)v, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
         }
