@@ -77,9 +77,13 @@ int vxh_graph_destroy(vxh_graph g);
  *   both  d : [tile][block pair p][row 32] -> (d[2p], d[2p+1]) as two fp16.
  *
  * Byte count equals GGUF's (18 or 34 bytes per 32 weights) apart from padding
- * rows to a multiple of 32 and blocks to an even count (padding has d = 0). */
+ * rows to a multiple of 32 and blocks to an even count (padding has d = 0).
+ *
+ *   F32   qs: [row][n_pairs * 64] fp32, zero past n_cols and the logical rows;
+ *             d unused.  GEMMs read it through vxh_gemm_acc only (exact,
+ *             non-AVX2 panels); gathers copy rows unscaled. */
 typedef struct {
-    int type;          /* 2 = Q4_0, 8 = Q8_0 (vx_type / GGML ids)           */
+    int type;          /* 2 = Q4_0, 8 = Q8_0, 0 = F32 (vx_type / GGML ids)  */
     int n_rows;        /* physical rows, a multiple of 32                     */
     int n_cols;        /* K, a multiple of 32                                 */
     int n_pairs;       /* ceil(K/64): block pairs per row                     */
@@ -105,7 +109,8 @@ int vxh_qmat_get_rows(const vxh_qmat *m, void *host_dst, int n_rows, int group,
 int vxh_synth_blocks(void *dev_blocks, int type, int n_rows, int n_cols, uint64_t seed,
                      float std, vxh_stream s);
 /* Gather rows of a tiled matrix as fp32: out[i][:] = scale * dequant(row
- * ids[i]) for i < n (ids read from device memory; out-of-range ids -> zeros).
+ * ids[i]) for i < n (ids read from device memory; out-of-range ids -> zeros;
+ * F32 rows are copied without the scale, as the reference copies them).
  * Replaces the embedding lookup of src/model.c:454-500. */
 int vxh_qmat_gather_rows(const vxh_qmat *m, const int *dev_ids, int n, float scale,
                          float *out, int ld_out, vxh_stream s);

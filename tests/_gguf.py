@@ -97,7 +97,8 @@ def llama_gguf(path, rng, n_layers, n_embd, n_heads, n_kv_heads, n_ff, n_vocab,
                rope_theta=10000.0, std=0.02, with_attn_output=True, norm_random=False,
                emb_type=GGML_Q4_0, out_type=GGML_Q4_0, with_output=True, matrix_type=GGML_Q4_0):
     """Write a random-init Llama-style model (weights N(0, std) quantised with
-    the reference quantiser, norms F32).  Returns dict of the raw arrays."""
+    the reference quantiser or kept F32, norms F32).  Returns dict of the raw
+    arrays."""
     hd = n_embd // n_heads
     kvd = n_kv_heads * hd
     kv = [
@@ -115,7 +116,9 @@ def llama_gguf(path, rng, n_layers, n_embd, n_heads, n_kv_heads, n_ff, n_vocab,
 
     def qmat(name, rows, cols, gt=GGML_Q4_0):
         w = rng.normal(0.0, std, size=(rows, cols)).astype(np.float32)
-        if gt == GGML_Q4_0:
+        if gt == GGML_F32:
+            b = w
+        elif gt == GGML_Q4_0:
             b = quantize_q4_0_np(w)
         else:
             b = quantize_q8_0_np(w)

@@ -15,7 +15,7 @@ import numpy as np
 import pytest
 
 import _native as N
-from _gguf import llama_gguf, GGML_Q8_0, GGML_Q4_0
+from _gguf import llama_gguf, GGML_F32, GGML_Q8_0, GGML_Q4_0
 from _oracle_model import OracleModel
 
 O = N.oracle()
@@ -49,20 +49,23 @@ def ref_forward_logits(path, tokens, n_vocab, n_ctx=None, chunks=None):
 
 
 CASES = [
-    # layers, d, heads, kv, ff, vocab, attn_output, emb, out
-    (2, 64, 4, 2, 128, 96, True, GGML_Q4_0, GGML_Q4_0),
-    (2, 128, 4, 1, 256, 160, False, GGML_Q4_0, GGML_Q4_0),
-    (1, 96, 3, 3, 192, 64, True, GGML_Q8_0, GGML_Q8_0),
+    # layers, d, heads, kv, ff, vocab, attn_output, emb, out, layer matrices
+    (2, 64, 4, 2, 128, 96, True, GGML_Q4_0, GGML_Q4_0, GGML_Q4_0),
+    (2, 128, 4, 1, 256, 160, False, GGML_Q4_0, GGML_Q4_0, GGML_Q4_0),
+    (1, 96, 3, 3, 192, 64, True, GGML_Q8_0, GGML_Q8_0, GGML_Q4_0),
+    # F32 matrices (src/model.c:174-179, 206-211) and an F32 embedding (:459-463)
+    (2, 64, 4, 2, 128, 96, True, GGML_F32, GGML_F32, GGML_F32),
+    (1, 96, 3, 1, 192, 64, False, GGML_Q4_0, GGML_F32, GGML_F32),
 ]
 
 
 @pytest.mark.parametrize("case", CASES)
 def test_oracle_forward_matches_reference(tmp_path, case):
-    L, d, h, kv, ff, V, with_o, et, ot = case
+    L, d, h, kv, ff, V, with_o, et, ot, mt = case
     rng = np.random.default_rng(sum(case[:6]))
     path = str(tmp_path / "m.gguf")
     raw = llama_gguf(path, rng, L, d, h, kv, ff, V, std=0.05, with_attn_output=with_o,
-                     norm_random=True, emb_type=et, out_type=ot)
+                     norm_random=True, emb_type=et, out_type=ot, matrix_type=mt)
     tokens = rng.integers(0, V, 12).astype(np.int32)
     ref_logits, conf, ref_len = ref_forward_logits(path, tokens, V)
     assert conf[:7] == (L, h, kv, d, d // h, ff, V)

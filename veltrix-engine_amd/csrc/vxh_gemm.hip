@@ -660,6 +660,128 @@ static int vx_dot_dispatch(const vxh_qmat *W, int M, vx_gemm_args &a, hipStream_
     }
 }
 
+// ---------------------------------------------------------------------------
+// F32 weight matrices (src/model.c:174-179, 206-211 dispatch them to the fp32
+// GEMV): the workgroup decodes its 512-column slice of the panel to fp32
+// (hi + lo, exact) in LDS; wavefront w takes 16 output rows, 4 lanes per row
+// with float4 weight loads; the products of an fp32 weight and a 22-bit
+// activation are exact in fp64, so each row's slice sum is accumulated in
+// fp64 and added to the accumulator with the slice's row scale.
+// ---------------------------------------------------------------------------
+#define VX_F32_KS 512    // columns per workgroup slice (divides the 1024-column scale chunk)
+#define VX_F32_ROWS 64   // output rows per workgroup
+
+template <int M>
+__global__ __launch_bounds__(256) void vx_gemm_f32_kernel(vx_gemm_args a, int K, int n_ks)
+{
+    __shared__ float4 xs[M][VX_F32_KS / 4];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int grp = blockIdx.x / n_ks, ks = blockIdx.x % n_ks;
+    const int k0 = ks * VX_F32_KS, kn = min(VX_F32_KS, K - k0);   // K % 32 == 0, so kn % 32 == 0
+    // panel unit of column group g, row m: ((g/4 * 2 + g%2) * 2 + (g/2)%2) * 2M + m (hi), + M (lo)
+    for (int it = threadIdx.x; it < M * (VX_F32_KS / 8); it += 256) {
+        const int m = it / (VX_F32_KS / 8), gl = it % (VX_F32_KS / 8), g = k0 / 8 + gl;
+        float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (8 * gl < kn) {
+            const size_t base = ((size_t)((g >> 2) * 2 + (g & 1)) * 2 + ((g >> 1) & 1)) * (2 * M);
+            const vx_half8 hi = __builtin_bit_cast(vx_half8, a.panel[base + m]);
+            const vx_half8 lo = __builtin_bit_cast(vx_half8, a.panel[base + M + m]);
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[e] = (float)hi[e] + (float)lo[e];
+        }
+        xs[m][2 * gl] = make_float4(v[0], v[1], v[2], v[3]);
+        xs[m][2 * gl + 1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
+    __syncthreads();
+    const int r = lane >> 2, kq = lane & 3;
+    const int n = grp * VX_F32_ROWS + wave * 16 + r;
+    const int ldw = a.n_pairs * 64;
+    const float *wr = (const float *)a.wq + (size_t)min(n, a.n_tiles * 32 - 1) * ldw + k0;
+    double acc[M];
+#pragma unroll
+    for (int m = 0; m < M; m++) acc[m] = 0.0;
+#pragma unroll 8
+    for (int j = 0; j < VX_F32_KS / 16; j++) {
+        const int k = 16 * j + 4 * kq;
+        if (k >= kn) break;
+        const float4 w = *(const float4 *)(wr + k);
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            const float4 x = xs[m][k / 4];
+            acc[m] = fma((double)w.x, (double)x.x, acc[m]);
+            acc[m] = fma((double)w.y, (double)x.y, acc[m]);
+            acc[m] = fma((double)w.z, (double)x.z, acc[m]);
+            acc[m] = fma((double)w.w, (double)x.w, acc[m]);
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+        acc[m] += __shfl_xor(acc[m], 1);
+        acc[m] += __shfl_xor(acc[m], 2);
+    }
+    if (kq != 0 || n >= a.n_out) return;
+    const int chunk = (k0 / 64) / a.rs_chunk;
+    float osc[M];
+#pragma unroll
+    for (int m = 0; m < M; m++) osc[m] = a.rscale[m * a.rs_ld + chunk] * a.scale;
+    bool keep[M];
+#pragma unroll
+    for (int m = 0; m < M; m++) keep[m] = true;
+    if (a.gate) {
+        float gv[M];
+#pragma unroll
+        for (int m = 0; m < M; m++) gv[m] = a.gate[(size_t)m * a.ld_gate + n];
+#pragma unroll
+        for (int m = 0; m < M; m++) keep[m] = !(fabsf(gv[m]) < a.thr);
+    }
+#pragma unroll
+    for (int m = 0; m < M; m++)
+        if (keep[m])
+            __hip_atomic_fetch_add(&a.acc[(size_t)m * a.ld_acc + n], acc[m] * (double)osc[m], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int M>
+static int vx_launch_f32(const vxh_qmat *W, vx_gemm_args &a, hipStream_t st, hipEvent_t e0, hipEvent_t e1)
+{
+    a.n_tiles = W->n_rows / 32;
+    a.n_pairs = W->n_pairs;
+    const int K = W->n_cols;
+    const int n_ks = (K + VX_F32_KS - 1) / VX_F32_KS;
+    const int groups = (a.n_out + VX_F32_ROWS - 1) / VX_F32_ROWS;
+    if (a.rs_ld > 1 && (a.rs_chunk * 64) % VX_F32_KS)
+        return vxh_fail(VXH_ERR_PARAM, "gemm f32: slice of %d columns crosses a scale chunk", VX_F32_KS);
+    if (e0 || e1)
+        hipExtLaunchKernelGGL(vx_gemm_f32_kernel<M>, dim3(groups * n_ks), dim3(256), 0, st, e0, e1, 0, a, K, n_ks);
+    else
+        vx_gemm_f32_kernel<M><<<groups * n_ks, 256, 0, st>>>(a, K, n_ks);
+    VXH_LAUNCHED();
+    return VXH_OK;
+}
+
+static int vx_f32_dispatch(const vxh_qmat *W, int M, vx_gemm_args &a, hipStream_t st, hipEvent_t e0,
+                           hipEvent_t e1)
+{
+    switch (M) {
+    case 1: return vx_launch_f32<1>(W, a, st, e0, e1);
+    case 2: return vx_launch_f32<2>(W, a, st, e0, e1);
+    case 3: return vx_launch_f32<3>(W, a, st, e0, e1);
+    case 4: return vx_launch_f32<4>(W, a, st, e0, e1);
+    case 5: return vx_launch_f32<5>(W, a, st, e0, e1);
+    case 6: return vx_launch_f32<6>(W, a, st, e0, e1);
+    case 7: return vx_launch_f32<7>(W, a, st, e0, e1);
+    case 8: return vx_launch_f32<8>(W, a, st, e0, e1);
+    case 9: return vx_launch_f32<9>(W, a, st, e0, e1);
+    case 10: return vx_launch_f32<10>(W, a, st, e0, e1);
+    case 11: return vx_launch_f32<11>(W, a, st, e0, e1);
+    case 12: return vx_launch_f32<12>(W, a, st, e0, e1);
+    case 13: return vx_launch_f32<13>(W, a, st, e0, e1);
+    case 14: return vx_launch_f32<14>(W, a, st, e0, e1);
+    case 15: return vx_launch_f32<15>(W, a, st, e0, e1);
+    default: return vx_launch_f32<16>(W, a, st, e0, e1);
+    }
+}
+
 extern "C" int vxh_gemm_acc_timed(const vxh_qmat *W, const vxh_panel *X, int M, double *acc,
                                   int ld_acc, int n_out, float scale, const float *gate, int ld_gate,
                                   float thr, int path, vxh_event start, vxh_event stop, vxh_stream s)
@@ -689,6 +811,10 @@ extern "C" int vxh_gemm_acc_timed(const vxh_qmat *W, const vxh_panel *X, int M, 
     a.gate = gate;
     a.ld_gate = ld_gate;
     a.thr = thr;
+    if (W->type == 0) {
+        if (X->avx2) return vxh_fail(VXH_ERR_UNSUPPORTED, "F32 matrices take exact panels");
+        return vx_f32_dispatch(W, M, a, vxh_hs(s), (hipEvent_t)start, (hipEvent_t)stop);
+    }
     if (path == VXH_PATH_DOT) return vx_dot_dispatch(W, M, a, vxh_hs(s), (hipEvent_t)start, (hipEvent_t)stop);
     return vx_dispatch<VX_EPI_NONE>(W, M, X->avx2, a, vxh_hs(s), (hipEvent_t)start, (hipEvent_t)stop);
 }

@@ -775,6 +775,8 @@ template <int M, int EPI, int PRO>
 static int vx_dispatch_m(const vxh_qmat *W, int avx2, vx_gemm_args &a, hipStream_t st, hipEvent_t e0,
                          hipEvent_t e1)
 {
+    if (W->type != 2 && W->type != 8)
+        return vxh_fail(VXH_ERR_UNSUPPORTED, "matrix type %d: this GEMM takes Q4_0 and Q8_0", W->type);
     if (W->type == 2) {
         if constexpr (EPI == VX_EPI_NONE && PRO == VX_PRO_PANEL)
             if (avx2) return vx_launch_gemm<2, M, true, EPI, PRO>(W, a, st, e0, e1);

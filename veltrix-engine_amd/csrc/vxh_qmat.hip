@@ -17,12 +17,22 @@ __host__ __device__ static inline int vx_block_bytes(int type) { return type == 
 extern "C" int vxh_qmat_alloc(vxh_qmat *m, int type, int n_rows, int n_cols)
 {
     memset(m, 0, sizeof(*m));
-    if ((type != 2 && type != 8) || n_rows <= 0 || n_cols <= 0 || n_cols % 32)
+    if ((type != 0 && type != 2 && type != 8) || n_rows <= 0 || n_cols <= 0 || n_cols % 32)
         return vxh_fail(VXH_ERR_PARAM, "qmat_alloc: type %d rows %d cols %d", type, n_rows, n_cols);
     m->type = type;
     m->n_rows = (n_rows + 31) / 32 * 32;
     m->n_cols = n_cols;
     m->n_pairs = (n_cols / 32 + 1) / 2;
+    if (type == 0) {
+        // F32: plain rows of n_pairs * 64 floats, zero past n_cols and past
+        // the logical rows
+        size_t bytes = (size_t)m->n_rows * m->n_pairs * 64 * sizeof(float);
+        int rc = vxh_malloc(&m->qs, bytes);
+        if (rc) return rc;
+        VXH_CHECK(hipMemset(m->qs, 0, bytes));
+        VXH_CHECK(hipDeviceSynchronize());
+        return VXH_OK;
+    }
     size_t tiles = (size_t)m->n_rows / 32;
     size_t qs_bytes = tiles * m->n_pairs * (type == 2 ? 1024u : 2048u);
     size_t d_bytes = tiles * m->n_pairs * 32u * 4u;
@@ -163,6 +173,21 @@ __global__ void vx_unrepack_kernel(uint8_t *__restrict__ dstb, int type, int n_r
     }
 }
 
+// F32 rows: src[r][0..n_cols) <-> the matrix's physical row of r (row stride
+// ld floats).  One thread per float4.
+__global__ void vx_f32_rows_kernel(const float *__restrict__ src, float *__restrict__ dst, int n_rows,
+                                   int n_cols, int ld, int group, int group_stride, int row_offset, int to_matrix)
+{
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const int c4 = n_cols / 4;
+    if (i >= (long)n_rows * c4) return;
+    const int r = (int)(i / c4), k = (int)(i % c4) * 4;
+    const size_t pm = (size_t)vx_phys_row(r, group, group_stride, row_offset) * ld + k;
+    const size_t pr = (size_t)r * n_cols + k;
+    if (to_matrix) *(float4 *)(dst + pm) = *(const float4 *)(src + pr);
+    else *(float4 *)(dst + pr) = *(const float4 *)(src + pm);
+}
+
 static int check_map(const vxh_qmat *m, int n_rows, int group, int group_stride, int row_offset)
 {
     if (n_rows <= 0 || group <= 0) return vxh_fail(VXH_ERR_PARAM, "qmat rows: n_rows %d group %d", n_rows, group);
@@ -178,7 +203,8 @@ extern "C" int vxh_qmat_set_rows(vxh_qmat *m, const void *src, int src_on_device
     int rc = check_map(m, n_rows, group, group_stride, row_offset);
     if (rc) return rc;
     int nb = m->n_cols / 32;
-    size_t bytes = (size_t)n_rows * nb * vx_block_bytes(m->type);
+    size_t bytes = m->type == 0 ? (size_t)n_rows * m->n_cols * sizeof(float)
+                                : (size_t)n_rows * nb * vx_block_bytes(m->type);
     const void *dsrc = src;
     void *stage = nullptr;
     if (!src_on_device) {
@@ -187,10 +213,17 @@ extern "C" int vxh_qmat_set_rows(vxh_qmat *m, const void *src, int src_on_device
         VXH_CHECK(hipMemcpyAsync(stage, src, bytes, hipMemcpyHostToDevice, vxh_hs(s)));
         dsrc = stage;
     }
-    long n = (long)n_rows * m->n_pairs;
-    vx_repack_kernel<<<(unsigned)((n + 255) / 256), 256, 0, vxh_hs(s)>>>(
-        (const uint8_t *)dsrc, m->type, n_rows, nb, m->n_pairs, group, group_stride, row_offset,
-        (uint32_t *)m->qs, (uint32_t *)m->d);
+    if (m->type == 0) {
+        long n = (long)n_rows * (m->n_cols / 4);
+        vx_f32_rows_kernel<<<(unsigned)((n + 255) / 256), 256, 0, vxh_hs(s)>>>(
+            (const float *)dsrc, (float *)m->qs, n_rows, m->n_cols, m->n_pairs * 64, group, group_stride,
+            row_offset, 1);
+    } else {
+        long n = (long)n_rows * m->n_pairs;
+        vx_repack_kernel<<<(unsigned)((n + 255) / 256), 256, 0, vxh_hs(s)>>>(
+            (const uint8_t *)dsrc, m->type, n_rows, nb, m->n_pairs, group, group_stride, row_offset,
+            (uint32_t *)m->qs, (uint32_t *)m->d);
+    }
     VXH_LAUNCHED();
     if (stage) {
         VXH_CHECK(hipStreamSynchronize(vxh_hs(s)));
@@ -205,14 +238,22 @@ extern "C" int vxh_qmat_get_rows(const vxh_qmat *m, void *host_dst, int n_rows, 
     int rc = check_map(m, n_rows, group, group_stride, row_offset);
     if (rc) return rc;
     int nb = m->n_cols / 32;
-    size_t bytes = (size_t)n_rows * nb * vx_block_bytes(m->type);
+    size_t bytes = m->type == 0 ? (size_t)n_rows * m->n_cols * sizeof(float)
+                                : (size_t)n_rows * nb * vx_block_bytes(m->type);
     void *stage = nullptr;
     rc = vxh_malloc(&stage, bytes);
     if (rc) return rc;
-    long n = (long)n_rows * m->n_pairs;
-    vx_unrepack_kernel<<<(unsigned)((n + 255) / 256), 256, 0, vxh_hs(s)>>>(
-        (uint8_t *)stage, m->type, n_rows, nb, m->n_pairs, group, group_stride, row_offset,
-        (const uint32_t *)m->qs, (const uint32_t *)m->d);
+    if (m->type == 0) {
+        long n = (long)n_rows * (m->n_cols / 4);
+        vx_f32_rows_kernel<<<(unsigned)((n + 255) / 256), 256, 0, vxh_hs(s)>>>(
+            (const float *)m->qs, (float *)stage, n_rows, m->n_cols, m->n_pairs * 64, group, group_stride,
+            row_offset, 0);
+    } else {
+        long n = (long)n_rows * m->n_pairs;
+        vx_unrepack_kernel<<<(unsigned)((n + 255) / 256), 256, 0, vxh_hs(s)>>>(
+            (uint8_t *)stage, m->type, n_rows, nb, m->n_pairs, group, group_stride, row_offset,
+            (const uint32_t *)m->qs, (const uint32_t *)m->d);
+    }
     VXH_LAUNCHED();
     VXH_CHECK(hipMemcpyAsync(host_dst, stage, bytes, hipMemcpyDeviceToHost, vxh_hs(s)));
     VXH_CHECK(hipStreamSynchronize(vxh_hs(s)));
@@ -318,6 +359,10 @@ __global__ void vx_gather_kernel(const uint32_t *__restrict__ qs, const uint32_t
     float *o = out + (size_t)i * ld_out;
     for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < n_cols; c += gridDim.x * blockDim.x) {
         if (id < 0 || id >= n_rows_logical) { o[c] = 0.0f; continue; }
+        if (type == 0) {   // F32 rows are copied as they are (src/model.c:459-463)
+            o[c] = ((const float *)qs)[(size_t)id * n_pairs * 64 + c];
+            continue;
+        }
         int T = id / 32, j = id % 32;
         int b = c / 32, e = c % 32, p = b / 2, blk = b % 2, h = e / 16;
         uint32_t dd = dpl[((size_t)T * n_pairs + p) * 32 + j];

@@ -338,13 +338,19 @@ vx_error vx_dev_ensure_kv(vx_model *m)
 /* --------------------------------------------------------------------------- */
 /* creation from GGUF                                                           */
 /* --------------------------------------------------------------------------- */
-static int is_mat_type(int t) { return t == VX_TYPE_Q4_0 || t == VX_TYPE_Q8_0; }
+static int is_quant_type(int t) { return t == VX_TYPE_Q4_0 || t == VX_TYPE_Q8_0; }
+/* matrix types a GGUF may carry: the quantised ones and F32 (src/model.c:174-179, 206-211) */
+static int is_mat_type(int t) { return is_quant_type(t) || t == VX_TYPE_F32; }
 
 static vx_error check_mat(const vx_gguf_tensor *t, int rows, int cols, int *type)
 {
     if (!t) return VX_OK;
     if (!is_mat_type(t->type)) {
-        vx_set_error("%s: type %d not supported (Q4_0 and Q8_0 only)", t->name, t->type);
+        vx_set_error("%s: type %d not supported (Q4_0, Q8_0 and F32 only)", t->name, t->type);
+        return VX_ERR_UNSUPPORTED;
+    }
+    if (t->type == VX_TYPE_F32 && cols % 32) {
+        vx_set_error("%s: F32 rows of %d columns (a multiple of 32 needed)", t->name, cols);
         return VX_ERR_UNSUPPORTED;
     }
     if (t->ne[0] != cols || t->ne[1] != rows) {
@@ -352,7 +358,8 @@ static vx_error check_mat(const vx_gguf_tensor *t, int rows, int cols, int *type
                      (long long)t->ne[0], rows, cols);
         return VX_ERR_FORMAT;
     }
-    size_t need = (size_t)rows * (cols / 32) * (t->type == VX_TYPE_Q4_0 ? 18 : 34);
+    size_t need = t->type == VX_TYPE_F32 ? (size_t)rows * cols * sizeof(float)
+                                         : (size_t)rows * (cols / 32) * (t->type == VX_TYPE_Q4_0 ? 18 : 34);
     if (t->nbytes < need) {
         vx_set_error("%s: truncated (%zu of %zu bytes)", t->name, t->nbytes, need);
         return VX_ERR_FORMAT;
@@ -422,6 +429,7 @@ static vx_error create_from_gguf(vx_gguf *g, vx_model *m)
             if ((e = put_rows(d, &d->out, to->data, 0, rows, rows, 0, 0)) != VX_OK) return e;
             d->has_out = 1;
             d->out_rows = rows;
+            if (to->type == VX_TYPE_F32) d->has_f32 = 1;
         }
     }
     if (tn) {
@@ -456,6 +464,7 @@ static vx_error create_from_gguf(vx_gguf *g, vx_model *m)
         if (tqkv < 0) tqkv = VX_TYPE_Q4_0;
         if (tgu < 0) tgu = VX_TYPE_Q4_0;
         if (td1 < 0) td1 = VX_TYPE_Q4_0;
+        if (tqkv == VX_TYPE_F32 || tgu == VX_TYPE_F32 || td1 == VX_TYPE_F32 || to1 == VX_TYPE_F32) d->has_f32 = 1;
         TRY(vxh_qmat_alloc(&Ld->wqkv, tqkv, dd + 2 * kvd, dd));
         if (tq && (e = put_rows(d, &Ld->wqkv, tq->data, 0, dd, dd, 0, 0))) return e;
         if (tk && (e = put_rows(d, &Ld->wqkv, tk->data, 0, kvd, kvd, 0, dd))) return e;
@@ -524,7 +533,7 @@ vx_error vx_model_create_synthetic(const vx_model_config *cfg, const vx_synth_sp
     if (!cfg || !spec || !out) return VX_ERR_PARAM;
     *out = NULL;
     int mt = spec->matrix_type, et = spec->embd_type, ot = spec->output_type;
-    if (!is_mat_type(mt) || !is_mat_type(et) || !is_mat_type(ot)) return VX_ERR_UNSUPPORTED;
+    if (!is_quant_type(mt) || !is_quant_type(et) || !is_quant_type(ot)) return VX_ERR_UNSUPPORTED;
     vx_model *m = (vx_model *)calloc(1, sizeof(vx_model));
     if (!m) return VX_ERR_MEMORY;
     vx_model_config *c = &m->config;
@@ -659,9 +668,9 @@ vx_error vx_model_set_options(vx_model *m, const vx_model_options *opt)
         int has_o = 1;
         for (int l = 0; l < d->n_layers; l++) has_o &= d->layers[l].has_o;
         if (opt->fused != VX_FUSED_PROLOGUE || opt->q4_kernel != VX_Q4_EXACT || opt->pro_max_rows < VX_MAX_BATCH ||
-            (d->hd != 64 && d->hd != 128) || !has_o) {
-            vx_set_error("fp16 KV cache: needs the prologue path, exact Q4_0, pro_max_rows >= %d and "
-                         "head_dim 64 or 128", VX_MAX_BATCH);
+            (d->hd != 64 && d->hd != 128) || !has_o || d->has_f32) {
+            vx_set_error("fp16 KV cache: needs the prologue path, exact Q4_0, pro_max_rows >= %d, "
+                         "head_dim 64 or 128 and no F32 matrices", VX_MAX_BATCH);
             return VX_ERR_UNSUPPORTED;
         }
     }
@@ -699,6 +708,7 @@ static float scale_for(const vx_dev *d, int type)
      * reference; the x86 Q4_0 kernel bypasses it (src/model.c:212-244) */
     float s = vx_get_synthetic_weight_scale();
     if (type == VX_TYPE_Q4_0 && d->opt.q4_kernel == VX_Q4_AVX2_LANES) return 1.0f;
+    if (type == VX_TYPE_F32) return 1.0f;   /* F32 GEMVs read the weights as they are */
     return s;
 }
 
@@ -816,7 +826,7 @@ static vx_error zero_acc(vx_dev *d)
  * the exact one (the AVX2-lane tails need the separate row kernels). */
 static int fused_ok(const vx_dev *d)
 {
-    if (d->opt.fused != VX_FUSED_EPILOGUE || d->opt.q4_kernel != VX_Q4_EXACT) return 0;
+    if (d->opt.fused != VX_FUSED_EPILOGUE || d->opt.q4_kernel != VX_Q4_EXACT || d->has_f32) return 0;
     if ((d->d + 2 * d->kvd) % 32 || d->hd % 8 || d->F % 32) return 0;
     for (int l = 0; l < d->n_layers; l++)
         if (!d->layers[l].has_o) return 0;
@@ -947,7 +957,7 @@ static vx_error forward_fused(vx_model *m, int M, int n_past, int logits_mode)
 static int pro_ok(const vx_dev *d, int M)
 {
     if (d->opt.fused != VX_FUSED_PROLOGUE || M > d->opt.pro_max_rows) return 0;
-    if (d->opt.q4_kernel != VX_Q4_EXACT) return 0;
+    if (d->opt.q4_kernel != VX_Q4_EXACT || d->has_f32) return 0;
     for (int l = 0; l < d->n_layers; l++)
         if (!d->layers[l].has_o) return 0;
     return 1;
@@ -1209,7 +1219,7 @@ vx_error vx_dev_forward(vx_model *m, int M, int n_past, int logits_mode)
 static int pf_ok(const vx_dev *d)
 {
     return d->opt.prefill_min_rows > 0 && d->opt.q4_kernel == VX_Q4_EXACT && !d->opt.kv_half &&
-           d->hd % 4 == 0 && d->hd <= 128;
+           !d->has_f32 && d->hd % 4 == 0 && d->hd <= 128;
 }
 
 static vx_error pf_alloc(vx_dev *d)
@@ -1397,7 +1407,8 @@ vx_error vx_model_read_tensor(const vx_model *m, const char *name, void *dst, si
         if (q && !group) group = rows;
     }
     if (!q) { vx_set_error("no device matrix named %s", name); return VX_ERR_PARAM; }
-    size_t need = (size_t)rows * (q->n_cols / 32) * (q->type == VX_TYPE_Q4_0 ? 18 : 34);
+    size_t need = q->type == VX_TYPE_F32 ? (size_t)rows * q->n_cols * sizeof(float)
+                                         : (size_t)rows * (q->n_cols / 32) * (q->type == VX_TYPE_Q4_0 ? 18 : 34);
     if (bytes < need) { vx_set_error("%s needs %zu bytes", name, need); return VX_ERR_PARAM; }
     TRY(vxh_qmat_get_rows(q, dst, rows, group, stride, off, d->stream));
     return VX_OK;

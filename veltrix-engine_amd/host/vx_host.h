@@ -68,6 +68,7 @@ typedef struct vx_dev {
     int has_out, out_rows;
     float *out_norm;
     int has_out_norm;
+    int has_f32;                       /* an F32 layer or output matrix: the plain-panel forward only */
     /* KV cache and RoPE tables, allocated on first use */
     int n_ctx_alloc;
     unsigned kv_gen;                   /* bumped whenever the cache is allocated or dropped */
