@@ -877,6 +877,8 @@ def main():
     ap.add_argument("--prof-every", type=int, default=7,
                     help="time every n-th verify GEMM of each class with kernel events")
     args = ap.parse_args()
+    if args.prof_steps < 1 or args.prof_every < 1:
+        ap.error("--prof-steps and --prof-every must be at least 1 (the roofline comes from that pass)")
     ws = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or ws != 1:
         print(f"bench.py: this engine runs the verify path on ONE GPU; --gpus {args.gpus} "
