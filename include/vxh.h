@@ -370,13 +370,20 @@ int vxh_gemm_fused(const vxh_qmat *W, const vxh_xpanel *X, int M, double *acc, i
  * The reference runs a prompt one token per forward (src/speculative.c:100-107,
  * src/model.c:450-616); these run a chunk of prompt rows as one batch.
  *
+ * vxh_rows_panel: fp32 rows X[M][ldx] (16-byte aligned, ldx % 4 == 0,
+ * K % 32 == 0) converted once into the large-M GEMM's activation operand:
+ * fp16 hi + lo of every element, laid out as the GEMM's LDS stages
+ * ([64-row group][64-column pair][16 KiB]); vxh_rows_panel_bytes(M, K) bytes.
+ *
  * vxh_gemm_rows: Y[m][n] = (R ? R[m][n] : 0) + scale * sum_k X[m][k] W[n][k]
- * for m < M (any M >= 1), n < n_out, from fp32 rows X[M][ldx] (16-byte
- * aligned, ldx % 4 == 0, K = W->n_cols).  Compute-bound MFMA tiles of 64 rows
- * x 128 columns; weights enter as the exact fp16 pair d*q = hi + lo and the
- * activations as fp16 hi + lo, summed over all of K in fp32 (within the fp32
- * GEMV's rounding of src/quantize.c:728-750).  Y may alias R. */
-int vxh_gemm_rows(const vxh_qmat *W, const float *X, int ldx, int M, float *Y, int ldy, int n_out,
+ * for m < M (any M >= 1), n < n_out, from the rows panel of X (built with
+ * K = W->n_cols).  Compute-bound MFMA tiles of 64 rows x 128 columns;
+ * weights enter as the exact fp16 pair d*q = hi + lo and the activations as
+ * fp16 hi + lo, summed over all of K in fp32 (within the fp32 GEMV's
+ * rounding of src/quantize.c:728-750).  Y may alias R. */
+size_t vxh_rows_panel_bytes(int M, int K);
+int vxh_rows_panel(const float *X, int ldx, int M, int K, void *px, vxh_stream s);
+int vxh_gemm_rows(const vxh_qmat *W, const void *px, int M, float *Y, int ldy, int n_out,
                   const float *R, int ldr, float scale, vxh_stream s);
 /* vxh_rope_kv for fp32 q|k|v rows qkv[M][ld_qkv] (no deferred norm, not
  * cleared): rotated q to q_out[M][ldq], k and v into the cache rows. */

@@ -27,8 +27,8 @@ struct vx_pf_args {
     const uint4 *wq;
     const uint32_t *wd;
     int n_tiles, n_pairs, K;
-    const float *x;
-    int ldx, M;
+    const uint4 *px;   // rows panel (vxh_rows_panel): [row group][pair][PF_STAGE units]
+    int M;
     float *y;
     int ldy, n_out;
     const float *r;
@@ -37,11 +37,14 @@ struct vx_pf_args {
 };
 
 // Workgroup = 4 wavefronts = 4 weight tiles of 32 rows (128 output columns)
-// x PF_BM activation rows.  Per block pair (64 of K) the workgroup stages the
-// activation slice in LDS as MFMA A units (lane l: row l%32, elements
-// 16(l/32) + 8s .. +7 of block blk, matching the weight layout's lane split),
-// hi and lo, double-buffered: pair p+1 is converted into the other buffer
-// while pair p is multiplied, one barrier per pair.  Each wavefront keeps
+// x PF_BM activation rows.  Per block pair (64 of K) the workgroup copies the
+// activation slice of the rows panel into LDS -- MFMA A units (lane l: row
+// l%32, elements 16(l/32) + 8s .. +7 of block blk, matching the weight
+// layout's lane split), hi and lo, converted once per GEMM input by
+// vx_pf_panel_kernel instead of by each of the column workgroups (which
+// spent more VALU on it than on the weights) -- double-buffered: pair p+1 is
+// copied into the other buffer while pair p is multiplied, one barrier per
+// pair.  Each wavefront keeps
 // PF_RING pairs of its weights in flight, unpacks a pair once and runs 3
 // MFMAs per (tile, block, K half).  64-row tiles keep the grid at several
 // workgroups per CU for the 4096-column matrices of a 512-row chunk.
@@ -49,7 +52,6 @@ template <int QT>
 __global__ __launch_bounds__(256) void vx_pf_gemm_kernel(vx_pf_args a)
 {
     constexpr int WPP = QT == 2 ? 1 : 2;
-    constexpr int UPT = PF_STAGE / 2 / 256;   // (hi, lo) unit pairs staged per thread per pair
     __shared__ uint4 lds[2 * PF_STAGE];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int T = blockIdx.x * 4 + wave;
@@ -61,42 +63,18 @@ __global__ __launch_bounds__(256) void vx_pf_gemm_kernel(vx_pf_args a)
     const uint4 *wp = a.wq + (size_t)Tc * a.n_pairs * WPP * 64 + lane;
     const uint32_t *sp = a.wd + (size_t)Tc * a.n_pairs * 32 + c;
 
-    // staging: thread t owns unit pairs u = t + 256 j; u = ((mt*2 + blk)*2 + s)*64 + ln
-    float4 xa[UPT][2];
+    // staging: the pair's PF_STAGE units of the rows panel, already in the
+    // LDS layout: a contiguous 16 KiB copy, 4 units per thread
+    constexpr int XU = PF_STAGE / 256;
+    const uint4 *xp = a.px + (size_t)blockIdx.y * a.n_pairs * PF_STAGE + threadIdx.x;
+    uint4 xa[XU];
     auto load_x = [&](int p) {
 #pragma unroll
-        for (int j = 0; j < UPT; j++) {
-            const int u = threadIdx.x + 256 * j;
-            const int ln = u & 63, s = (u >> 6) & 1, blk = (u >> 7) & 1, mt = u >> 8;
-            const int row = m0 + mt * 32 + (ln & 31);
-            const int k = 64 * p + 32 * blk + 16 * (ln >> 5) + 8 * s;
-            if (row < a.M && k < a.K) {   // K % 32 == 0: a block is wholly in range or out
-                const float *src = a.x + (size_t)row * a.ldx + k;
-                xa[j][0] = *(const float4 *)src;
-                xa[j][1] = *(const float4 *)(src + 4);
-            } else {
-                xa[j][0] = make_float4(0.f, 0.f, 0.f, 0.f);
-                xa[j][1] = xa[j][0];
-            }
-        }
+        for (int j = 0; j < XU; j++) xa[j] = xp[(size_t)p * PF_STAGE + 256 * j];
     };
     auto store_x = [&](uint4 *buf) {
 #pragma unroll
-        for (int j = 0; j < UPT; j++) {
-            const int u = threadIdx.x + 256 * j;
-            const float v[8] = {xa[j][0].x, xa[j][0].y, xa[j][0].z, xa[j][0].w,
-                                xa[j][1].x, xa[j][1].y, xa[j][1].z, xa[j][1].w};
-            vx_half8 hi, lo;
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const _Float16 t = (_Float16)v[e];
-                hi[e] = t;
-                lo[e] = (_Float16)(v[e] - (float)t);
-            }
-            const int ln = u & 63, rest = u >> 6;   // rest = (mt*2 + blk)*2 + s
-            buf[(rest * 2 + 0) * 64 + ln] = __builtin_bit_cast(uint4, hi);
-            buf[(rest * 2 + 1) * 64 + ln] = __builtin_bit_cast(uint4, lo);
-        }
+        for (int j = 0; j < XU; j++) buf[threadIdx.x + 256 * j] = xa[j];
     };
 
     vx_f32x16 D[PF_MT];
@@ -198,13 +176,65 @@ __global__ __launch_bounds__(256) void vx_pf_gemm_kernel(vx_pf_args a)
     }
 }
 
-extern "C" int vxh_gemm_rows(const vxh_qmat *W, const float *X, int ldx, int M, float *Y, int ldy, int n_out,
+// Rows panel: fp32 rows x[M][ldx] as the GEMM's LDS stages, one thread per
+// (hi, lo) unit pair u of a (row group rg, pair p): u = ((mt*2 + blk)*2 + s)*64
+// + ln covers row 64 rg + 32 mt + ln % 32, elements 64 p + 32 blk + 16 (ln/32)
+// + 8 s .. + 7; hi = fp16(x), lo = fp16(x - hi).  Rows past M and columns past
+// K are zeros.
+__global__ void vx_pf_panel_kernel(const float *__restrict__ x, int ldx, int M, int K, int n_pairs,
+                                   uint4 *__restrict__ px)
+{
+    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const int rg = blockIdx.y;
+    if (idx >= (long)n_pairs * (PF_STAGE / 2)) return;
+    const int p = (int)(idx / (PF_STAGE / 2)), u = (int)(idx % (PF_STAGE / 2));
+    const int ln = u & 63, s = (u >> 6) & 1, blk = (u >> 7) & 1, mt = u >> 8;
+    const int row = rg * PF_BM + mt * 32 + (ln & 31);
+    const int k = 64 * p + 32 * blk + 16 * (ln >> 5) + 8 * s;
+    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (row < M && k < K) {   // K % 32 == 0: a block is wholly in range or out
+        const float4 a = *(const float4 *)(x + (size_t)row * ldx + k);
+        const float4 b = *(const float4 *)(x + (size_t)row * ldx + k + 4);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    }
+    vx_half8 hi, lo;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const _Float16 t = (_Float16)v[e];
+        hi[e] = t;
+        lo[e] = (_Float16)(v[e] - (float)t);
+    }
+    uint4 *o = px + ((size_t)rg * n_pairs + p) * PF_STAGE + (u >> 6) * 128 + ln;
+    o[0] = __builtin_bit_cast(uint4, hi);
+    o[64] = __builtin_bit_cast(uint4, lo);
+}
+
+extern "C" size_t vxh_rows_panel_bytes(int M, int K)
+{
+    if (M < 1 || K < 1) return 0;
+    return (size_t)((M + PF_BM - 1) / PF_BM) * ((K + 63) / 64) * PF_STAGE * sizeof(uint4);
+}
+
+extern "C" int vxh_rows_panel(const float *X, int ldx, int M, int K, void *px, vxh_stream s)
+{
+    if (!X || !px || M < 1 || K < 32 || K % 32 || ldx < K || ldx % 4 || ((uintptr_t)X & 15) || ((uintptr_t)px & 15))
+        return vxh_fail(VXH_ERR_PARAM, "rows_panel: M %d K %d ldx %d", M, K, ldx);
+    const int n_pairs = (K + 63) / 64;
+    const long per_rg = (long)n_pairs * (PF_STAGE / 2);
+    const dim3 grid((unsigned)((per_rg + 255) / 256), (unsigned)((M + PF_BM - 1) / PF_BM));
+    vx_pf_panel_kernel<<<grid, 256, 0, vxh_hs(s)>>>(X, ldx, M, K, n_pairs, (uint4 *)px);
+    VXH_LAUNCHED();
+    return VXH_OK;
+}
+
+extern "C" int vxh_gemm_rows(const vxh_qmat *W, const void *px, int M, float *Y, int ldy, int n_out,
                              const float *R, int ldr, float scale, vxh_stream s)
 {
-    if (!W || !X || !Y || M < 1 || n_out < 1 || n_out > W->n_rows || ldx < W->n_cols || ldy < n_out ||
-        (R && ldr < n_out) || ((uintptr_t)X & 15) || ldx % 4)
-        return vxh_fail(VXH_ERR_PARAM, "gemm_rows: M %d n_out %d (rows %d, K %d, ldx %d, ldy %d)", M, n_out,
-                        W->n_rows, W->n_cols, ldx, ldy);
+    if (!W || !px || !Y || M < 1 || n_out < 1 || n_out > W->n_rows || ldy < n_out || (R && ldr < n_out) ||
+        ((uintptr_t)px & 15))
+        return vxh_fail(VXH_ERR_PARAM, "gemm_rows: M %d n_out %d (rows %d, K %d, ldy %d)", M, n_out, W->n_rows,
+                        W->n_cols, ldy);
     if (W->type != 2 && W->type != 8) return vxh_fail(VXH_ERR_UNSUPPORTED, "gemm_rows: type %d", W->type);
     vx_pf_args a;
     a.wq = (const uint4 *)W->qs;
@@ -212,8 +242,7 @@ extern "C" int vxh_gemm_rows(const vxh_qmat *W, const float *X, int ldx, int M, 
     a.n_tiles = W->n_rows / 32;
     a.n_pairs = W->n_pairs;
     a.K = W->n_cols;
-    a.x = X;
-    a.ldx = ldx;
+    a.px = (const uint4 *)px;
     a.M = M;
     a.y = Y;
     a.ldy = ldy;

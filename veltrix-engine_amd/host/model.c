@@ -181,7 +181,7 @@ static void dev_free(vx_dev *d)
     vxh_free(d->ss); vxh_free(d->hrows); vxh_free(d->cnt); vxh_free(d->cnt_row);
     vxh_free(d->x2); vxh_free(d->acc_y);
     vxh_free(d->pf_tok); vxh_free(d->pf_x); vxh_free(d->pf_xn); vxh_free(d->pf_qkv);
-    vxh_free(d->pf_q); vxh_free(d->pf_att); vxh_free(d->pf_gu); vxh_free(d->pf_h);
+    vxh_free(d->pf_q); vxh_free(d->pf_att); vxh_free(d->pf_gu); vxh_free(d->pf_h); vxh_free(d->pf_px);
     vxh_workspace_free(&d->pf_ws);
     vxh_panel_free(&d->pan_d);
     vxh_panel_free(&d->pan_f);
@@ -691,8 +691,9 @@ vx_error vx_model_set_options(vx_model *m, const vx_model_options *opt)
         TRY(vxh_stream_sync(d->stream));
         vxh_workspace_free(&d->pf_ws);
         vxh_free(d->pf_tok); vxh_free(d->pf_x); vxh_free(d->pf_xn); vxh_free(d->pf_qkv);
-        vxh_free(d->pf_q); vxh_free(d->pf_att); vxh_free(d->pf_gu); vxh_free(d->pf_h);
+        vxh_free(d->pf_q); vxh_free(d->pf_att); vxh_free(d->pf_gu); vxh_free(d->pf_h); vxh_free(d->pf_px);
         d->pf_tok = NULL; d->pf_x = d->pf_xn = d->pf_qkv = d->pf_q = d->pf_att = d->pf_gu = d->pf_h = NULL;
+        d->pf_px = NULL;
         d->pf_ready = 0;
     }
     if (cap_changed && m->k_cache) return dev_alloc_workspace(d, d->n_ctx_alloc, d->opt.attn_cap);
@@ -1234,6 +1235,7 @@ static vx_error pf_alloc(vx_dev *d)
     TRY(vxh_malloc((void **)&d->pf_att, sizeof(float) * R * d->d));
     TRY(vxh_malloc((void **)&d->pf_gu, sizeof(float) * R * d->ld_gu));
     TRY(vxh_malloc((void **)&d->pf_h, sizeof(float) * R * d->F));
+    TRY(vxh_malloc((void **)&d->pf_px, vxh_rows_panel_bytes(VX_PF_ROWS, d->F > d->d ? d->F : d->d)));
     size_t an = vxh_attention_workspace_floats(VX_PF_ROWS, d->n_ctx_alloc, d->opt.attn_cap, d->n_heads, d->n_kv,
                                                d->hd);
     TRY(vxh_workspace_alloc(&d->pf_ws, 32, an));
@@ -1259,21 +1261,25 @@ static vx_error forward_prefill(vx_model *m, const int *tokens, int M, int n_pas
         vx_dev_layer *Ld = &d->layers[l];
         float *kc = m->k_cache + (size_t)l * n_ctx * kvd, *vc = m->v_cache + (size_t)l * n_ctx * kvd;
         TRY(vxh_rmsnorm(d->pf_x, dd, M, dd, Ld->attn_norm, d->pf_xn, dd, s));
-        TRY(vxh_gemm_rows(&Ld->wqkv, d->pf_xn, dd, M, d->pf_qkv, d->ld_qkv, dd + 2 * kvd, NULL, 0,
+        TRY(vxh_rows_panel(d->pf_xn, dd, M, dd, d->pf_px, s));
+        TRY(vxh_gemm_rows(&Ld->wqkv, d->pf_px, M, d->pf_qkv, d->ld_qkv, dd + 2 * kvd, NULL, 0,
                           scale_for(d, Ld->wqkv.type), s));
         TRY(vxh_rope_kv_rows(d->pf_qkv, d->ld_qkv, M, n_past, n_ctx, d->n_heads, d->n_kv, d->hd, Ld->bq, Ld->bk,
                              Ld->bv, d->rope_cos, d->rope_sin, d->n_pos, d->pf_q, dd, kc, vc, s));
         TRY(vxh_attention(d->pf_q, M, n_past, n_ctx, d->n_heads, d->n_kv, d->hd, d->opt.attn_cap, kc, vc,
                           d->pf_att, dd, &d->pf_ws, s));
-        if (Ld->has_o)
-            TRY(vxh_gemm_rows(&Ld->wo, d->pf_att, dd, M, d->pf_x, dd, dd, d->pf_x, dd, scale_for(d, Ld->wo.type), s));
-        else
+        if (Ld->has_o) {
+            TRY(vxh_rows_panel(d->pf_att, dd, M, dd, d->pf_px, s));
+            TRY(vxh_gemm_rows(&Ld->wo, d->pf_px, M, d->pf_x, dd, dd, d->pf_x, dd, scale_for(d, Ld->wo.type), s));
+        } else
             TRY(vxh_add_rows(d->pf_x, dd, d->pf_att, dd, M, dd, s));
         TRY(vxh_rmsnorm(d->pf_x, dd, M, dd, Ld->ffn_norm, d->pf_xn, dd, s));
-        TRY(vxh_gemm_rows(&Ld->wgu, d->pf_xn, dd, M, d->pf_gu, d->ld_gu, d->ld_gu, NULL, 0,
+        TRY(vxh_rows_panel(d->pf_xn, dd, M, dd, d->pf_px, s));
+        TRY(vxh_gemm_rows(&Ld->wgu, d->pf_px, M, d->pf_gu, d->ld_gu, d->ld_gu, NULL, 0,
                           scale_for(d, Ld->wgu.type), s));
         TRY(vxh_swiglu_rows(d->pf_gu, d->ld_gu, M, d->F, d->opt.ffn_gate_threshold, d->pf_h, d->F, s));
-        TRY(vxh_gemm_rows(&Ld->wd, d->pf_h, d->F, M, d->pf_x, dd, dd, d->pf_x, dd, scale_for(d, Ld->wd.type), s));
+        TRY(vxh_rows_panel(d->pf_h, d->F, M, d->F, d->pf_px, s));
+        TRY(vxh_gemm_rows(&Ld->wd, d->pf_px, M, d->pf_x, dd, dd, d->pf_x, dd, scale_for(d, Ld->wd.type), s));
     }
     if (!last_logits) return VX_OK;
     /* the last row's logits through the decode GEMM (src/model.c:598-615) */

@@ -110,6 +110,7 @@ typedef struct vx_dev {
     int pf_ready;
     int *pf_tok;
     float *pf_x, *pf_xn, *pf_qkv, *pf_q, *pf_att, *pf_gu, *pf_h;
+    void *pf_px;                       /* rows panel of the GEMM input (vxh_rows_panel) */
     vxh_workspace pf_ws;
     /* GEMM profiling (vx_model_set_profiling) */
     int prof_on;                       /* 0: off; n: every n-th launch per class   */
