@@ -838,7 +838,8 @@ __global__ __launch_bounds__(CMB_THREADS) void vx_attention_combine_kernel(
         if (threadIdx.x == 0) {
             // one counter per 256-byte line
             unsigned *c = cnt + (size_t)m * 64;
-            const unsigned old = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            // acquire-release: publishes this head's rows, sees the other heads'
+            const unsigned old = __hip_atomic_fetch_add(c, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
             s_last = old + 1 == (unsigned)n_heads;
             if (s_last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }

@@ -694,9 +694,12 @@ __global__ __launch_bounds__(256) void vx_gemm_kernel(vx_gemm_args a)
         // atomics to complete (they are performed at device scope), one
         // thread counts the workgroup into its tile group (n_splits
         // arrivals); the last of those counts the tile group into the
-        // super-group.  The workgroup completing the super-group sees every
-        // partial sum of it.  Counters sit VX_CNT_STRIDE words apart (one
-        // per 256-byte line) and are reset by their last arriver.
+        // super-group.  Both counts are acquire-release at agent scope, so
+        // each arrival releases its workgroup's sums and the last one, with
+        // the acquire fence below, sees every partial sum of the super-group
+        // under the memory model (not only through write-through caches).
+        // Counters sit VX_CNT_STRIDE words apart (one per 256-byte line) and
+        // are reset by their last arriver.
         __shared__ int s_last;
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
@@ -704,13 +707,13 @@ __global__ __launch_bounds__(256) void vx_gemm_kernel(vx_gemm_args a)
         if (threadIdx.x == 0) {
             const int n_groups = (a.n_tiles + 3) / 4;
             unsigned *c1 = a.e.cnt + (size_t)(a.e.n_sg + grp) * VX_CNT_STRIDE;
-            int last = __hip_atomic_fetch_add(c1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 ==
+            int last = __hip_atomic_fetch_add(c1, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) + 1 ==
                        (unsigned)a.n_splits;
             if (last) {
                 __hip_atomic_store(c1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 unsigned *c2 = a.e.cnt + (size_t)sg * VX_CNT_STRIDE;
                 const int groups = min(a.e.sg_groups, n_groups - sg * a.e.sg_groups);
-                last = __hip_atomic_fetch_add(c2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 ==
+                last = __hip_atomic_fetch_add(c2, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) + 1 ==
                        (unsigned)groups;
                 if (last) __hip_atomic_store(c2, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
