@@ -14,6 +14,7 @@ ORACLE_SO = os.path.join(REPO, "oracle", "liboracle.so")
 REF_SO = {
     "scalar": os.path.join(REPO, "oracle", "_ref", "libvxref_scalar.so"),
     "avx2": os.path.join(REPO, "oracle", "_ref", "libvxref_avx2.so"),
+    "avx2gemv": os.path.join(REPO, "oracle", "_ref", "libvxref_avx2gemv.so"),
 }
 PRODUCT_SO = os.path.join(REPO, "veltrix-engine_amd", "lib", "libveltrix_amd.so")
 

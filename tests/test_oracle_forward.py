@@ -8,6 +8,7 @@ attn_o_inplace=1.  With attn_o_inplace=0 (the engine's out-of-place semantics)
 the oracle is compared against the reference on models without an
 attn_output tensor, where the reference skips that product.
 """
+import contextlib
 import ctypes as C
 import os
 
@@ -19,11 +20,30 @@ from _gguf import llama_gguf, GGML_F32, GGML_Q8_0, GGML_Q4_0
 from _oracle_model import OracleModel
 
 O = N.oracle()
+_libc = C.CDLL("libc.so.6")
+_M_PERTURB = -6      # glibc mallopt parameter
+
+
+@contextlib.contextmanager
+def zero_filled_malloc():
+    """glibc's M_PERTURB with byte 0xff fills every fresh malloc chunk with
+    0x00 (perturb ^ 0xff).  The reference's x86 Q4_0 GEMV reads four floats
+    past x (src/simd/avx2.c:351-352); for the down projection those are the
+    8-float pad between ffn_h and ffn_h2 of a malloc'd scratch
+    (src/model.c:413-433) that nothing writes, so its value is heap garbage
+    unless malloc hands out zeroed memory -- which is the oracle's reading."""
+    _libc.mallopt(_M_PERTURB, 0xff)
+    try:
+        yield
+    finally:
+        _libc.mallopt(_M_PERTURB, 0)
+
+
 pytestmark = pytest.mark.skipif(not N.ref_available("scalar"), reason="reference build absent")
 
 
-def ref_forward_logits(path, tokens, n_vocab, n_ctx=None, chunks=None):
-    R = N.ref("scalar")
+def ref_forward_logits(path, tokens, n_vocab, n_ctx=None, chunks=None, kind="scalar"):
+    R = N.ref(kind)
     R.vx_set_n_threads(1)
     mp = C.POINTER(N.VxModel)()
     err = R.vx_model_create(path.encode(), C.byref(mp))
@@ -114,3 +134,51 @@ def test_oracle_forward_context_clamp_and_cap(tmp_path):
         O.or_forward(om.ptr, np.array([t], np.int32), 1, got[i])
     assert om.cache_len == ref_len
     assert N.close(got, ref_logits, atol=1e-5, rtol=1e-5)
+
+
+AVX2_CASES = [
+    # layers, d, heads, kv, ff, vocab, attn_output, emb, out
+    (2, 64, 4, 2, 128, 96, True, GGML_Q4_0, GGML_Q4_0),
+    (2, 128, 4, 1, 256, 160, False, GGML_Q4_0, GGML_Q4_0),
+    (1, 96, 3, 3, 192, 64, True, GGML_Q8_0, GGML_Q8_0),
+]
+
+
+@pytest.mark.skipif(not N.ref_available("avx2gemv"), reason="reference AVX2-GEMV build absent")
+@pytest.mark.parametrize("case", AVX2_CASES)
+def test_oracle_avx2_lane_forward_matches_reference_avx2_gemv_build(tmp_path, case):
+    """The AVX2-lane composition (q4_mode 1: every GEMV in the lane pattern of
+    src/simd/avx2.c:311-370, the 4-float x tails of src/model.c:425-435, the
+    down projection's zero pad) against the reference's own forward with its
+    x86 GEMV dispatch (src/model.c:174-244) and AVX2 attention dot products
+    (:312-325) compiled in, and tensor.c's portable RoPE/softmax/RMSNorm/SiLU
+    (libvxref_avx2gemv.so; the x86 RoPE reads uninitialised angles, so the
+    full x86 build cannot pin this).  The reference's down-projection tail is
+    unwritten heap memory; it runs under zero_filled_malloc so that tail is
+    the zero pad the oracle reads.  One thread, so the reference's in-place
+    attn_o is the oracle's row-by-row recurrence (attn_o_inplace = 1).  The
+    lane pattern moves logits by O(1) against exact mode, so the 1e-5 bar
+    below catches any wrong GEMV, tail or wiring; what remains is the
+    attention's 8-wide dot-product order."""
+    L, d, h, kv, ff, V, with_o, et, ot = case
+    rng = np.random.default_rng(sum(case[:6]) + 11)
+    path = str(tmp_path / "m.gguf")
+    raw = llama_gguf(path, rng, L, d, h, kv, ff, V, std=0.05, with_attn_output=with_o,
+                     norm_random=True, emb_type=et, out_type=ot)
+    tokens = rng.integers(0, V, 12).astype(np.int32)
+    with zero_filled_malloc():
+        ref_logits, conf, ref_len = ref_forward_logits(path, tokens, V, kind="avx2gemv")
+    assert conf[:7] == (L, h, kv, d, d // h, ff, V)
+    om = OracleModel(raw, L, d, h, kv, ff, V, n_ctx=4096, q4_mode=1, attn_o_inplace=1)
+    got = np.zeros((len(tokens), V), np.float32)
+    for i, t in enumerate(tokens):
+        assert O.or_forward(om.ptr, np.array([t], np.int32), 1, got[i]) == 0
+    assert om.cache_len == ref_len == len(tokens)
+    assert N.close(got, ref_logits, atol=1e-5, rtol=1e-5), N.max_violation(got, ref_logits, 1e-5, 1e-5)
+    # the lane pattern is visible: exact mode differs by far more than the bar
+    ex = OracleModel(raw, L, d, h, kv, ff, V, n_ctx=4096, q4_mode=0, attn_o_inplace=1)
+    exact = np.zeros((len(tokens), V), np.float32)
+    for i, t in enumerate(tokens):
+        assert O.or_forward(ex.ptr, np.array([t], np.int32), 1, exact[i]) == 0
+    assert np.abs(exact - ref_logits).max() > 1e-3
+
