@@ -512,11 +512,33 @@ __device__ __forceinline__ void vx_attention_mfma_body(
         constexpr int Q4 = HD / 4, QS = Q4 + 1;                      // float4 per row, padded stride
         __shared__ float4 s_q[16 * QS];
         constexpr int QI = 16 * Q4 / ATT_THREADS;                  // q items per thread (1 or 2)
+        const int lo = n_past < n_ctx ? n_past : n_ctx - 1;
+        const int hi = min(n_past + M - 1, n_ctx - 1);
+        const int c0 = (blockIdx.x % ncg) * 4 * ACH;
+        const bool has_new = hi >= c0 && lo < c0 + 4 * ACH;          // uniform over the workgroup
+        const int n_new = M * 2 * Q4;                                // new k/v items (row, k|v, float4)
+        // new k/v item `it` of this forward: its q|k|v column, cache element,
+        // RoPE pair and position
+        auto new_item = [&](int it, int &row, int &col, int &el, int &pr, int &rp, const float *&bias, bool &rot) {
+            const int d4 = it % Q4, kind = (it / Q4) % 2, mr = it / (2 * Q4);
+            row = mr;
+            el = g * HD + 4 * d4;
+            col = (kind ? qd + kvd : qd) + el;
+            pr = 2 * d4;
+            rp = n_past + mr;
+            bias = kind ? qa.bv : qa.bk;
+            rot = kind == 0;
+        };
+        // the q items and the first new item of each thread load in one batch
+        // (a workgroup holding new rows pays one round trip for both, not one
+        // after the other); a thread without a first new item loads item 0,
+        // whose addresses are those of a q item of row 0
         {
-            int row[QI], col[QI], pr[QI], rp[QI];
+            constexpr int B = QI + 1;
+            int row[B], col[B], el[B], pr[B], rp[B];
             bool ok[QI];
-            const float *bias[QI];
-            bool rot[QI];
+            const float *bias[B];
+            bool rot[B];
 #pragma unroll
             for (int u = 0; u < QI; u++) {
                 const int it = threadIdx.x + u * ATT_THREADS, qn = it / Q4, d4 = it % Q4;
@@ -525,48 +547,47 @@ __device__ __forceinline__ void vx_attention_mfma_body(
                 const int mj = ok[u] ? qj % M : 0, hj = ok[u] ? qj / M : 0;
                 row[u] = mj;
                 col[u] = (g * G + hj) * HD + 4 * d4;
+                el[u] = col[u];
                 pr[u] = 2 * d4;
                 rp[u] = n_past + mj;
                 bias[u] = qa.bq;
                 rot[u] = true;
             }
-            float4 o[QI];
-            vx_qkv4_items<QI>(qa, row, col, col, pr, rp, bias, rot, half, o);
+            const bool first_new = has_new && (int)threadIdx.x < n_new;
+            new_item(first_new ? (int)threadIdx.x : 0, row[QI], col[QI], el[QI], pr[QI], rp[QI], bias[QI], rot[QI]);
+            float4 o[B];
+            vx_qkv4_items<B>(qa, row, col, el, pr, rp, bias, rot, half, o);
 #pragma unroll
             for (int u = 0; u < QI; u++) {
                 const int it = threadIdx.x + u * ATT_THREADS;
                 s_q[(it / Q4) * QS + it % Q4] =
                     vx_keep4(ok[u], make_float4(o[u].x * scale, o[u].y * scale, o[u].z * scale, o[u].w * scale));
             }
+            if (first_new) {
+                const int it = threadIdx.x;
+                // the new row as the cache holds it (fp16 mode: rounded)
+                s_new[it] = vx_kv_round4<KH>(o[QI]);
+                if (qg == 0) {
+                    const int kind = (it / Q4) % 2, pos = min(n_past + row[QI], n_ctx - 1);
+                    vx_kv_store4<KH>(kind ? vc : kc, (size_t)pos * kvd + el[QI], o[QI]);
+                }
+            }
         }
-        const int lo = n_past < n_ctx ? n_past : n_ctx - 1;
-        const int hi = min(n_past + M - 1, n_ctx - 1);
-        const int c0 = (blockIdx.x % ncg) * 4 * ACH;
-        const bool has_new = hi >= c0 && lo < c0 + 4 * ACH;          // uniform over the workgroup
         if (has_new) {
-            for (int it0 = threadIdx.x; it0 < M * 2 * Q4; it0 += 2 * ATT_THREADS) {
+            for (int it0 = ATT_THREADS + threadIdx.x; it0 < n_new; it0 += 2 * ATT_THREADS) {
                 int row[2], col[2], el[2], pr[2], rp[2];
                 const float *bias[2];
                 bool rot[2];
 #pragma unroll
-                for (int u = 0; u < 2; u++) {
-                    const int it = min(it0 + u * ATT_THREADS, M * 2 * Q4 - 1);
-                    const int d4 = it % Q4, kind = (it / Q4) % 2, mr = it / (2 * Q4);
-                    row[u] = mr;
-                    el[u] = g * HD + 4 * d4;
-                    col[u] = (kind ? qd + kvd : qd) + el[u];
-                    pr[u] = 2 * d4;
-                    rp[u] = n_past + mr;
-                    bias[u] = kind ? qa.bv : qa.bk;
-                    rot[u] = kind == 0;
-                }
+                for (int u = 0; u < 2; u++)
+                    new_item(min(it0 + u * ATT_THREADS, n_new - 1), row[u], col[u], el[u], pr[u], rp[u], bias[u],
+                             rot[u]);
                 float4 o[2];
                 vx_qkv4_items<2>(qa, row, col, el, pr, rp, bias, rot, half, o);
 #pragma unroll
                 for (int u = 0; u < 2; u++) {
                     const int it = it0 + u * ATT_THREADS;
-                    if (it >= M * 2 * Q4) continue;
-                    // the new rows as the cache holds them (fp16 mode: rounded)
+                    if (it >= n_new) continue;
                     s_new[it] = vx_kv_round4<KH>(o[u]);
                     if (qg == 0) {
                         const int kind = (it / Q4) % 2, pos = min(n_past + row[u], n_ctx - 1);
