@@ -51,7 +51,11 @@ def test_gemm_q4_0_exact(P, rows, cols, M):
     assert close(Y, exact, atol=2e-5, rtol=2e-5), max_violation(Y, exact, 2e-5, 2e-5)
 
 
-@pytest.mark.parametrize("rows,cols,M", SHAPES[:7])
+# every exact shape, plus a draft-size matrix at one row (the decode GEMV)
+AVX2_SHAPES = SHAPES + [(2048, 5632, 1)]
+
+
+@pytest.mark.parametrize("rows,cols,M", AVX2_SHAPES)
 def test_gemm_q4_0_avx2_lanes(P, rows, cols, M):
     print(f"gemm_q4_0 avx2 rows={rows} cols={cols} M={M}", flush=True)
     rng = np.random.default_rng(rows * 5 + cols + M)

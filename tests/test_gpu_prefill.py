@@ -53,6 +53,7 @@ CASES = [
     (2, 256, 4, 2, 512, 512, GGML_Q4_0, 512),
     (2, 256, 8, 2, 640, 300, GGML_Q4_0, 600),
     (1, 192, 3, 3, 384, 256, GGML_Q8_0, 300),
+    (1, 256, 2, 1, 256, 64, GGML_Q4_0, 300),      # head_dim 128: two chunks per attention wavefront
 ]
 
 

@@ -527,6 +527,7 @@ def test_pro_attn_combines_partials(P, H, KV, hd, M, typ):
     (4, 4, 128, 1, 260, 200, 4096),       # past the context: clamped row
     (8, 8, 128, 16, 100, 512, 4096),      # 16 query vectors per kv head
     (16, 2, 32, 3, 90, 256, 4096),        # head_dim 32: 32-position chunks
+    (8, 2, 128, 64, 300, 512, 200),       # prompt-prefill batch: 64 rows, cap inside a two-chunk wavefront
 ])
 def test_attention_matches_reference(P, H, KV, hd, M, n_past, n_ctx, cap):
     """vxh_attention against softmax attention in float64 on the same cache

@@ -406,7 +406,7 @@ __device__ __forceinline__ void vx_kv_store4(float *base, size_t i, float4 v)
         *(float4 *)(base + i) = v;
 }
 
-template <bool QKV, int HD, bool KH = false>
+template <bool QKV, int HD, bool KH = false, int NCW = 1>
 __device__ __forceinline__ void vx_attention_mfma_body(
     const float *__restrict__ q, int M, int n_past, int n_ctx, int n_heads, int n_kv, int cap,
     float *__restrict__ kc, float *__restrict__ vc, int n_chunks, int n_chunks_w, int n_qg,
@@ -415,48 +415,54 @@ __device__ __forceinline__ void vx_attention_mfma_body(
     constexpr int NJ = HD / 16;      // K float4 per lane per 16 positions; also P.V chains
     constexpr int NV = HD / 16;      // V floats per lane per step
     constexpr int NV4 = NV / 4;
+    constexpr int WCH = NCW * ACH;   // positions of one wavefront (NCW chunks of ACH, walked in order)
+    // V of the first chunk with its K (the wavefront holds both): at head_dim
+    // 64, where the draft decode has too few wavefronts to hide a second round
+    // trip, and whenever a wavefront walks several chunks (its V then streams
+    // while the scores of the chunk run).  A one-chunk wavefront at head_dim
+    // 128 loads V after issuing the score MFMAs, so K and V need not be live
+    // together and 3 wavefronts fit a SIMD.
+    constexpr bool V_EARLY = HD == 64 || NCW > 1;
     static_assert(HD == 64 || HD == 128, "head_dim 64 or 128");
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int n = lane & 15, r = lane >> 4;
-    const int ncg = (n_chunks_w + 3) / 4;
+    const int nw_w = (n_chunks_w + NCW - 1) / NCW;   // wavefront chunks holding positions to store
+    const int nw = (n_chunks + NCW - 1) / NCW;       // wavefront chunks attended (partials per query)
+    const int ncg = (nw_w + 3) / 4;
     const int g = blockIdx.x / (n_qg * ncg);
     const int qg = (blockIdx.x / ncg) % n_qg;
     const int ch = (blockIdx.x % ncg) * 4 + wave;
-    if (!QKV && ch >= n_chunks_w) return;   // QKV: after the workgroup barrier below
-    const bool attend = ch < n_chunks;
+    if (!QKV && ch >= nw_w) return;   // QKV: after the workgroup barrier below
+    const bool attend = ch < nw;
     const int G = n_heads / n_kv, QM = G * M;
     const int kvd = n_kv * HD, qd = n_heads * HD, half = HD / 2;
-    const int t0 = ch * ACH;
+    const int t0 = ch * WCH;
 
-    // K rows of positions t0 + 16 pg + n (dims 16 j + 4 r .. + 3) and V rows
-    // of positions t0 + 16 pg + 4 r + s (dims 64 u + 4 n .. + 3) from the cache;
-    // positions past the cache end read as zeros
+    // K rows of positions tc + 16 pg + n (dims 16 j + 4 r .. + 3) and V rows
+    // of positions tc + 16 pg + 4 r + s (dims 64 u + 4 n .. + 3) of chunk tc
+    // from the cache; positions past the cache end read as zeros
     float4 kr[2][NJ], vr[2][4][NV4];
-    // K first; at head_dim 128 V after the score MFMAs are issued (its
-    // latency overlaps the scores and the softmax, and K and V need not be
-    // live together, so 3 wavefronts fit a SIMD); at 64 (draft decode: too
-    // few wavefronts to hide a second round trip) V with K
-    auto load_k = [&]() {
+    auto load_k = [&](int tc) {
 #pragma unroll
         for (int pg = 0; pg < 2; pg++) {
-            const int pos = t0 + 16 * pg + n;
+            const int pos = tc + 16 * pg + n;
             const size_t off = (size_t)min(pos, n_ctx - 1) * kvd + g * HD + 4 * r;
 #pragma unroll
             for (int j = 0; j < NJ; j++) kr[pg][j] = vx_kv_load4<KH>(kc, off + 16 * j);
         }
 #pragma unroll
         for (int pg = 0; pg < 2; pg++) {
-            const bool ok = t0 + 16 * pg + n < n_ctx;
+            const bool ok = tc + 16 * pg + n < n_ctx;
 #pragma unroll
             for (int j = 0; j < NJ; j++) kr[pg][j] = vx_keep4(ok, kr[pg][j]);
         }
     };
-    auto load_v = [&]() {
+    auto load_v = [&](int tc) {
 #pragma unroll
         for (int pg = 0; pg < 2; pg++)
 #pragma unroll
             for (int st = 0; st < 4; st++) {
-                const int pv = t0 + 16 * pg + 4 * r + st;
+                const int pv = tc + 16 * pg + 4 * r + st;
                 const size_t ov = (size_t)min(pv, n_ctx - 1) * kvd + g * HD + 4 * n;
 #pragma unroll
                 for (int u = 0; u < NV4; u++) vr[pg][st][u] = vx_kv_load4<KH>(vc, ov + 64 * u);
@@ -465,13 +471,13 @@ __device__ __forceinline__ void vx_attention_mfma_body(
         for (int pg = 0; pg < 2; pg++)
 #pragma unroll
             for (int st = 0; st < 4; st++) {
-                const bool okv = t0 + 16 * pg + 4 * r + st < n_ctx;
+                const bool okv = tc + 16 * pg + 4 * r + st < n_ctx;
 #pragma unroll
                 for (int u = 0; u < NV4; u++) vr[pg][st][u] = vx_keep4(okv, vr[pg][st][u]);
             }
     };
-    load_k();
-    if constexpr (HD == 64) load_v();
+    load_k(t0);
+    if constexpr (V_EARLY) load_v(t0);
 
     // query n of this group: q vector (hl, m), its causal length cs
     const int qi = qg * 16 + n;
@@ -514,8 +520,8 @@ __device__ __forceinline__ void vx_attention_mfma_body(
         constexpr int QI = 16 * Q4 / ATT_THREADS;                  // q items per thread (1 or 2)
         const int lo = n_past < n_ctx ? n_past : n_ctx - 1;
         const int hi = min(n_past + M - 1, n_ctx - 1);
-        const int c0 = (blockIdx.x % ncg) * 4 * ACH;
-        const bool has_new = hi >= c0 && lo < c0 + 4 * ACH;          // uniform over the workgroup
+        const int c0 = (blockIdx.x % ncg) * 4 * WCH;
+        const bool has_new = hi >= c0 && lo < c0 + 4 * WCH;          // uniform over the workgroup
         const int n_new = M * 2 * Q4;                                // new k/v items (row, k|v, float4)
         // new k/v item `it` of this forward: its q|k|v column, cache element,
         // RoPE pair and position
@@ -599,87 +605,108 @@ __device__ __forceinline__ void vx_attention_mfma_body(
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < NJ; j++) qv[j] = s_q[n * QS + 4 * j + r];
-        if (has_new) {
-#pragma unroll
-            for (int pg = 0; pg < 2; pg++) {
-                const int mn = new_row(t0 + 16 * pg + n);
-                if (mn >= 0)
-#pragma unroll
-                    for (int j = 0; j < NJ; j++) kr[pg][j] = s_new[(mn * 2) * Q4 + 4 * j + r];
-            }
-        }
         has_new_wg = has_new;
     }
-    if (ch >= n_chunks_w) return;
+    if (ch >= nw_w) return;
     if (!attend) return;
 
-    // scores of the chunk's 32 positions: S[pg] item i = position 16 pg + 4 r + i
-    vx_f32x4 S[2];
-#pragma unroll
-    for (int pg = 0; pg < 2; pg++) {
-        S[pg] = vx_f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int j = 0; j < NJ; j++) {
-            S[pg] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[pg][j].x, qv[j].x, S[pg], 0, 0, 0);
-            S[pg] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[pg][j].y, qv[j].y, S[pg], 0, 0, 0);
-            S[pg] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[pg][j].z, qv[j].z, S[pg], 0, 0, 0);
-            S[pg] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[pg][j].w, qv[j].w, S[pg], 0, 0, 0);
-        }
-    }
-    if constexpr (HD != 64) load_v();
-    if (QKV && has_new_wg) {
-#pragma unroll
-        for (int pg = 0; pg < 2; pg++)
-#pragma unroll
-            for (int st = 0; st < 4; st++) {
-                const int mv = new_row(t0 + 16 * pg + 4 * r + st);
-                if (mv >= 0)
-#pragma unroll
-                    for (int u = 0; u < NV4; u++) vr[pg][st][u] = s_new[(mv * 2 + 1) * (HD / 4) + n + 16 * u];
-            }
-    }
-    // chunk softmax statistics of query n (src/tensor.c:156-171 per chunk)
-    float sc[2][4];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int pg = 0; pg < 2; pg++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int t = t0 + 16 * pg + 4 * r + i;
-            sc[pg][i] = t < cs ? S[pg][i] : -INFINITY;
-            mx = fmaxf(mx, sc[pg][i]);
-        }
-    mx = vx_max_x32(vx_max_x16(mx));
-    float p[2][4], l = 0.0f;
-#pragma unroll
-    for (int pg = 0; pg < 2; pg++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            p[pg][i] = mx == -INFINITY || sc[pg][i] == -INFINITY ? 0.0f : expf(sc[pg][i] - mx);
-            l += p[pg][i];
-        }
-    l = vx_sum_x32(vx_sum_x16(l));
-
-    // P.V
+    // The wavefront's chunks in order, with the online-softmax rescale
+    // (src/tensor.c:156-171 over the chunks): running max rm and sum rl of
+    // query n, output accumulators O rescaled when the max grows.
+    float rm = -INFINITY, rl = 0.0f;
     vx_f32x4 O[NJ];
 #pragma unroll
     for (int c = 0; c < NJ; c++) O[c] = vx_f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int pg = 0; pg < 2; pg++)
+    for (int cc = 0; cc < NCW; cc++) {
+        const int tc = t0 + cc * ACH;
+        if (cc > 0) load_v(tc);        // this chunk's V streams while its scores run
+        // this forward's own k rows from LDS (the cache rows may not be written yet)
+        if (QKV && has_new_wg) {
 #pragma unroll
-        for (int st = 0; st < 4; st++)
+            for (int pg = 0; pg < 2; pg++) {
+                const int mn = new_row(tc + 16 * pg + n);
+                if (mn >= 0)
 #pragma unroll
-            for (int c = 0; c < NJ; c++) {
-                const float4 v4 = vr[pg][st][c / 4];
-                const float a = (c % 4) == 0 ? v4.x : (c % 4) == 1 ? v4.y : (c % 4) == 2 ? v4.z : v4.w;
-                O[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, p[pg][st], O[c], 0, 0, 0);
+                    for (int j = 0; j < NJ; j++) kr[pg][j] = s_new[(mn * 2) * (HD / 4) + 4 * j + r];
             }
+        }
+        // scores of the chunk's 32 positions: S[pg] item i = position 16 pg + 4 r + i
+        vx_f32x4 S[2];
+#pragma unroll
+        for (int pg = 0; pg < 2; pg++) {
+            S[pg] = vx_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                S[pg] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[pg][j].x, qv[j].x, S[pg], 0, 0, 0);
+                S[pg] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[pg][j].y, qv[j].y, S[pg], 0, 0, 0);
+                S[pg] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[pg][j].z, qv[j].z, S[pg], 0, 0, 0);
+                S[pg] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[pg][j].w, qv[j].w, S[pg], 0, 0, 0);
+            }
+        }
+        if (cc + 1 < NCW) load_k(tc + ACH);       // the next chunk's K behind this chunk's V
+        if constexpr (!V_EARLY) load_v(tc);
+        if (QKV && has_new_wg) {
+#pragma unroll
+            for (int pg = 0; pg < 2; pg++)
+#pragma unroll
+                for (int st = 0; st < 4; st++) {
+                    const int mv = new_row(tc + 16 * pg + 4 * r + st);
+                    if (mv >= 0)
+#pragma unroll
+                        for (int u = 0; u < NV4; u++) vr[pg][st][u] = s_new[(mv * 2 + 1) * (HD / 4) + n + 16 * u];
+                }
+        }
+        // chunk statistics of query n against the running ones
+        float sc[2][4];
+        float cm = -INFINITY;
+#pragma unroll
+        for (int pg = 0; pg < 2; pg++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int t = tc + 16 * pg + 4 * r + i;
+                sc[pg][i] = t < cs ? S[pg][i] : -INFINITY;
+                cm = fmaxf(cm, sc[pg][i]);
+            }
+        cm = vx_max_x32(vx_max_x16(cm));
+        const float nm = fmaxf(rm, cm);
+        float p[2][4], l = 0.0f;
+#pragma unroll
+        for (int pg = 0; pg < 2; pg++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                p[pg][i] = nm == -INFINITY || sc[pg][i] == -INFINITY ? 0.0f : expf(sc[pg][i] - nm);
+                l += p[pg][i];
+            }
+        l = vx_sum_x32(vx_sum_x16(l));
+        if (cc == 0) {
+            rl = l;
+        } else {
+            const float fo = rm == -INFINITY ? 0.0f : expf(rm - nm);
+            rl = rl * fo + l;
+#pragma unroll
+            for (int c = 0; c < NJ; c++) O[c] *= fo;
+        }
+        rm = nm;
+
+        // P.V
+#pragma unroll
+        for (int pg = 0; pg < 2; pg++)
+#pragma unroll
+            for (int st = 0; st < 4; st++)
+#pragma unroll
+                for (int c = 0; c < NJ; c++) {
+                    const float4 v4 = vr[pg][st][c / 4];
+                    const float a = (c % 4) == 0 ? v4.x : (c % 4) == 1 ? v4.y : (c % 4) == 2 ? v4.z : v4.w;
+                    O[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, p[pg][st], O[c], 0, 0, 0);
+                }
+    }
     if (!qok) return;
     const size_t ps = PART_STRIDE(HD);
-    float *pq = part + (((size_t)g * n_chunks + ch) * QM + qi) * ps;
+    float *pq = part + (((size_t)g * nw + ch) * QM + qi) * ps;
     if (r == 0) {
-        pq[0] = mx;
-        pq[1] = l;
+        pq[0] = rm;
+        pq[1] = rl;
     }
 #pragma unroll
     for (int i = 0; i < 4; i++)
@@ -689,17 +716,32 @@ __device__ __forceinline__ void vx_attention_mfma_body(
                 make_float4(O[4 * u][i], O[4 * u + 1][i], O[4 * u + 2][i], O[4 * u + 3][i]);
 }
 
-// q rows given (the verify forward, after the RoPE kernel): 3 wavefronts per
-// SIMD fit the registers, so a 7B-shape layer's 2304 wavefronts run in one
-// round.  q|k|v sums (draft decode): the default register budget.
+// Wavefront chunks: the q-rows kernel at head_dim 128 (prompt prefill: many
+// query groups per head, so half the wavefronts still fill the chip) walks
+// two 32-position chunks per wavefront, V streaming behind K, and writes half
+// the partials (rocprofv3, 2048-token prefill: 205 -> 188 us per launch).  The
+// q|k|v kernels keep one chunk per wavefront: at head_dim 128 (the verify,
+// nine rows) two chunks made the attention 24 -> 27.6 us per layer -- half as
+// many wavefronts, each with a longer K -> V chain -- and 3 wavefronts per SIMD
+// fit the registers of one.
+template <int HD, bool QKV>
+struct vx_att_ncw_of {
+    static constexpr int v = HD == 128 && !QKV ? 2 : 1;
+};
+static int vx_att_ncw(int head_dim, bool qkv)
+{
+    if (head_dim == 128) return qkv ? vx_att_ncw_of<128, true>::v : vx_att_ncw_of<128, false>::v;
+    return qkv ? vx_att_ncw_of<64, true>::v : vx_att_ncw_of<64, false>::v;
+}
+
 template <int HD>
 __global__ __launch_bounds__(ATT_THREADS) __attribute__((amdgpu_waves_per_eu(3))) void vx_attention_mfma_kernel(
     const float *__restrict__ q, int M, int n_past, int n_ctx, int n_heads, int n_kv, int cap,
     float *__restrict__ kc, float *__restrict__ vc, int n_chunks, int n_chunks_w, int n_qg,
     float *__restrict__ part, vx_qkv_args qa)
 {
-    vx_attention_mfma_body<false, HD>(q, M, n_past, n_ctx, n_heads, n_kv, cap, kc, vc, n_chunks, n_chunks_w,
-                                      n_qg, part, qa);
+    vx_attention_mfma_body<false, HD, false, vx_att_ncw_of<HD, false>::v>(
+        q, M, n_past, n_ctx, n_heads, n_kv, cap, kc, vc, n_chunks, n_chunks_w, n_qg, part, qa);
 }
 
 template <int HD, bool KH = false>
@@ -708,8 +750,8 @@ __global__ __launch_bounds__(ATT_THREADS) __attribute__((amdgpu_waves_per_eu(3))
     float *__restrict__ kc, float *__restrict__ vc, int n_chunks, int n_chunks_w, int n_qg,
     float *__restrict__ part, vx_qkv_args qa)
 {
-    vx_attention_mfma_body<true, HD, KH>(q, M, n_past, n_ctx, n_heads, n_kv, cap, kc, vc, n_chunks, n_chunks_w,
-                                     n_qg, part, qa);
+    vx_attention_mfma_body<true, HD, KH, vx_att_ncw_of<HD, true>::v>(
+        q, M, n_past, n_ctx, n_heads, n_kv, cap, kc, vc, n_chunks, n_chunks_w, n_qg, part, qa);
 }
 
 // One workgroup per (row m, head): merge the chunks' partial results with
@@ -927,9 +969,12 @@ static int vx_attention_run(const float *q, const vx_qkv_args *qa, long n_clr, i
     size_t lds = vx_attn_lds(qpg, head_dim);
     vx_qkv_args none;
     memset(&none, 0, sizeof(none));
-    if ((head_dim == 64 || head_dim == 128) && (!qa || M <= VX_ATT_MFMA_MAX_M)) {
-        // fp32-MFMA kernel: 4 chunks per workgroup, one per wavefront
-        const int nqg = (QM + 15) / 16, ncg = (n_chunks_w + 3) / 4;
+    const bool mfma = (head_dim == 64 || head_dim == 128) && (!qa || M <= VX_ATT_MFMA_MAX_M);
+    if (mfma) {
+        // fp32-MFMA kernel: 4 wavefronts per workgroup, NCW chunks per wavefront
+        const int ncw = vx_att_ncw(head_dim, qa != nullptr);
+        const int nw_w = (n_chunks_w + ncw - 1) / ncw;
+        const int nqg = (QM + 15) / 16, ncg = (nw_w + 3) / 4;
         const int grid = n_kv_heads * nqg * ncg;
         const vx_qkv_args &A = qa ? *qa : none;
         if (kv_half && head_dim == 64)
@@ -965,6 +1010,11 @@ static int vx_attention_run(const float *q, const vx_qkv_args *qa, long n_clr, i
             q, M, n_past, n_ctx, n_heads, n_kv_heads, head_dim, cap, kc, vc, n_chunks, n_chunks, qpg,
             n_qg, ws->part, none);
     VXH_LAUNCHED();
+    // partials per query: one per wavefront chunk of the MFMA kernels
+    if (mfma) {
+        const int ncw = vx_att_ncw(head_dim, qa != nullptr);
+        n_chunks = (n_chunks + ncw - 1) / ncw;
+    }
     if (n_chunks_out) *n_chunks_out = n_chunks;
     if (parts_only) return VXH_OK;
     double *clr = qa ? (double *)qa->qkv : nullptr;
