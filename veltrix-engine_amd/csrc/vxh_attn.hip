@@ -406,7 +406,7 @@ __device__ __forceinline__ void vx_kv_store4(float *base, size_t i, float4 v)
         *(float4 *)(base + i) = v;
 }
 
-template <bool QKV, int HD, bool KH = false, int NCW = 1>
+template <bool QKV, int HD, bool KH = false, int NCW = 1, int NPG = 2, bool MERGE = false>
 __device__ __forceinline__ void vx_attention_mfma_body(
     const float *__restrict__ q, int M, int n_past, int n_ctx, int n_heads, int n_kv, int cap,
     float *__restrict__ kc, float *__restrict__ vc, int n_chunks, int n_chunks_w, int n_qg,
@@ -415,7 +415,8 @@ __device__ __forceinline__ void vx_attention_mfma_body(
     constexpr int NJ = HD / 16;      // K float4 per lane per 16 positions; also P.V chains
     constexpr int NV = HD / 16;      // V floats per lane per step
     constexpr int NV4 = NV / 4;
-    constexpr int WCH = NCW * ACH;   // positions of one wavefront (NCW chunks of ACH, walked in order)
+    constexpr int CH = NPG * 16;     // positions of one chunk (NPG groups of 16)
+    constexpr int WCH = NCW * CH;    // positions of one wavefront (NCW chunks, walked in order)
     // V of the first chunk with its K (the wavefront holds both): at head_dim
     // 64, where the draft decode has too few wavefronts to hide a second round
     // trip, and whenever a wavefront walks several chunks (its V then streams
@@ -426,13 +427,17 @@ __device__ __forceinline__ void vx_attention_mfma_body(
     static_assert(HD == 64 || HD == 128, "head_dim 64 or 128");
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int n = lane & 15, r = lane >> 4;
-    const int nw_w = (n_chunks_w + NCW - 1) / NCW;   // wavefront chunks holding positions to store
-    const int nw = (n_chunks + NCW - 1) / NCW;       // wavefront chunks attended (partials per query)
+    // n_chunks / n_chunks_w count ACH-position chunks (attended / holding
+    // rows to store); this kernel's wavefronts take WCH positions each
+    const int nw_w = (n_chunks_w * ACH + WCH - 1) / WCH;   // wavefronts holding positions to store
+    const int nw = (n_chunks * ACH + WCH - 1) / WCH;       // wavefronts with positions to attend
     const int ncg = (nw_w + 3) / 4;
     const int g = blockIdx.x / (n_qg * ncg);
     const int qg = (blockIdx.x / ncg) % n_qg;
-    const int ch = (blockIdx.x % ncg) * 4 + wave;
-    if (!QKV && ch >= nw_w) return;   // QKV: after the workgroup barrier below
+    const int wg = blockIdx.x % ncg;
+    const int ch = wg * 4 + wave;
+    // QKV, MERGE: every wavefront reaches the workgroup barriers below
+    if (!QKV && !MERGE && ch >= nw_w) return;
     const bool attend = ch < nw;
     const int G = n_heads / n_kv, QM = G * M;
     const int kvd = n_kv * HD, qd = n_heads * HD, half = HD / 2;
@@ -441,17 +446,17 @@ __device__ __forceinline__ void vx_attention_mfma_body(
     // K rows of positions tc + 16 pg + n (dims 16 j + 4 r .. + 3) and V rows
     // of positions tc + 16 pg + 4 r + s (dims 64 u + 4 n .. + 3) of chunk tc
     // from the cache; positions past the cache end read as zeros
-    float4 kr[2][NJ], vr[2][4][NV4];
+    float4 kr[NPG][NJ], vr[NPG][4][NV4];
     auto load_k = [&](int tc) {
 #pragma unroll
-        for (int pg = 0; pg < 2; pg++) {
+        for (int pg = 0; pg < NPG; pg++) {
             const int pos = tc + 16 * pg + n;
             const size_t off = (size_t)min(pos, n_ctx - 1) * kvd + g * HD + 4 * r;
 #pragma unroll
             for (int j = 0; j < NJ; j++) kr[pg][j] = vx_kv_load4<KH>(kc, off + 16 * j);
         }
 #pragma unroll
-        for (int pg = 0; pg < 2; pg++) {
+        for (int pg = 0; pg < NPG; pg++) {
             const bool ok = tc + 16 * pg + n < n_ctx;
 #pragma unroll
             for (int j = 0; j < NJ; j++) kr[pg][j] = vx_keep4(ok, kr[pg][j]);
@@ -459,7 +464,7 @@ __device__ __forceinline__ void vx_attention_mfma_body(
     };
     auto load_v = [&](int tc) {
 #pragma unroll
-        for (int pg = 0; pg < 2; pg++)
+        for (int pg = 0; pg < NPG; pg++)
 #pragma unroll
             for (int st = 0; st < 4; st++) {
                 const int pv = tc + 16 * pg + 4 * r + st;
@@ -468,7 +473,7 @@ __device__ __forceinline__ void vx_attention_mfma_body(
                 for (int u = 0; u < NV4; u++) vr[pg][st][u] = vx_kv_load4<KH>(vc, ov + 64 * u);
             }
 #pragma unroll
-        for (int pg = 0; pg < 2; pg++)
+        for (int pg = 0; pg < NPG; pg++)
 #pragma unroll
             for (int st = 0; st < 4; st++) {
                 const bool okv = tc + 16 * pg + 4 * r + st < n_ctx;
@@ -505,7 +510,18 @@ __device__ __forceinline__ void vx_attention_mfma_body(
     // forward is clamped) -- head g's new k/v rows too (query group 0 also
     // stores them into the cache); the wavefronts take them from LDS.
     bool has_new_wg = false;   // QKV: this workgroup's chunks hold rows of this forward
-    __shared__ float4 s_new[QKV ? VX_ATT_MFMA_MAX_M * 2 * (HD / 4) : 1];   // [row][k, v][d4]
+    // LDS (float4 units): the new k/v rows [row][k, v][d4] and the q vectors
+    // (QKV), then the accumulators the workgroup merges (MERGE).  At head_dim
+    // 128 the three would take 58 KB (2 workgroups per CU), so the merge
+    // reuses the first two once every wavefront is past its chunks (one more
+    // barrier); at 64 they fit side by side in 25 KB.
+    constexpr int N_NEW = QKV ? VX_ATT_MFMA_MAX_M * 2 * (HD / 4) : 0, N_Q = QKV ? 16 * (HD / 4 + 1) : 0;
+    constexpr int N_MRG = MERGE ? 3 * NJ * 64 : 0;
+    constexpr bool ALIAS = QKV && MERGE && (N_NEW + N_Q + N_MRG) * 16 > 32768;
+    constexpr int N_BUF0 = ALIAS ? (N_NEW + N_Q > N_MRG ? N_NEW + N_Q : N_MRG) : N_NEW + N_Q + N_MRG;
+    constexpr int N_BUF = N_BUF0 > 0 ? N_BUF0 : 1;
+    __shared__ float4 s_buf[N_BUF];
+    float4 *const s_new = s_buf;
     // new row of this forward at cache position pos, or -1 (rows sit at
     // min(n_past + m, n_ctx - 1); only a one-row forward is clamped)
     auto new_row = [&](int pos) -> int {
@@ -516,11 +532,11 @@ __device__ __forceinline__ void vx_attention_mfma_body(
     };
     if constexpr (QKV) {
         constexpr int Q4 = HD / 4, QS = Q4 + 1;                      // float4 per row, padded stride
-        __shared__ float4 s_q[16 * QS];
+        float4 *const s_q = s_buf + N_NEW;
         constexpr int QI = 16 * Q4 / ATT_THREADS;                  // q items per thread (1 or 2)
         const int lo = n_past < n_ctx ? n_past : n_ctx - 1;
         const int hi = min(n_past + M - 1, n_ctx - 1);
-        const int c0 = (blockIdx.x % ncg) * 4 * WCH;
+        const int c0 = wg * 4 * WCH;
         const bool has_new = hi >= c0 && lo < c0 + 4 * WCH;          // uniform over the workgroup
         const int n_new = M * 2 * Q4;                                // new k/v items (row, k|v, float4)
         // new k/v item `it` of this forward: its q|k|v column, cache element,
@@ -607,8 +623,7 @@ __device__ __forceinline__ void vx_attention_mfma_body(
         for (int j = 0; j < NJ; j++) qv[j] = s_q[n * QS + 4 * j + r];
         has_new_wg = has_new;
     }
-    if (ch >= nw_w) return;
-    if (!attend) return;
+    if (!MERGE && (ch >= nw_w || !attend)) return;
 
     // The wavefront's chunks in order, with the online-softmax rescale
     // (src/tensor.c:156-171 over the chunks): running max rm and sum rl of
@@ -619,22 +634,23 @@ __device__ __forceinline__ void vx_attention_mfma_body(
     for (int c = 0; c < NJ; c++) O[c] = vx_f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int cc = 0; cc < NCW; cc++) {
-        const int tc = t0 + cc * ACH;
+        if (MERGE && !attend) break;
+        const int tc = t0 + cc * CH;
         if (cc > 0) load_v(tc);        // this chunk's V streams while its scores run
         // this forward's own k rows from LDS (the cache rows may not be written yet)
         if (QKV && has_new_wg) {
 #pragma unroll
-            for (int pg = 0; pg < 2; pg++) {
+            for (int pg = 0; pg < NPG; pg++) {
                 const int mn = new_row(tc + 16 * pg + n);
                 if (mn >= 0)
 #pragma unroll
                     for (int j = 0; j < NJ; j++) kr[pg][j] = s_new[(mn * 2) * (HD / 4) + 4 * j + r];
             }
         }
-        // scores of the chunk's 32 positions: S[pg] item i = position 16 pg + 4 r + i
-        vx_f32x4 S[2];
+        // scores of the chunk's positions: S[pg] item i = position 16 pg + 4 r + i
+        vx_f32x4 S[NPG];
 #pragma unroll
-        for (int pg = 0; pg < 2; pg++) {
+        for (int pg = 0; pg < NPG; pg++) {
             S[pg] = vx_f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int j = 0; j < NJ; j++) {
@@ -644,11 +660,11 @@ __device__ __forceinline__ void vx_attention_mfma_body(
                 S[pg] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[pg][j].w, qv[j].w, S[pg], 0, 0, 0);
             }
         }
-        if (cc + 1 < NCW) load_k(tc + ACH);       // the next chunk's K behind this chunk's V
+        if (cc + 1 < NCW) load_k(tc + CH);        // the next chunk's K behind this chunk's V
         if constexpr (!V_EARLY) load_v(tc);
         if (QKV && has_new_wg) {
 #pragma unroll
-            for (int pg = 0; pg < 2; pg++)
+            for (int pg = 0; pg < NPG; pg++)
 #pragma unroll
                 for (int st = 0; st < 4; st++) {
                     const int mv = new_row(tc + 16 * pg + 4 * r + st);
@@ -658,10 +674,10 @@ __device__ __forceinline__ void vx_attention_mfma_body(
                 }
         }
         // chunk statistics of query n against the running ones
-        float sc[2][4];
+        float sc[NPG][4];
         float cm = -INFINITY;
 #pragma unroll
-        for (int pg = 0; pg < 2; pg++)
+        for (int pg = 0; pg < NPG; pg++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int t = tc + 16 * pg + 4 * r + i;
@@ -670,9 +686,9 @@ __device__ __forceinline__ void vx_attention_mfma_body(
             }
         cm = vx_max_x32(vx_max_x16(cm));
         const float nm = fmaxf(rm, cm);
-        float p[2][4], l = 0.0f;
+        float p[NPG][4], l = 0.0f;
 #pragma unroll
-        for (int pg = 0; pg < 2; pg++)
+        for (int pg = 0; pg < NPG; pg++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 p[pg][i] = nm == -INFINITY || sc[pg][i] == -INFINITY ? 0.0f : expf(sc[pg][i] - nm);
@@ -691,7 +707,7 @@ __device__ __forceinline__ void vx_attention_mfma_body(
 
         // P.V
 #pragma unroll
-        for (int pg = 0; pg < 2; pg++)
+        for (int pg = 0; pg < NPG; pg++)
 #pragma unroll
             for (int st = 0; st < 4; st++)
 #pragma unroll
@@ -701,9 +717,53 @@ __device__ __forceinline__ void vx_attention_mfma_body(
                     O[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, p[pg][st], O[c], 0, 0, 0);
                 }
     }
+    int pidx = ch, np = nw;    // this partial's index, partials per query
+    if constexpr (MERGE) {
+        // the workgroup's four wavefronts merged in LDS into one partial
+        // (online-softmax rescale), written by wavefront 0
+        __shared__ float s_ml[4][2][16];                                    // [wavefront][max, sum][query]
+        vx_f32x4 *const s_o = (vx_f32x4 *)(s_buf + (ALIAS ? 0 : N_NEW + N_Q));   // [wavefront - 1][chain][lane]
+        if (r == 0) {
+            s_ml[wave][0][n] = rm;
+            s_ml[wave][1][n] = rl;
+        }
+        if (ALIAS) __syncthreads();   // no wavefront reads the q vectors or new rows any more
+        if (wave > 0)
+#pragma unroll
+            for (int c = 0; c < NJ; c++) s_o[((wave - 1) * NJ + c) * 64 + lane] = O[c];
+        __syncthreads();
+        if (wave != 0) return;
+        float gm = rm;
+#pragma unroll
+        for (int w = 1; w < 4; w++) gm = fmaxf(gm, s_ml[w][0][n]);
+        if (gm != -INFINITY) {
+            const float f0 = rm == -INFINITY ? 0.0f : expf(rm - gm);
+            rl *= f0;
+#pragma unroll
+            for (int c = 0; c < NJ; c++) O[c] *= f0;
+#pragma unroll
+            for (int w = 1; w < 4; w++) {
+                const float mw = s_ml[w][0][n];
+                const float f = mw == -INFINITY ? 0.0f : expf(mw - gm);
+                rl = fmaf(f, s_ml[w][1][n], rl);
+#pragma unroll
+                for (int c = 0; c < NJ; c++) {
+                    const vx_f32x4 v = s_o[((w - 1) * NJ + c) * 64 + lane];
+                    O[c][0] = fmaf(f, v[0], O[c][0]);
+                    O[c][1] = fmaf(f, v[1], O[c][1]);
+                    O[c][2] = fmaf(f, v[2], O[c][2]);
+                    O[c][3] = fmaf(f, v[3], O[c][3]);
+                }
+            }
+        }
+        rm = gm;
+        pidx = wg;
+        np = (nw + 3) / 4;
+        if (wg >= np) return;
+    }
     if (!qok) return;
     const size_t ps = PART_STRIDE(HD);
-    float *pq = part + (((size_t)g * nw + ch) * QM + qi) * ps;
+    float *pq = part + (((size_t)g * np + pidx) * QM + qi) * ps;
     if (r == 0) {
         pq[0] = rm;
         pq[1] = rl;
@@ -716,22 +776,36 @@ __device__ __forceinline__ void vx_attention_mfma_body(
                 make_float4(O[4 * u][i], O[4 * u + 1][i], O[4 * u + 2][i], O[4 * u + 3][i]);
 }
 
-// Wavefront chunks: the q-rows kernel at head_dim 128 (prompt prefill: many
-// query groups per head, so half the wavefronts still fill the chip) walks
-// two 32-position chunks per wavefront, V streaming behind K, and writes half
-// the partials (rocprofv3, 2048-token prefill: 205 -> 188 us per launch).  The
-// q|k|v kernels keep one chunk per wavefront: at head_dim 128 (the verify,
-// nine rows) two chunks made the attention 24 -> 27.6 us per layer -- half as
-// many wavefronts, each with a longer K -> V chain -- and 3 wavefronts per SIMD
-// fit the registers of one.
+// Work per wavefront of the fp32-MFMA kernels.
+// * NCW chunks per wavefront: the q-rows kernel at head_dim 128 (prompt
+//   prefill: many query groups per head, so half the wavefronts still fill the
+//   chip) walks two, V streaming behind K, and writes half the partials
+//   (rocprofv3, 2048-token prefill: 205 -> 188 us per launch).  At head_dim
+//   128 with q|k|v sums (the verify, nine rows) two chunks made the attention
+//   24 -> 27.6 us per layer: half as many wavefronts, each with a longer K -> V
+//   chain.
+// * NPG groups of 16 positions per chunk, MERGE: the draft decode (head_dim
+//   64, q|k|v sums, one row) has few wavefronts and each spends most of its
+//   time on its own instructions, so its wavefronts take 16 positions and the
+//   four of a workgroup merge their partials in LDS (one partial per 64
+//   positions for the output projection to combine).
 template <int HD, bool QKV>
-struct vx_att_ncw_of {
-    static constexpr int v = HD == 128 && !QKV ? 2 : 1;
+struct vx_att_cfg {
+    static constexpr int NCW = HD == 128 && !QKV ? 2 : 1;
+    static constexpr int NPG = QKV ? 1 : 2;
+    static constexpr bool MERGE = QKV;
+    static constexpr int WCH = NCW * NPG * 16;
 };
-static int vx_att_ncw(int head_dim, bool qkv)
+// positions per wavefront and whether a workgroup merges its partials
+static void vx_att_geom(int head_dim, bool qkv, int *wch, bool *merge)
 {
-    if (head_dim == 128) return qkv ? vx_att_ncw_of<128, true>::v : vx_att_ncw_of<128, false>::v;
-    return qkv ? vx_att_ncw_of<64, true>::v : vx_att_ncw_of<64, false>::v;
+    if (head_dim == 128) {
+        *wch = qkv ? vx_att_cfg<128, true>::WCH : vx_att_cfg<128, false>::WCH;
+        *merge = qkv ? vx_att_cfg<128, true>::MERGE : vx_att_cfg<128, false>::MERGE;
+    } else {
+        *wch = qkv ? vx_att_cfg<64, true>::WCH : vx_att_cfg<64, false>::WCH;
+        *merge = qkv ? vx_att_cfg<64, true>::MERGE : vx_att_cfg<64, false>::MERGE;
+    }
 }
 
 template <int HD>
@@ -740,7 +814,8 @@ __global__ __launch_bounds__(ATT_THREADS) __attribute__((amdgpu_waves_per_eu(3))
     float *__restrict__ kc, float *__restrict__ vc, int n_chunks, int n_chunks_w, int n_qg,
     float *__restrict__ part, vx_qkv_args qa)
 {
-    vx_attention_mfma_body<false, HD, false, vx_att_ncw_of<HD, false>::v>(
+    using C = vx_att_cfg<HD, false>;
+    vx_attention_mfma_body<false, HD, false, C::NCW, C::NPG, C::MERGE>(
         q, M, n_past, n_ctx, n_heads, n_kv, cap, kc, vc, n_chunks, n_chunks_w, n_qg, part, qa);
 }
 
@@ -750,7 +825,8 @@ __global__ __launch_bounds__(ATT_THREADS) __attribute__((amdgpu_waves_per_eu(3))
     float *__restrict__ kc, float *__restrict__ vc, int n_chunks, int n_chunks_w, int n_qg,
     float *__restrict__ part, vx_qkv_args qa)
 {
-    vx_attention_mfma_body<true, HD, KH, vx_att_ncw_of<HD, true>::v>(
+    using C = vx_att_cfg<HD, true>;
+    vx_attention_mfma_body<true, HD, KH, C::NCW, C::NPG, C::MERGE>(
         q, M, n_past, n_ctx, n_heads, n_kv, cap, kc, vc, n_chunks, n_chunks_w, n_qg, part, qa);
 }
 
@@ -971,9 +1047,11 @@ static int vx_attention_run(const float *q, const vx_qkv_args *qa, long n_clr, i
     memset(&none, 0, sizeof(none));
     const bool mfma = (head_dim == 64 || head_dim == 128) && (!qa || M <= VX_ATT_MFMA_MAX_M);
     if (mfma) {
-        // fp32-MFMA kernel: 4 wavefronts per workgroup, NCW chunks per wavefront
-        const int ncw = vx_att_ncw(head_dim, qa != nullptr);
-        const int nw_w = (n_chunks_w + ncw - 1) / ncw;
+        // fp32-MFMA kernel: 4 wavefronts per workgroup, wch positions each
+        int wch;
+        bool merge;
+        vx_att_geom(head_dim, qa != nullptr, &wch, &merge);
+        const int nw_w = (n_chunks_w * ACH + wch - 1) / wch;
         const int nqg = (QM + 15) / 16, ncg = (nw_w + 3) / 4;
         const int grid = n_kv_heads * nqg * ncg;
         const vx_qkv_args &A = qa ? *qa : none;
@@ -1012,8 +1090,11 @@ static int vx_attention_run(const float *q, const vx_qkv_args *qa, long n_clr, i
     VXH_LAUNCHED();
     // partials per query: one per wavefront chunk of the MFMA kernels
     if (mfma) {
-        const int ncw = vx_att_ncw(head_dim, qa != nullptr);
-        n_chunks = (n_chunks + ncw - 1) / ncw;
+        int wch;
+        bool merge;
+        vx_att_geom(head_dim, qa != nullptr, &wch, &merge);
+        const int nw = (n_chunks * ACH + wch - 1) / wch;
+        n_chunks = merge ? (nw + 3) / 4 : nw;
     }
     if (n_chunks_out) *n_chunks_out = n_chunks;
     if (parts_only) return VXH_OK;
