@@ -114,6 +114,11 @@ int vxh_synth_blocks(void *dev_blocks, int type, int n_rows, int n_cols, uint64_
  * Replaces the embedding lookup of src/model.c:454-500. */
 int vxh_qmat_gather_rows(const vxh_qmat *m, const int *dev_ids, int n, float scale,
                          float *out, int ld_out, vxh_stream s);
+/* The same gather, and the n_clr doubles at clr zeroed by the same launch
+ * (a forward's accumulators that no kernel reads during it).  No counterpart
+ * in the reference. */
+int vxh_qmat_gather_rows_clear(const vxh_qmat *m, const int *dev_ids, int n, float scale,
+                               float *out, int ld_out, double *clr, long n_clr, vxh_stream s);
 
 /* Longest row a panel or a row kernel takes (elements). */
 #define VXH_MAX_K 24576

@@ -352,8 +352,14 @@ extern "C" int vxh_synth_blocks(void *dev_blocks, int type, int n_rows, int n_co
 __global__ void vx_gather_kernel(const uint32_t *__restrict__ qs, const uint32_t *__restrict__ dpl,
                                  int type, int n_rows_logical, int n_cols, int n_pairs,
                                  const int *__restrict__ ids, float scale, float *__restrict__ out,
-                                 int ld_out)
+                                 int ld_out, double *__restrict__ clr, long n_clr)
 {
+    if (clr) {
+        // this block's share of the range to clear
+        const long nb = (long)gridDim.x * gridDim.y, bi = (long)blockIdx.y * gridDim.x + blockIdx.x;
+        const long per = (n_clr + nb - 1) / nb, e = min(bi * per + per, n_clr);
+        for (long k = bi * per + threadIdx.x; k < e; k += blockDim.x) clr[k] = 0.0;
+    }
     int i = blockIdx.y;
     int id = ids[i];
     float *o = out + (size_t)i * ld_out;
@@ -381,16 +387,25 @@ __global__ void vx_gather_kernel(const uint32_t *__restrict__ qs, const uint32_t
     }
 }
 
-extern "C" int vxh_qmat_gather_rows(const vxh_qmat *m, const int *dev_ids, int n, float scale,
-                                    float *out, int ld_out, vxh_stream s)
+extern "C" int vxh_qmat_gather_rows_clear(const vxh_qmat *m, const int *dev_ids, int n, float scale,
+                                          float *out, int ld_out, double *clr, long n_clr, vxh_stream s)
 {
-    if (n <= 0) return VXH_OK;
+    if (n_clr < 0 || (n_clr > 0 && !clr)) return vxh_fail(VXH_ERR_PARAM, "gather: clear %ld doubles at %p", n_clr,
+                                                          (void *)clr);
+    if (n <= 0) return n_clr > 0 ? vxh_fill_f32((float *)clr, 0.0f, 2 * (size_t)n_clr, s) : VXH_OK;
     int gx = (m->n_cols + 255) / 256;
     if (gx > 64) gx = 64;
     dim3 grid(gx, n);
     vx_gather_kernel<<<grid, 256, 0, vxh_hs(s)>>>((const uint32_t *)m->qs, (const uint32_t *)m->d,
                                                   m->type, m->n_rows, m->n_cols, m->n_pairs, dev_ids,
-                                                  scale, out, ld_out);
+                                                  scale, out, ld_out, n_clr > 0 ? clr : nullptr, n_clr);
     VXH_LAUNCHED();
     return VXH_OK;
+}
+
+extern "C" int vxh_qmat_gather_rows(const vxh_qmat *m, const int *dev_ids, int n, float scale,
+                                    float *out, int ld_out, vxh_stream s)
+{
+    if (n <= 0) return VXH_OK;
+    return vxh_qmat_gather_rows_clear(m, dev_ids, n, scale, out, ld_out, nullptr, 0, s);
 }

@@ -176,7 +176,7 @@ static void dev_free(vx_dev *d)
     vxh_free(d->rope_cos); vxh_free(d->rope_sin);
     vxh_free(d->tok); vxh_free(d->x); vxh_free(d->xn); vxh_free(d->xtail);
     vxh_free(d->q); vxh_free(d->att); vxh_free(d->logits);
-    vxh_free(d->acc_qkv); vxh_free(d->acc_x); vxh_free(d->acc_gu); vxh_free(d->acc_lg);
+    vxh_free(d->acc_qkv); vxh_free(d->acc_gu); vxh_free(d->acc_lg);
     vxh_free(d->stats); vxh_free(d->acc_out);
     vxh_free(d->ss); vxh_free(d->hrows); vxh_free(d->cnt); vxh_free(d->cnt_row);
     vxh_free(d->x2); vxh_free(d->acc_y);
@@ -238,7 +238,11 @@ static vx_error dev_alloc_common(vx_model *m)
     d->ld_gu = gu_rows(d->F);
     d->ld_lg = round32(d->V);
     TRY(vxh_malloc((void **)&d->acc_qkv, sizeof(double) * B * (size_t)d->ld_qkv));
-    TRY(vxh_malloc((void **)&d->acc_x, sizeof(double) * B * (size_t)d->d));
+    /* ss then acc_x in one allocation, so the prologue forward clears both
+     * (the sums of squares, the rows it starts from) with one range */
+    const size_t n_ss = (size_t)(d->n_layers + 1) * 2 * B;
+    TRY(vxh_malloc((void **)&d->ss, sizeof(double) * (n_ss + (size_t)B * d->d)));
+    d->acc_x = d->ss + n_ss;
     TRY(vxh_malloc((void **)&d->acc_gu, sizeof(double) * B * (size_t)d->ld_gu));
     TRY(vxh_malloc((void **)&d->acc_lg, sizeof(double) * B * (size_t)d->ld_lg));
     d->acc_dirty = 1;                  /* zeroed before the first forward */
@@ -249,7 +253,6 @@ static vx_error dev_alloc_common(vx_model *m)
     TRY(vxh_xpanel_alloc(&d->xp_att, B, d->d));
     TRY(vxh_xpanel_alloc(&d->xp_x, B, d->d));
     TRY(vxh_xpanel_alloc(&d->xp_h, B, d->F));
-    TRY(vxh_malloc((void **)&d->ss, sizeof(double) * (size_t)(d->n_layers + 1) * 2 * B));
     TRY(vxh_malloc((void **)&d->hrows, sizeof(float) * B * (size_t)d->F));
     TRY(vxh_malloc((void **)&d->cnt, sizeof(unsigned) * VX_N_COUNTERS));
     TRY(vxh_malloc((void **)&d->cnt_row, sizeof(unsigned) * B * 64));
@@ -813,6 +816,7 @@ static vx_error zero_acc(vx_dev *d)
     vxh_stream s = d->stream;
     TRY(vxh_fill_f32((float *)d->acc_qkv, 0.0f, 2 * (size_t)B * d->ld_qkv, s));
     TRY(vxh_fill_f32((float *)d->acc_x, 0.0f, 2 * (size_t)B * d->d, s));
+    d->acc_x_rows = 0;
     TRY(vxh_fill_f32((float *)d->acc_gu, 0.0f, 2 * (size_t)B * d->ld_gu, s));
     TRY(vxh_fill_f32((float *)d->acc_lg, 0.0f, 2 * (size_t)B * d->ld_lg, s));
     TRY(vxh_fill_f32((float *)d->acc_y, 0.0f, 2 * (size_t)B * d->d, s));
@@ -856,7 +860,7 @@ static vx_error forward_fused(vx_model *m, int M, int n_past, int logits_mode)
     vxh_stream s = d->stream;
     vx_error e;
 #define SS(l, j) (d->ss + ((size_t)(l) * 2 + (j)) * B)
-    if (d->acc_dirty && (e = zero_acc(d)) != VX_OK) return e;
+    if ((d->acc_dirty || d->acc_x_rows) && (e = zero_acc(d)) != VX_OK) return e;
     d->acc_dirty = 1;
     TRY(vxh_fill_f32((float *)d->ss, 0.0f, 2 * (size_t)(L + 1) * 2 * B, s));
     if (d->has_embd) TRY(vxh_qmat_gather_rows(&d->embd, d->tok, M, vx_get_synthetic_weight_scale(), d->x, dd, s));
@@ -996,9 +1000,18 @@ static vx_error forward_pro(vx_model *m, int M, int n_past, int logits_mode)
 #define SS(l, j) (d->ss + ((size_t)(l) * 2 + (j)) * B)
     if (d->acc_dirty && (e = zero_acc(d)) != VX_OK) return e;
     d->acc_dirty = 1;
-    TRY(vxh_fill_f32((float *)d->ss, 0.0f, 2 * (size_t)(L + 1) * 2 * B, s));
-    if (d->has_embd) TRY(vxh_qmat_gather_rows(&d->embd, d->tok, M, vx_get_synthetic_weight_scale(), d->x, dd, s));
-    else TRY(vxh_fill_f32(d->x, 0.0f, (size_t)M * dd, s));
+    /* the sums of squares and acc_x's rows (the previous prologue forward's
+     * output GEMM may have left its last down projection in acc_x_rows of
+     * them) are cleared by the embedding gather's launch */
+    const long n_clr = (long)(L + 1) * 2 * B + (long)(M > d->acc_x_rows ? M : d->acc_x_rows) * dd;
+    if (d->has_embd)
+        TRY(vxh_qmat_gather_rows_clear(&d->embd, d->tok, M, vx_get_synthetic_weight_scale(), d->x, dd, d->ss,
+                                       n_clr, s));
+    else {
+        TRY(vxh_fill_f32(d->x, 0.0f, (size_t)M * dd, s));
+        TRY(vxh_fill_f32((float *)d->ss, 0.0f, 2 * (size_t)n_clr, s));
+    }
+    d->acc_x_rows = 0;
 
     /* one- and two-row forwards (draft decode): the output projection
      * combines the attention partials itself */
@@ -1087,19 +1100,20 @@ static vx_error forward_pro(vx_model *m, int M, int n_past, int logits_mode)
             if ((e = pgemm(d, &Ld->wd, &p, M, d->acc_x, dd, dd, VX_PROF_DOWN, dd))) return e;
         }
     }
-    /* x += last down projection (clears acc_x) */
-    TRY(vxh_acc_store(d->acc_x, dd, M, dd, d->x, dd, d->x, dd, s));
-
     int gu_cleared = 0;
-    if (logits_mode != VX_LOGITS_NONE) {
+    if (logits_mode != VX_LOGITS_NONE && d->has_out) {
+        /* the output GEMM adds the last down projection to the residual in
+         * its prologue (t = x + acc_x, as the residual kinds do) and leaves
+         * acc_x to the next forward's clear */
         const int rows = logits_mode == VX_LOGITS_LAST ? 1 : M;
         const int r0 = logits_mode == VX_LOGITS_LAST ? M - 1 : 0;
-        const int orows = d->has_out ? d->out_rows : 0;
+        const int orows = d->out_rows;
         if (orows < V) TRY(vxh_fill_rows(d->logits, V, rows, orows, V - orows, -1e30f, s));
-        if (d->has_out) {
+        {
             memset(&p, 0, sizeof(p));
-            p.kind = VXH_PRO_ROWS;
+            p.kind = VXH_PRO_RESID;
             p.x = d->x + (size_t)r0 * dd; p.ldx = dd;
+            p.src = d->acc_x + (size_t)r0 * dd; p.ld_src = dd;
             p.w = d->has_out_norm ? d->out_norm : NULL;
             p.ss = d->has_out_norm ? SS(L, 0) : NULL;
             p.clear = d->acc_gu; p.n_clear = (size_t)M * d->ld_gu;
@@ -1111,9 +1125,17 @@ static vx_error forward_pro(vx_model *m, int M, int n_past, int logits_mode)
             else
                 TRY(vxh_acc_store(d->acc_lg, d->ld_lg, rows, orows, d->logits, V, NULL, 0, s));
         }
+    } else {
+        /* x += last down projection (clears acc_x) */
+        TRY(vxh_acc_store(d->acc_x, dd, M, dd, d->x, dd, d->x, dd, s));
+        if (logits_mode != VX_LOGITS_NONE) {   /* no output matrix: every logit -1e30 */
+            const int rows = logits_mode == VX_LOGITS_LAST ? 1 : M;
+            TRY(vxh_fill_rows(d->logits, V, rows, 0, V, -1e30f, s));
+        }
     }
     if (!gu_cleared && L > 0) TRY(vxh_fill_f32((float *)d->acc_gu, 0.0f, 2 * (size_t)M * d->ld_gu, s));
 #undef SS
+    d->acc_x_rows = gu_cleared ? M : 0;
     d->acc_dirty = 0;
     return VX_OK;
 }
@@ -1151,7 +1173,7 @@ vx_error vx_dev_forward(vx_model *m, int M, int n_past, int logits_mode)
     vxh_stream s = d->stream;
     vx_error e;
 
-    if (d->acc_dirty && (e = zero_acc(d)) != VX_OK) return e;
+    if ((d->acc_dirty || d->acc_x_rows) && (e = zero_acc(d)) != VX_OK) return e;
     d->acc_dirty = 1;
     if (d->has_embd) TRY(vxh_qmat_gather_rows(&d->embd, d->tok, M, vx_get_synthetic_weight_scale(), d->x, dd, s));
     else TRY(vxh_fill_f32(d->x, 0.0f, (size_t)M * dd, s));
@@ -1283,7 +1305,7 @@ static vx_error forward_prefill(vx_model *m, const int *tokens, int M, int n_pas
     }
     if (!last_logits) return VX_OK;
     /* the last row's logits through the decode GEMM (src/model.c:598-615) */
-    if (d->acc_dirty && (e = zero_acc(d)) != VX_OK) return e;
+    if ((d->acc_dirty || d->acc_x_rows) && (e = zero_acc(d)) != VX_OK) return e;
     const float *src = d->pf_x + (size_t)(M - 1) * dd;
     const int V = d->V, orows = d->has_out ? d->out_rows : 0;
     if (orows < V) TRY(vxh_fill_rows(d->logits, V, 1, orows, V - orows, -1e30f, s));

@@ -82,6 +82,10 @@ typedef struct vx_dev {
     double *acc_qkv, *acc_x, *acc_gu, *acc_lg;
     int ld_qkv, ld_gu, ld_lg;
     int acc_dirty;                     /* a forward failed part-way: re-zero first */
+    int acc_x_rows;                    /* rows of acc_x still holding a down projection
+                                        * (the prologue forward's output GEMM reads it
+                                        * in place); the next prologue forward clears
+                                        * them with its embedding gather, others re-zero */
     vxh_panel pan_d, pan_f;
     vxh_workspace ws;
     /* sampling buffers */
@@ -94,7 +98,7 @@ typedef struct vx_dev {
      * ss[(l * 2 + j) * 16 + m] (j = 0 attention norm, 1 FFN norm; l = L is
      * the output norm) and the last-arriver counters (zero between uses) */
     vxh_xpanel xp_att, xp_x, xp_h;
-    double *ss;
+    double *ss;                        /* [(L+1)][2][16]; acc_x follows it in one allocation */
     float *hrows;                      /* [16][F] SwiGLU output of the fused path    */
     unsigned *cnt;                     /* [VX_N_COUNTERS] GEMM arrival counters      */
     unsigned *cnt_row;                 /* [16 * 64] attention rows, 64 words apart   */
