@@ -392,10 +392,32 @@ __device__ __forceinline__ void vx_pro_attn(const vx_pro_args &p, int p0, int np
 
 #define VX_RING 4
 
+// Wavefronts (tiles) per workgroup: 8 for the residual prologue of Q4_0
+// verify batches at 8-pair slices (every workgroup rebuilds its K slice of
+// the panel from x, the fp64 pending sums and the norm weight; 8 tiles per
+// workgroup halve those rebuilds: 22016x4096 at M = 9 20.6 -> 18.6 us,
+// 12288x4096 13.2 -> 12.8 us), 4 otherwise (Q8_0 11008x4096 15.2 -> 16.7 us
+// and the 16-pair logits GEMM 26.7 -> 27.5 us with 8).
+template <int QT, int M, bool AVX2, int PPW, int EPI, int PRO>
+struct vx_nwv {
+    static constexpr int v =
+        PRO == VX_PRO_RESID && QT == 2 && M >= 5 && PPW == 8 && EPI == VX_EPI_NONE && !AVX2 ? 8 : 4;
+};
+
 // QT: 2 = Q4_0, 8 = Q8_0.
 template <int QT, int M, bool AVX2, int PPW, int EPI = VX_EPI_NONE, int PRO = VX_PRO_PANEL>
-__global__ __launch_bounds__(256) void vx_gemm_kernel(vx_gemm_args a)
+__global__ __launch_bounds__((64 * vx_nwv<QT, M, AVX2, PPW, EPI, PRO>::v)) void vx_gemm_kernel(vx_gemm_args a)
 {
+    constexpr int NWV = vx_nwv<QT, M, AVX2, PPW, EPI, PRO>::v;   // wavefronts, one tile each
+    constexpr int NT = 64 * NWV;                          // threads
+    static_assert(NWV == 4 || (EPI == VX_EPI_NONE && !AVX2 && PRO != VX_PRO_ATTN),
+                  "epilogues, AVX2 corrections and the attention prologue assume 4 wavefronts");
+    // With 8 wavefronts per workgroup the compiler may give a wavefront at
+    // most 256 registers and, seeing no AGPR use, selects the VGPR-destination
+    // MFMA form, whose destinations it overlaps with their own A/B sources
+    // (results have been wrong with that form here).  An AGPR clobber keeps
+    // the AGPR-destination form.
+    if constexpr (NWV > 4) asm volatile("" ::: "a0");
     static_assert(EPI == VX_EPI_NONE || PRO == VX_PRO_PANEL, "fused epilogues read panels");
     static_assert(!AVX2 || PRO == VX_PRO_PANEL, "AVX2-lane corrections come with panels");
     constexpr bool PANEL = PRO == VX_PRO_PANEL;
@@ -408,14 +430,14 @@ __global__ __launch_bounds__(256) void vx_gemm_kernel(vx_gemm_args a)
     // and slowed 22016x4096 at M = 9 from 21.1 to 23.8 us)
     constexpr bool DUAL = M >= 5 && (PRO == VX_PRO_PANEL || PRO == VX_PRO_ROWS);
     constexpr int UNITS = PPW * 8 * NS;    // panel units of a full slice
-    constexpr int UPT = (UNITS + 255) / 256;
-    __shared__ uint4 lds[UPT * 256];
+    constexpr int UPT = (UNITS + NT - 1) / NT;
+    __shared__ uint4 lds[UPT * NT];
     __shared__ float lcorr[AVX2 ? PPW * 2 * M : 1];
     __shared__ float lrs[PANEL ? 1 : M];   // prologue kinds: output scale of each row's slice
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int grp = blockIdx.x / a.n_splits, split = blockIdx.x % a.n_splits;
-    const int T = grp * 4 + wave;
+    const int T = grp * NWV + wave;
     const bool tile_ok = T < a.n_tiles;
     const int Tc = tile_ok ? T : 0;
     const int p0 = split * PPW;
@@ -429,7 +451,7 @@ __global__ __launch_bounds__(256) void vx_gemm_kernel(vx_gemm_args a)
         if (a.p.clr) {
             const long per = (a.p.n_clr + gridDim.x - 1) / gridDim.x;
             const long b = (long)blockIdx.x * per, e = min(b + per, a.p.n_clr);
-            for (long i = b + threadIdx.x; i < e; i += 256) a.p.clr[i] = 0.0;
+            for (long i = b + threadIdx.x; i < e; i += NT) a.p.clr[i] = 0.0;
         }
     }
 
@@ -439,14 +461,14 @@ __global__ __launch_bounds__(256) void vx_gemm_kernel(vx_gemm_args a)
     if constexpr (PANEL) {
         const uint4 *psrc = a.panel + (size_t)p0 * 8 * NS;
 #pragma unroll
-        for (int j = 0; j < UPT; j++) pv[j] = psrc[min(j * 256 + (int)threadIdx.x, units - 1)];
+        for (int j = 0; j < UPT; j++) pv[j] = psrc[min(j * NT + (int)threadIdx.x, units - 1)];
     }
     // prologue kinds: the slice's source rows; wavefront w builds rows
     // m = w + 4r, lane l the 8-column groups l + 64j.  Up to 4 groups per lane
     // are loaded here, ahead of the weights, so their round trips overlap
     // (verify at M = 9: 3 groups; 186 -> 192 tok/s); larger slices go row by
     // row after them (8 preloaded groups cost occupancy: logits GEMM 24 -> 30 us).
-    constexpr int RW = PANEL ? 1 : (M + 3) / 4;
+    constexpr int RW = PANEL ? 1 : (M + NWV - 1) / NWV;
     constexpr int GL = PANEL ? 1 : (PPW * 8 + 63) / 64;
     constexpr bool PRELOAD = !PANEL && PRO != VX_PRO_ATTN && RW * GL <= 4;
     const int ng = np * 8, k0 = p0 * 64;
@@ -454,7 +476,7 @@ __global__ __launch_bounds__(256) void vx_gemm_kernel(vx_gemm_args a)
     if constexpr (PRELOAD) {
 #pragma unroll
         for (int rr = 0; rr < RW; rr++) {
-            const int m = wave + 4 * rr;
+            const int m = wave + NWV * rr;
             if (m >= M) continue;
 #pragma unroll
             for (int j = 0; j < GL; j++) {
@@ -485,7 +507,7 @@ __global__ __launch_bounds__(256) void vx_gemm_kernel(vx_gemm_args a)
     }
     if constexpr (PANEL) {
 #pragma unroll
-        for (int j = 0; j < UPT; j++) lds[j * 256 + threadIdx.x] = pv[j];
+        for (int j = 0; j < UPT; j++) lds[j * NT + threadIdx.x] = pv[j];
     } else if constexpr (PRO == VX_PRO_ATTN) {
         static_assert(M <= VX_PRO_ATTN_MAX_M && M * PPW * 16 <= 256, "ATTN slice columns exceed the workgroup");
         vx_pro_attn<M, PPW>(a.p, p0, np, lds, lrs);
@@ -493,7 +515,7 @@ __global__ __launch_bounds__(256) void vx_gemm_kernel(vx_gemm_args a)
         const bool lead = grp == 0;
 #pragma unroll
         for (int rr = 0; rr < RW; rr++) {
-            const int m = wave + 4 * rr;
+            const int m = wave + NWV * rr;
             if (m >= M) continue;
             const float rin = (PRO == VX_PRO_SWIGLU && a.p.ss_in) ? vx_rms_inv((float)a.p.ss_in[m], a.p.ss_K)
                                                                   : 1.0f;
@@ -724,7 +746,7 @@ __global__ __launch_bounds__(256) void vx_gemm_kernel(vx_gemm_args a)
         // drop this XCD's cached lines so that plain loads see the device-
         // scope sums (and the other workgroups' device-scope stores)
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-        vx_gemm_epilogue<EPI, M>(a, sg, lds, UPT * 256);
+        vx_gemm_epilogue<EPI, M>(a, sg, lds, UPT * NT);
     }
 }
 
@@ -738,12 +760,13 @@ static int vx_launch_ppw(const vxh_qmat *W, vx_gemm_args &a, hipStream_t st, hip
     if (PRO == VX_PRO_PANEL && a.rs_ld > 1 && a.rs_chunk % PPW)
         return vxh_fail(VXH_ERR_PARAM, "gemm: K slice of %d pairs crosses a %d-pair scale chunk", PPW,
                         a.rs_chunk);
-    const int groups = (a.n_tiles + 3) / 4;
+    constexpr int NWV = vx_nwv<QT, M, AVX2, PPW, EPI, PRO>::v;
+    const int groups = (a.n_tiles + NWV - 1) / NWV;
     if (e0 || e1)   // events recorded by the dispatch itself around the kernel
         hipExtLaunchKernelGGL(vx_gemm_kernel<QT, M, AVX2, PPW, EPI, PRO>, dim3(groups * a.n_splits),
-                              dim3(256), 0, st, e0, e1, 0, a);
+                              dim3(64 * NWV), 0, st, e0, e1, 0, a);
     else
-        vx_gemm_kernel<QT, M, AVX2, PPW, EPI, PRO><<<groups * a.n_splits, 256, 0, st>>>(a);
+        vx_gemm_kernel<QT, M, AVX2, PPW, EPI, PRO><<<groups * a.n_splits, 64 * NWV, 0, st>>>(a);
     VXH_LAUNCHED();
     return VXH_OK;
 }
