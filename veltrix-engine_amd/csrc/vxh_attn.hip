@@ -372,14 +372,17 @@ __device__ __forceinline__ float4 vx_keep4(bool ok, float4 v)
 // (KH = true, a flagged mode: round to nearest even on store, exact widening
 // on load).  i is an element index, a multiple of 4.
 template <bool KH>
-__device__ __forceinline__ float4 vx_kv_load4(const float *base, size_t i)
+__device__ __forceinline__ float4 vx_kv_load4(const float *base, uint32_t i)
 {
+    // a 32-bit byte offset from the (uniform) base: the load takes the
+    // scalar-base form, no 64-bit address arithmetic per lane
+    const char *p = (const char *)base + (uint32_t)(i * (KH ? 2u : 4u));
     if constexpr (KH) {
-        const uint2 h = *(const uint2 *)((const uint16_t *)base + i);
+        const uint2 h = *(const uint2 *)p;
         return make_float4(vx_half_bits_to_float(h.x & 0xFFFFu), vx_half_bits_to_float(h.x >> 16),
                            vx_half_bits_to_float(h.y & 0xFFFFu), vx_half_bits_to_float(h.y >> 16));
     } else {
-        return *(const float4 *)(base + i);
+        return *(const float4 *)p;
     }
 }
 __device__ __forceinline__ uint32_t vx_half_bits(float x)
@@ -445,21 +448,28 @@ __device__ __forceinline__ void vx_attention_mfma_body(
 
     // K rows of positions tc + 16 pg + n (dims 16 j + 4 r .. + 3) and V rows
     // of positions tc + 16 pg + 4 r + s (dims 64 u + 4 n .. + 3) of chunk tc
-    // from the cache; positions past the cache end read as zeros
+    // from the cache; positions past the cache end read as zeros (with one
+    // chunk per wavefront only a chunk that reaches past it -- wavefront-
+    // uniform -- runs the selects; a branch between a multi-chunk wavefront's
+    // loads would wait for the next chunk's K before this chunk's P.V).
+    // Offsets are 32-bit element indices from the layer's cache base.
     float4 kr[NPG][NJ], vr[NPG][4][NV4];
+    const uint32_t head0 = (uint32_t)(g * HD), ukvd = (uint32_t)kvd;
     auto load_k = [&](int tc) {
 #pragma unroll
         for (int pg = 0; pg < NPG; pg++) {
             const int pos = tc + 16 * pg + n;
-            const size_t off = (size_t)min(pos, n_ctx - 1) * kvd + g * HD + 4 * r;
+            const uint32_t off = (uint32_t)min(pos, n_ctx - 1) * ukvd + head0 + 4 * r;
 #pragma unroll
             for (int j = 0; j < NJ; j++) kr[pg][j] = vx_kv_load4<KH>(kc, off + 16 * j);
         }
+        if (NCW > 1 || tc + 16 * NPG > n_ctx) {
 #pragma unroll
-        for (int pg = 0; pg < NPG; pg++) {
-            const bool ok = tc + 16 * pg + n < n_ctx;
+            for (int pg = 0; pg < NPG; pg++) {
+                const bool ok = tc + 16 * pg + n < n_ctx;
 #pragma unroll
-            for (int j = 0; j < NJ; j++) kr[pg][j] = vx_keep4(ok, kr[pg][j]);
+                for (int j = 0; j < NJ; j++) kr[pg][j] = vx_keep4(ok, kr[pg][j]);
+            }
         }
     };
     auto load_v = [&](int tc) {
@@ -468,18 +478,20 @@ __device__ __forceinline__ void vx_attention_mfma_body(
 #pragma unroll
             for (int st = 0; st < 4; st++) {
                 const int pv = tc + 16 * pg + 4 * r + st;
-                const size_t ov = (size_t)min(pv, n_ctx - 1) * kvd + g * HD + 4 * n;
+                const uint32_t ov = (uint32_t)min(pv, n_ctx - 1) * ukvd + head0 + 4 * n;
 #pragma unroll
                 for (int u = 0; u < NV4; u++) vr[pg][st][u] = vx_kv_load4<KH>(vc, ov + 64 * u);
             }
+        if (NCW > 1 || tc + 16 * NPG > n_ctx) {
 #pragma unroll
-        for (int pg = 0; pg < NPG; pg++)
+            for (int pg = 0; pg < NPG; pg++)
 #pragma unroll
-            for (int st = 0; st < 4; st++) {
-                const bool okv = tc + 16 * pg + 4 * r + st < n_ctx;
+                for (int st = 0; st < 4; st++) {
+                    const bool okv = tc + 16 * pg + 4 * r + st < n_ctx;
 #pragma unroll
-                for (int u = 0; u < NV4; u++) vr[pg][st][u] = vx_keep4(okv, vr[pg][st][u]);
-            }
+                    for (int u = 0; u < NV4; u++) vr[pg][st][u] = vx_keep4(okv, vr[pg][st][u]);
+                }
+        }
     };
     load_k(t0);
     if constexpr (V_EARLY) load_v(t0);
