@@ -194,6 +194,10 @@ int vx_speculative_decode(vx_speculative_state *s, int *output, int max_tokens)
     dm->cache_len = n - 1;
     int draft_len = n - 1;   /* committed tokens held in the draft's KV cache */
     const int tctx = td->n_ctx_alloc, dctx = dd->n_ctx_alloc;
+    /* each draft forward writes its logits row straight into its slot of D
+     * (which the decision reads), so the sampler copies nothing; the draft's
+     * own buffer is put back below and on every exit */
+    float *const dlogits = dd->logits;
 
     for (int round = 0; generated < max_tokens; round++) {
         /* drafts this round: the round emits up to kk+1 tokens, and positions
@@ -214,15 +218,18 @@ int vx_speculative_decode(vx_speculative_state *s, int *output, int max_tokens)
             int pend = n - draft_len;
             if (pend < 1 || pend > VX_MAX_BATCH) goto done;
             CHK(vxh_upload(dd->tok, committed + draft_len, sizeof(int) * (size_t)pend, dd->stream));
+            dd->logits = s->D;
             CHKE(vx_dev_forward(dm, pend, draft_len, VX_LOGITS_LAST));
             draft_len = n;
             for (int i = 0; i < kk; i++) s->uh[i] = vx_uniform(s->seed, 1, (uint64_t)round * k + i);
             CHK(vxh_upload(s->u_draft, s->uh, sizeof(float) * (size_t)kk, dd->stream));
             for (int i = 0; i < kk; i++) {
+                dd->logits = s->D + (size_t)i * Vd;
                 if (i > 0) CHKE(vx_dev_forward_ids(dm, s->dtok + i, 1, n + i - 1, VX_LOGITS_LAST));
                 CHK(vxh_sample_keep(dd->logits, Vd, T, s->top_p, s->u_draft + i, s->dtok + 1 + i,
-                                    s->nuc + 8 * i, s->D + (size_t)i * Vd, dd->stream));
+                                    s->nuc + 8 * i, dd->logits, dd->stream));
             }
+            dd->logits = dlogits;
             CHK(vxh_stream_sync(dd->stream));
         }
         double tb = vx_now_ms();
@@ -275,6 +282,7 @@ int vx_speculative_decode(vx_speculative_state *s, int *output, int max_tokens)
         dm->cache_len = draft_len;
     }
 done:
+    dd->logits = dlogits;
     return generated;
 }
 
