@@ -1,7 +1,7 @@
 """GPU parity of the dequant GEMM / GEMV entry points against the oracle.
 
-Bar: |gpu - oracle| <= 1e-4 + 1e-3*|oracle| elementwise (floating point, the
-north-star tolerance); dequantisation and repacking are bit-exact.
+Bar: |gpu - oracle| <= 1e-4 + 1e-3*|oracle| elementwise (the floating-point
+tolerance of the verify path); dequantisation and repacking are bit-exact.
 """
 import ctypes as C
 
