@@ -89,6 +89,11 @@ typedef struct {
     int n_pairs;       /* ceil(K/64): block pairs per row                     */
     void *qs;          /* device                                              */
     void *d;           /* device                                              */
+    int cached;        /* 0: the GEMMs stream qs with non-temporal loads (the
+                        * default: a matrix read once per forward should not
+                        * evict what the next launches reuse); nonzero: plain
+                        * loads, so the matrix may stay in the caches between
+                        * forwards (vxh_qmat_alloc sets 0)                  */
 } vxh_qmat;
 
 int vxh_qmat_alloc(vxh_qmat *m, int type, int n_rows, int n_cols);

@@ -152,7 +152,7 @@ def test_gemm_zero_and_one_hot(P):
 
 class _QMat(C.Structure):
     _fields_ = [("type", C.c_int), ("n_rows", C.c_int), ("n_cols", C.c_int), ("n_pairs", C.c_int),
-                ("qs", C.c_void_p), ("d", C.c_void_p)]
+                ("qs", C.c_void_p), ("d", C.c_void_p), ("cached", C.c_int)]
 
 
 class _Panel(C.Structure):
@@ -214,3 +214,45 @@ def test_dot_path_matches_oracle(P, typ, rows, cols, M):
     ok, nfb = N.parity(Y, ref, exact)
     print(f"max |d| {np.abs(Y.astype(np.float64) - ref).max():.2e}; elements on the exact-value fallback: {nfb}")
     assert ok, N.max_violation(Y, ref)
+
+
+@pytest.mark.parametrize("typ,rows,cols,M", [(2, 2048, 5632, 1), (2, 4096, 4096, 9), (8, 1024, 4096, 9)])
+def test_cached_and_streamed_weights_agree(P, typ, rows, cols, M):
+    """vxh_qmat.cached = 1 (plain weight loads) against the default 0
+    (non-temporal loads): the same products, bit for bit."""
+    vp = C.c_void_p
+    L = N.bind_vxh(P)
+    L.vxh_qmat_alloc.argtypes = [vp, C.c_int, C.c_int, C.c_int]
+    L.vxh_qmat_set_rows.argtypes = [vp, vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, vp]
+    L.vxh_qmat_free.argtypes = [vp]
+    L.vxh_panel_alloc.argtypes = [vp, C.c_int, C.c_int]
+    L.vxh_panel_free.argtypes = [vp]
+    L.vxh_prep_panel.argtypes = [vp, vp, C.c_int, C.c_int, C.c_int, C.c_int, vp, C.c_int, vp]
+    L.vxh_gemm_acc.argtypes = [vp, vp, C.c_int, vp, C.c_int, C.c_int, C.c_float, vp, C.c_int, C.c_float, C.c_int, vp]
+    print(f"cached vs streamed {'Q4_0' if typ == 2 else 'Q8_0'} {rows}x{cols} M={M}", flush=True)
+    rng = np.random.default_rng(rows + cols + M + typ + 5)
+    W = N.rand_q4_0(rng, rows, cols) if typ == 2 else N.rand_q8_0(rng, rows, cols)
+    X = rng.normal(0, 1, (M, cols)).astype(np.float32)
+    q = _QMat()
+    assert L.vxh_qmat_alloc(C.byref(q), typ, rows, cols) == 0, L.vxh_last_error()
+    assert q.cached == 0
+    assert L.vxh_qmat_set_rows(C.byref(q), N._ptr(W), 0, rows, rows, 0, 0, None) == 0, L.vxh_last_error()
+    pan = _Panel()
+    assert L.vxh_panel_alloc(C.byref(pan), M, cols) == 0
+    dx = N.DevBuf(L, X)
+    accs = [N.DevBuf(L, np.zeros(M * rows, np.float64)) for _ in range(2)]
+    try:
+        assert L.vxh_prep_panel(C.byref(pan), dx.ptr, cols, M, cols, 0, None, 0, None) == 0
+        for cached, acc in zip((0, 1), accs):
+            q.cached = cached
+            assert L.vxh_gemm_acc(C.byref(q), C.byref(pan), M, acc.ptr, rows, rows, 1.0, None, 0, 0.0, 0,
+                                  None) == 0, L.vxh_last_error()
+        assert L.vxh_stream_sync(None) == 0
+        got = [a.get(np.float64, M * rows) for a in accs]
+    finally:
+        for b in [dx] + accs:
+            b.free()
+        L.vxh_panel_free(C.byref(pan))
+        L.vxh_qmat_free(C.byref(q))
+    assert np.any(got[0] != 0.0)
+    assert np.array_equal(got[0], got[1])

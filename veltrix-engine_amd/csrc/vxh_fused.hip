@@ -384,6 +384,7 @@ extern "C" int vxh_gemm_fused(const vxh_qmat *W, const vxh_xpanel *X, int M, dou
     vx_gemm_args a;
     memset(&a, 0, sizeof(a));
     a.wq = (const uint4 *)W->qs;
+    a.wcache = W->cached;
     a.wd = (const uint32_t *)W->d;
     a.panel = (const uint4 *)X->data;
     a.rscale = X->rs;

@@ -175,6 +175,7 @@ struct vx_gemm_args {
     const double *ss;
     int ss_K;
     int n_tiles, n_pairs, n_splits;
+    int wcache;             // weights with plain loads (else non-temporal)
     double *acc;
     int ld_acc;
     int n_out;
@@ -392,6 +393,15 @@ __device__ __forceinline__ void vx_pro_attn(const vx_pro_args &p, int p0, int np
 
 #define VX_RING 4
 
+// A weight load: non-temporal unless the matrix is marked to stay cached.
+__device__ __forceinline__ uint4 vx_load_w(const uint4 *p, int cached)
+{
+    if (cached) return *p;
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 v = __builtin_nontemporal_load((const u32x4 *)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // Wavefronts (tiles) per workgroup: 8 for the residual prologue of Q4_0
 // verify batches at 8-pair slices (every workgroup rebuilds its K slice of
 // the panel from x, the fp64 pending sums and the norm weight; 8 tiles per
@@ -502,7 +512,7 @@ __global__ __launch_bounds__((64 * vx_nwv<QT, M, AVX2, PPW, EPI, PRO>::v)) void 
     for (int i = 0; i < VX_RING; i++) {
         const int pi = min(i, np - 1);
 #pragma unroll
-        for (int q = 0; q < WPP; q++) w[i][q] = wp[((size_t)pi * WPP + q) * 64];
+        for (int q = 0; q < WPP; q++) w[i][q] = vx_load_w(wp + ((size_t)pi * WPP + q) * 64, a.wcache);
         sc[i] = sp[(size_t)pi * 32];
     }
     if constexpr (PANEL) {
@@ -585,7 +595,7 @@ __global__ __launch_bounds__((64 * vx_nwv<QT, M, AVX2, PPW, EPI, PRO>::v)) void 
         if (i + VX_RING < PPW) {
             const int pi = min(i + VX_RING, np - 1);
 #pragma unroll
-            for (int q = 0; q < WPP; q++) w[i % VX_RING][q] = wp[((size_t)pi * WPP + q) * 64];
+            for (int q = 0; q < WPP; q++) w[i % VX_RING][q] = vx_load_w(wp + ((size_t)pi * WPP + q) * 64, a.wcache);
             sc[i % VX_RING] = sp[(size_t)pi * 32];
         }
         if (DUAL && i < np) {

@@ -78,6 +78,7 @@ extern "C" int vxh_gemm_pro(const vxh_qmat *W, int M, const vxh_pro *p, double *
     vx_gemm_args a;
     memset(&a, 0, sizeof(a));
     a.wq = (const uint4 *)W->qs;
+    a.wcache = W->cached;
     a.wd = (const uint32_t *)W->d;
     a.rs_ld = 1;
     a.rs_chunk = 1 << 30;
