@@ -371,18 +371,27 @@ __device__ __forceinline__ float4 vx_keep4(bool ok, float4 v)
 // KV cache rows in fp32 (KH = false, the reference's cache) or IEEE fp16
 // (KH = true, a flagged mode: round to nearest even on store, exact widening
 // on load).  i is an element index, a multiple of 4.
-template <bool KH>
+// nt: a non-temporal load (a cache too large to stay in the caches between
+// forwards should not evict what does).
+template <bool KH, bool NT>
 __device__ __forceinline__ float4 vx_kv_load4(const float *base, uint32_t i)
 {
     // a 32-bit byte offset from the (uniform) base: the load takes the
     // scalar-base form, no 64-bit address arithmetic per lane
     const char *p = (const char *)base + (uint32_t)(i * (KH ? 2u : 4u));
     if constexpr (KH) {
-        const uint2 h = *(const uint2 *)p;
+        typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+        u32x2 h;
+        if constexpr (NT) h = __builtin_nontemporal_load((const u32x2 *)p);
+        else h = *(const u32x2 *)p;
         return make_float4(vx_half_bits_to_float(h.x & 0xFFFFu), vx_half_bits_to_float(h.x >> 16),
                            vx_half_bits_to_float(h.y & 0xFFFFu), vx_half_bits_to_float(h.y >> 16));
     } else {
-        return *(const float4 *)p;
+        typedef float f32x4 __attribute__((ext_vector_type(4)));
+        f32x4 v;
+        if constexpr (NT) v = __builtin_nontemporal_load((const f32x4 *)p);
+        else v = *(const f32x4 *)p;
+        return make_float4(v.x, v.y, v.z, v.w);
     }
 }
 __device__ __forceinline__ uint32_t vx_half_bits(float x)
@@ -409,7 +418,7 @@ __device__ __forceinline__ void vx_kv_store4(float *base, size_t i, float4 v)
         *(float4 *)(base + i) = v;
 }
 
-template <bool QKV, int HD, bool KH = false, int NCW = 1, int NPG = 2, bool MERGE = false>
+template <bool QKV, int HD, bool KH = false, int NCW = 1, int NPG = 2, bool MERGE = false, bool NT = false>
 __device__ __forceinline__ void vx_attention_mfma_body(
     const float *__restrict__ q, int M, int n_past, int n_ctx, int n_heads, int n_kv, int cap,
     float *__restrict__ kc, float *__restrict__ vc, int n_chunks, int n_chunks_w, int n_qg,
@@ -461,7 +470,7 @@ __device__ __forceinline__ void vx_attention_mfma_body(
             const int pos = tc + 16 * pg + n;
             const uint32_t off = (uint32_t)min(pos, n_ctx - 1) * ukvd + head0 + 4 * r;
 #pragma unroll
-            for (int j = 0; j < NJ; j++) kr[pg][j] = vx_kv_load4<KH>(kc, off + 16 * j);
+            for (int j = 0; j < NJ; j++) kr[pg][j] = vx_kv_load4<KH, NT>(kc, off + 16 * j);
         }
         if (NCW > 1 || tc + 16 * NPG > n_ctx) {
 #pragma unroll
@@ -480,7 +489,7 @@ __device__ __forceinline__ void vx_attention_mfma_body(
                 const int pv = tc + 16 * pg + 4 * r + st;
                 const uint32_t ov = (uint32_t)min(pv, n_ctx - 1) * ukvd + head0 + 4 * n;
 #pragma unroll
-                for (int u = 0; u < NV4; u++) vr[pg][st][u] = vx_kv_load4<KH>(vc, ov + 64 * u);
+                for (int u = 0; u < NV4; u++) vr[pg][st][u] = vx_kv_load4<KH, NT>(vc, ov + 64 * u);
             }
         if (NCW > 1 || tc + 16 * NPG > n_ctx) {
 #pragma unroll
@@ -820,25 +829,25 @@ static void vx_att_geom(int head_dim, bool qkv, int *wch, bool *merge)
     }
 }
 
-template <int HD>
+template <int HD, bool NT = false>
 __global__ __launch_bounds__(ATT_THREADS) __attribute__((amdgpu_waves_per_eu(3))) void vx_attention_mfma_kernel(
     const float *__restrict__ q, int M, int n_past, int n_ctx, int n_heads, int n_kv, int cap,
     float *__restrict__ kc, float *__restrict__ vc, int n_chunks, int n_chunks_w, int n_qg,
     float *__restrict__ part, vx_qkv_args qa)
 {
     using C = vx_att_cfg<HD, false>;
-    vx_attention_mfma_body<false, HD, false, C::NCW, C::NPG, C::MERGE>(
+    vx_attention_mfma_body<false, HD, false, C::NCW, C::NPG, C::MERGE, NT>(
         q, M, n_past, n_ctx, n_heads, n_kv, cap, kc, vc, n_chunks, n_chunks_w, n_qg, part, qa);
 }
 
-template <int HD, bool KH = false>
+template <int HD, bool KH = false, bool NT = false>
 __global__ __launch_bounds__(ATT_THREADS) __attribute__((amdgpu_waves_per_eu(3))) void vx_attention_mfma_qkv_kernel(
     const float *__restrict__ q, int M, int n_past, int n_ctx, int n_heads, int n_kv, int cap,
     float *__restrict__ kc, float *__restrict__ vc, int n_chunks, int n_chunks_w, int n_qg,
     float *__restrict__ part, vx_qkv_args qa)
 {
     using C = vx_att_cfg<HD, true>;
-    vx_attention_mfma_body<true, HD, KH, C::NCW, C::NPG, C::MERGE>(
+    vx_attention_mfma_body<true, HD, KH, C::NCW, C::NPG, C::MERGE, NT>(
         q, M, n_past, n_ctx, n_heads, n_kv, cap, kc, vc, n_chunks, n_chunks_w, n_qg, part, qa);
 }
 
@@ -1026,6 +1035,36 @@ extern "C" size_t vxh_attention_workspace_floats(int M, int n_ctx, int cap, int 
 
 // parts_only: the first launch alone; the partials stay in ws->part for a
 // consumer that combines them itself (*n_chunks_out chunks per query).
+#define VX_KV_STREAM_BYTES (16.0 * 1024 * 1024)
+
+// The fp32-MFMA kernels for a head size, cache precision and q source (q
+// rows, or the q|k|v sums of A when qkv is set).
+template <bool NT>
+static void vx_attention_mfma_launch(const float *q, bool qkv, const vx_qkv_args &A, int M, int n_past, int n_ctx,
+                                     int n_heads, int n_kv_heads, int head_dim, int cap, float *kc, float *vc,
+                                     int n_chunks, int n_chunks_w, int nqg, int grid, float *part, int kv_half,
+                                     vxh_stream s)
+{
+    if (kv_half && head_dim == 64)
+        vx_attention_mfma_qkv_kernel<64, true, NT><<<grid, ATT_THREADS, 0, vxh_hs(s)>>>(
+            nullptr, M, n_past, n_ctx, n_heads, n_kv_heads, cap, kc, vc, n_chunks, n_chunks_w, nqg, part, A);
+    else if (kv_half)
+        vx_attention_mfma_qkv_kernel<128, true, NT><<<grid, ATT_THREADS, 0, vxh_hs(s)>>>(
+            nullptr, M, n_past, n_ctx, n_heads, n_kv_heads, cap, kc, vc, n_chunks, n_chunks_w, nqg, part, A);
+    else if (head_dim == 64 && qkv)
+        vx_attention_mfma_qkv_kernel<64, false, NT><<<grid, ATT_THREADS, 0, vxh_hs(s)>>>(
+            nullptr, M, n_past, n_ctx, n_heads, n_kv_heads, cap, kc, vc, n_chunks, n_chunks_w, nqg, part, A);
+    else if (head_dim == 64)
+        vx_attention_mfma_kernel<64, NT><<<grid, ATT_THREADS, 0, vxh_hs(s)>>>(
+            q, M, n_past, n_ctx, n_heads, n_kv_heads, cap, kc, vc, n_chunks, n_chunks_w, nqg, part, A);
+    else if (qkv)
+        vx_attention_mfma_qkv_kernel<128, false, NT><<<grid, ATT_THREADS, 0, vxh_hs(s)>>>(
+            nullptr, M, n_past, n_ctx, n_heads, n_kv_heads, cap, kc, vc, n_chunks, n_chunks_w, nqg, part, A);
+    else
+        vx_attention_mfma_kernel<128, NT><<<grid, ATT_THREADS, 0, vxh_hs(s)>>>(
+            q, M, n_past, n_ctx, n_heads, n_kv_heads, cap, kc, vc, n_chunks, n_chunks_w, nqg, part, A);
+}
+
 static int vx_attention_run(const float *q, const vx_qkv_args *qa, long n_clr, int M, int n_past,
                             int n_ctx, int n_heads, int n_kv_heads, int head_dim, int cap, float *kc,
                             float *vc, float *out, int ld_out, vxh_workspace *ws,
@@ -1067,30 +1106,16 @@ static int vx_attention_run(const float *q, const vx_qkv_args *qa, long n_clr, i
         const int nqg = (QM + 15) / 16, ncg = (nw_w + 3) / 4;
         const int grid = n_kv_heads * nqg * ncg;
         const vx_qkv_args &A = qa ? *qa : none;
-        if (kv_half && head_dim == 64)
-            vx_attention_mfma_qkv_kernel<64, true><<<grid, ATT_THREADS, 0, vxh_hs(s)>>>(
-                nullptr, M, n_past, n_ctx, n_heads, n_kv_heads, cap, kc, vc, n_chunks, n_chunks_w, nqg,
-                ws->part, A);
-        else if (kv_half)
-            vx_attention_mfma_qkv_kernel<128, true><<<grid, ATT_THREADS, 0, vxh_hs(s)>>>(
-                nullptr, M, n_past, n_ctx, n_heads, n_kv_heads, cap, kc, vc, n_chunks, n_chunks_w, nqg,
-                ws->part, A);
-        else if (head_dim == 64 && qa)
-            vx_attention_mfma_qkv_kernel<64><<<grid, ATT_THREADS, 0, vxh_hs(s)>>>(
-                nullptr, M, n_past, n_ctx, n_heads, n_kv_heads, cap, kc, vc, n_chunks, n_chunks_w, nqg,
-                ws->part, A);
-        else if (head_dim == 64)
-            vx_attention_mfma_kernel<64><<<grid, ATT_THREADS, 0, vxh_hs(s)>>>(
-                q, M, n_past, n_ctx, n_heads, n_kv_heads, cap, kc, vc, n_chunks, n_chunks_w, nqg,
-                ws->part, A);
-        else if (qa)
-            vx_attention_mfma_qkv_kernel<128><<<grid, ATT_THREADS, 0, vxh_hs(s)>>>(
-                nullptr, M, n_past, n_ctx, n_heads, n_kv_heads, cap, kc, vc, n_chunks, n_chunks_w, nqg,
-                ws->part, A);
+        // a layer's attended cache beyond VX_KV_STREAM_BYTES streams with
+        // non-temporal loads (a 7B target's 2048-position rows: 64 MB; a 1B
+        // draft's: 4 MB)
+        const bool nt = 2.0 * ctx * n_kv_heads * head_dim * (kv_half ? 2 : 4) > VX_KV_STREAM_BYTES;
+        if (nt)
+            vx_attention_mfma_launch<true>(q, qa != nullptr, A, M, n_past, n_ctx, n_heads, n_kv_heads, head_dim, cap, kc, vc,
+                                           n_chunks, n_chunks_w, nqg, grid, ws->part, kv_half, s);
         else
-            vx_attention_mfma_kernel<128><<<grid, ATT_THREADS, 0, vxh_hs(s)>>>(
-                q, M, n_past, n_ctx, n_heads, n_kv_heads, cap, kc, vc, n_chunks, n_chunks_w, nqg,
-                ws->part, A);
+            vx_attention_mfma_launch<false>(q, qa != nullptr, A, M, n_past, n_ctx, n_heads, n_kv_heads, head_dim, cap, kc, vc,
+                                            n_chunks, n_chunks_w, nqg, grid, ws->part, kv_half, s);
     } else if (qa)
         vx_attention_kernel<true><<<n_kv_heads * n_chunks_w * n_qg, ATT_THREADS, lds, vxh_hs(s)>>>(
             nullptr, M, n_past, n_ctx, n_heads, n_kv_heads, head_dim, cap, kc, vc, n_chunks, n_chunks_w,
