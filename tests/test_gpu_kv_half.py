@@ -37,9 +37,13 @@ def set_kv_half(P, mp, on, **over):
     return P.vx_model_set_options(mp, C.byref(opt))
 
 
-@pytest.mark.parametrize("d,h,kv", [(256, 4, 2), (512, 4, 2)])
-def test_kv_half_verify_matches_oracle(P, d, h, kv):
-    L, F, V, n_ctx, n_past, k = 2, 512, 512, 256, 100, 4
+@pytest.mark.parametrize("d,h,kv,L,n_ctx,n_past", [
+    (256, 4, 2, 2, 256, 100), (512, 4, 2, 2, 256, 100),
+    # a layer's cache beyond 16 MB is read with non-temporal loads (the
+    # streamed instantiations of the fp16-cache kernels): head_dim 128, 64
+    (2048, 16, 16, 1, 2304, 2100), (2048, 32, 32, 1, 2304, 2100)])
+def test_kv_half_verify_matches_oracle(P, d, h, kv, L, n_ctx, n_past):
+    F, V, k = 512, 512, 4
     hd = d // h
     kvd = kv * hd
     print(f"kv_half verify: d{d} {h}/{kv} heads (head_dim {hd}), {n_past} prefilled, k={k}", flush=True)

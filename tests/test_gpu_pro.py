@@ -375,6 +375,8 @@ def bind_attention(P):
     (8, 8, 128, 9, 300, 512, 4096, True),        # verify batch with biases
     (4, 2, 64, 1, 130, 120, 4096, False),        # past the context: row clamped to n_ctx - 1
     (8, 2, 32, 5, 70, 256, 40, True),            # attention cap below the positions
+    (32, 32, 128, 9, 2100, 2304, 4096, False),   # verify-sized cache (69 MB): non-temporal cache loads
+    (32, 32, 64, 1, 2100, 2304, 4096, False),    # the same at head_dim 64 (34 MB)
 ])
 def test_attention_qkv_matches_rope_then_attention(P, H, KV, hd, M, n_past, n_ctx, cap, bias):
     """vxh_attention_qkv against vxh_rope_kv_norm followed by vxh_attention on
@@ -528,6 +530,7 @@ def test_pro_attn_combines_partials(P, H, KV, hd, M, typ):
     (8, 8, 128, 16, 100, 512, 4096),      # 16 query vectors per kv head
     (16, 2, 32, 3, 90, 256, 4096),        # head_dim 32: 32-position chunks
     (8, 2, 128, 64, 300, 512, 200),       # prompt-prefill batch: 64 rows, cap inside a two-chunk wavefront
+    (32, 32, 64, 2, 2100, 2304, 4096),    # 34 MB of cache rows: read with non-temporal loads
 ])
 def test_attention_matches_reference(P, H, KV, hd, M, n_past, n_ctx, cap):
     """vxh_attention against softmax attention in float64 on the same cache

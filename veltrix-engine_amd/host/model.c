@@ -560,8 +560,13 @@ vx_error vx_model_create_synthetic(const vx_model_config *cfg, const vx_synth_sp
     {
         vx_dev *d = vx_dev_of(m);
         const int dd = d->d, kvd = d->kvd, F = d->F, V = d->V;
-        size_t big = (size_t)V * dd;
-        if ((size_t)F * dd > big) big = (size_t)F * dd;
+        /* the staging buffer holds the largest matrix synthesised through it:
+         * rows V, d, kvd or F (embedding/output, q and attn_o, k/v, gate/up)
+         * of d columns, or d rows of F columns (down) */
+        int rmax = V > dd ? V : dd;
+        if (kvd > rmax) rmax = kvd;
+        if (F > rmax) rmax = F;
+        size_t big = (size_t)rmax * dd;
         void *stage = NULL;
         int rc = vxh_malloc(&stage, big / 32 * 34);
         if (rc) { e = vx_from_vxh(rc); goto fail; }
