@@ -266,7 +266,7 @@ def set_mode(g, fused, thr, max_rows=16):
     assert g.P.vx_model_set_options(g.mp, C.byref(opt)) == 0
 
 
-@pytest.mark.parametrize("shape,thr", [("small", 0.01), ("d2048", 0.0)])
+@pytest.mark.parametrize("shape,thr", [("small", 0.01), ("d2048", 0.0), ("narrow_ffn", 0.01)])
 def test_pro_forward_matches_separate_and_oracle(P, tmp_path, shape, thr):
     """Verify batches of 9, 16 and 1 rows after a prefix, on the prologue path
     (fused = 2) and the separate-kernel path (fused = 0).  The d=2048 model
@@ -275,6 +275,9 @@ def test_pro_forward_matches_separate_and_oracle(P, tmp_path, shape, thr):
     the sums flips them; the default threshold is covered by the small model."""
     if shape == "small":
         dims = dict(L=2, d=128, h=4, kv=2, ff=256, V=300)
+    elif shape == "narrow_ffn":
+        # FFN and vocabulary both narrower than the model width
+        dims = dict(L=2, d=1024, h=8, kv=2, ff=256, V=300)
     else:
         dims = dict(L=2, d=2048, h=16, kv=4, ff=5632, V=1000)
     print(f"prologue forward {shape} thr {thr}", flush=True)
