@@ -277,7 +277,8 @@ __device__ __forceinline__ void vx_pro_values(const vx_pro_args &p, const vx_pro
 // head, lane d4) and every S-th chunk from t / U (S = 256 / U slices); the
 // slices merge in LDS.
 // chunks of partials whose loads one thread issues together (one round trip
-// per batch; 12 covers a 3072-position draft context at 8 slices)
+// per batch; with one partial per 64 positions, 12 cover a 6144-position
+// draft context at 8 slices)
 #define VX_CMB_BATCH 12
 
 template <int M, int PPW>
