@@ -1033,8 +1033,8 @@ extern "C" size_t vxh_attention_workspace_floats(int M, int n_ctx, int cap, int 
     return (size_t)n_kv_heads * n_chunks * (n_heads / n_kv_heads) * M * PART_STRIDE(head_dim);
 }
 
-// parts_only: the first launch alone; the partials stay in ws->part for a
-// consumer that combines them itself (*n_chunks_out chunks per query).
+// a layer's attended cache rows beyond this many bytes are read with
+// non-temporal loads
 #define VX_KV_STREAM_BYTES (16.0 * 1024 * 1024)
 
 // The fp32-MFMA kernels for a head size, cache precision and q source (q
@@ -1065,6 +1065,8 @@ static void vx_attention_mfma_launch(const float *q, bool qkv, const vx_qkv_args
             q, M, n_past, n_ctx, n_heads, n_kv_heads, cap, kc, vc, n_chunks, n_chunks_w, nqg, part, A);
 }
 
+// parts_only: the first launch alone; the partials stay in ws->part for a
+// consumer that combines them itself (*n_chunks_out chunks per query).
 static int vx_attention_run(const float *q, const vx_qkv_args *qa, long n_clr, int M, int n_past,
                             int n_ctx, int n_heads, int n_kv_heads, int head_dim, int cap, float *kc,
                             float *vc, float *out, int ld_out, vxh_workspace *ws,
