@@ -402,7 +402,8 @@ class _Panel(C.Structure):
 
 class _QMat(C.Structure):
     _fields_ = [("type", C.c_int), ("n_rows", C.c_int), ("n_cols", C.c_int), ("n_pairs", C.c_int),
-                ("qs", C.c_void_p), ("d", C.c_void_p), ("cached", C.c_int)]
+                ("qs", C.c_void_p), ("d", C.c_void_p), ("cached", C.c_int),
+                ("tq", C.c_void_p), ("td", C.c_void_p)]
 
 
 class _Pro(C.Structure):

@@ -64,9 +64,10 @@ typedef struct {
 } vx_model_options;
 
 #define VX_FUSED_NONE 0        /* separate row kernels (11 launches per layer)          */
-#define VX_FUSED_EPILOGUE 1    /* in the last workgroups of the producing GEMM (6)      */
 #define VX_FUSED_PROLOGUE 2    /* in the consuming GEMM, which builds its own input
-                                  panel slice; RMSNorm applied to the product (7)      */
+                                  panel slice; RMSNorm applied to the product (7).
+                                  Value 1 (row work in the producing GEMM's last
+                                  workgroups) was removed and is refused            */
 
 void vx_model_get_options(const vx_model *model, vx_model_options *opt);
 vx_error vx_model_set_options(vx_model *model, const vx_model_options *opt);

@@ -81,7 +81,18 @@ int vxh_graph_destroy(vxh_graph g);
  *
  *   F32   qs: [row][n_pairs * 64] fp32, zero past n_cols and the logical rows;
  *             d unused.  GEMMs read it through vxh_gemm_acc only (exact,
- *             non-AVX2 panels); gathers copy rows unscaled. */
+ *             non-AVX2 panels); gathers copy rows unscaled.
+ *
+ * Q4_0 and Q8_0 matrices also hold a copy in 64-row tiles for the GEMMs of
+ * 5..16 rows (the weights are the B operand of a 16x16x32 MFMA, one block
+ * per weight row and instruction); nb = n_cols/32 blocks, lane l = 16G + n:
+ *   Q4_0  tq: [tile][block][lane 64][4 dwords]  dword g = bytes 4G..4G+3 of
+ *             the block of row 64 tile + 16g + n (nibbles permuted as above).
+ *   Q8_0  tq: [tile][block][half j][lane 64][4 dwords]  dwords 2c, 2c+1 =
+ *             bytes 8G..8G+7 of row 64 tile + 16(2j + c) + n (permuted).
+ *   both  td: [tile][block][n 16][g 4] fp16 scale of row 64 tile + 16g + n.
+ * Rows past n_rows read as zeros; the copy adds 18 (34) bytes per 32 weights
+ * (HBM is not the constraint: 288 GB per MI355X). */
 typedef struct {
     int type;          /* 2 = Q4_0, 8 = Q8_0, 0 = F32 (vx_type / GGML ids)  */
     int n_rows;        /* physical rows, a multiple of 32                     */
@@ -93,7 +104,10 @@ typedef struct {
                         * default: a matrix read once per forward should not
                         * evict what the next launches reuse); nonzero: plain
                         * loads, so the matrix may stay in the caches between
-                        * forwards (vxh_qmat_alloc sets 0)                  */
+                        * forwards (vxh_qmat_alloc sets 0; the 64-row copy is
+                        * always streamed)                                  */
+    void *tq;          /* device, 64-row tiled copy (Q4_0/Q8_0; NULL for F32) */
+    void *td;          /* device                                              */
 } vxh_qmat;
 
 int vxh_qmat_alloc(vxh_qmat *m, int type, int n_rows, int n_cols);
@@ -316,66 +330,6 @@ int vxh_gemm_pro(const vxh_qmat *W, int M, const vxh_pro *p, double *acc, int ld
 int vxh_acc_store_norm(double *acc, int ld_acc, int M, int n, float *y, int ldy, const double *ss,
                        int ss_K, vxh_stream s);
 
-/* ---- fused forward path ---------------------------------------------------------
- * The same GEMM with the follow-up elementwise work of the reference's
- * forward (src/model.c:514-594) run inside it: the last workgroup to finish
- * each group of VXH_CHUNK output columns reads the final sums, writes the
- * results, clears the accumulator and resets its counter.
- *
- * Inputs are "x-panels": panel units as vxh_panel (M rows) whose K columns
- * are split in chunks of VXH_CHUNK, each chunk scaled by its own power of two;
- * rs[m * rs_ld + c] is the output scale of chunk c of row m (rs_ld = 1: one
- * scale per row).  RMSNorm is applied after the product: a panel holding
- * w .* x with ss[m] = sum x^2 gives W (w .* x) / sqrt(ss[m]/K + 1e-5), equal
- * to the GEMM of the reference's normalised row w .* (x / rms)
- * (src/tensor.c:128-142) up to rounding.  ss = NULL: no normalisation. */
-#define VXH_CHUNK 1024
-typedef struct {
-    void *data;        /* device, vxh_panel_bytes(M, K); padding reads as zeros */
-    float *rs;         /* device, [16][rs_ld]                                   */
-    int rs_ld;         /* chunks per row, (K + VXH_CHUNK - 1) / VXH_CHUNK        */
-    double *ss;        /* device [M] sum of squares (producers add into it) or NULL */
-    int M, K;
-} vxh_xpanel;
-
-int vxh_xpanel_alloc(vxh_xpanel *p, int max_M, int K);
-int vxh_xpanel_free(vxh_xpanel *p);
-/* Panel of w .* x[m] (norm_w NULL = ones) with per-chunk scales; adds
- * sum x[m]^2 into p->ss[m] when p->ss != NULL. */
-int vxh_rows_xpanel(const float *x, int ldx, int M, int K, const float *norm_w, vxh_xpanel *p,
-                    vxh_stream s);
-
-enum {
-    VXH_FEPI_STORE = 1,   /* y[m][n] = out (last_row_only: row M-1 only, as row 0)      */
-    VXH_FEPI_RESID = 2,   /* x[m][n] += out, then out_panel = w .* x, out_panel->ss += x^2 */
-    VXH_FEPI_SWIGLU = 3,  /* h = SwiGLU of the 16-row interleaved gate/up output
-                             (src/model.c:582-585, gate-skip threshold thr) -> out_panel  */
-    VXH_FEPI_ROPE = 4,    /* q | k | v output -> RoPE, q_out and the KV cache (as vxh_rope_kv) */
-};
-typedef struct {
-    int kind;
-    unsigned *counters;   /* device, n_counters words, zero before the call and after it:
-                             64 words (one 256-byte line) per super-group of VXH_CHUNK
-                             output columns (2 VXH_CHUNK for SWIGLU) and per 128 rows   */
-    int n_counters;
-    vxh_xpanel *out_panel;/* RESID, SWIGLU: the next GEMM's input (K = n_out or n_h)     */
-    const float *norm_w;  /* RESID: weight of the next RMSNorm (NULL = ones)             */
-    float *x; int ldx;    /* RESID: residual rows                                        */
-    float *y; int ldy;    /* STORE: output rows                                          */
-    int last_row_only;    /* STORE                                                       */
-    float *h; int ldh;    /* SWIGLU: h rows [M][ldh == n_h] (written; the panel's source) */
-    int n_h;              /* SWIGLU: F                                                   */
-    float thr;            /* SWIGLU: gate-skip threshold                                 */
-    int n_past, n_ctx, n_pos, n_heads, n_kv_heads, head_dim;   /* ROPE, as vxh_rope_kv   */
-    const float *bq, *bk, *bv, *cos_tab, *sin_tab;
-    float *q_out, *k_cache, *v_cache;
-} vxh_fepi;
-/* acc[M][ld_acc] must be zero (it is again on return); ld_acc >= n_out rounded up
- * to 32; n_out % 32 == 0 except for STORE. */
-int vxh_gemm_fused(const vxh_qmat *W, const vxh_xpanel *X, int M, double *acc, int ld_acc,
-                   int n_out, float scale, const vxh_fepi *e, vxh_event start, vxh_event stop,
-                   vxh_stream s);
-
 /* ---- prompt prefill at large M ---------------------------------------------------
  * The reference runs a prompt one token per forward (src/speculative.c:100-107,
  * src/model.c:450-616); these run a chunk of prompt rows as one batch.
@@ -480,16 +434,6 @@ int vxh_attention_parts_qkv_f16(double *qkv, int ld_qkv, const double *ss, int s
                                 int n_heads, int n_kv_heads, int head_dim, int cap,
                                 uint16_t *k_cache_layer, uint16_t *v_cache_layer, vxh_workspace *ws,
                                 int *n_chunks, vxh_stream s);
-
-/* vxh_attention whose second launch also builds the output projection's
- * x-panel p (K = n_heads * head_dim, one scale per row): the last head of
- * each row to finish reads the row back and writes its panel.  row_counters:
- * 64 * M device words (one counter per 256-byte line), zero before the call
- * and after it. */
-int vxh_attention_xpanel(const float *q, int M, int n_past, int n_ctx, int n_heads, int n_kv_heads,
-                         int head_dim, int cap, const float *k_cache_layer,
-                         const float *v_cache_layer, float *out, int ld_out, vxh_workspace *ws,
-                         unsigned *row_counters, vxh_xpanel *p, vxh_stream s);
 
 size_t vxh_attention_workspace_floats(int M, int n_ctx, int cap, int n_heads, int n_kv_heads,
                                       int head_dim);

@@ -18,7 +18,7 @@ import _native as N  # noqa: E402
 
 # C type -> members whose offsets are checked (all of them)
 STRUCTS = {
-    "vxh_qmat": ["type", "n_rows", "n_cols", "n_pairs", "qs", "d", "cached"],
+    "vxh_qmat": ["type", "n_rows", "n_cols", "n_pairs", "qs", "d", "cached", "tq", "td"],
     "vxh_panel": ["data", "corr", "rscale", "xs", "M", "K", "avx2", "rs_ld"],
     "vxh_workspace": ["acc", "acc_elems", "part", "part_floats"],
     "vxh_pro": ["kind", "x", "ldx", "src", "ld_src", "w", "x_out", "ld_xout", "ss", "ss_in", "ss_K", "thr",

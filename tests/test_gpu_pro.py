@@ -30,7 +30,8 @@ PRO_ROWS, PRO_RESID, PRO_SWIGLU, PRO_ATTN = 1, 2, 3, 4
 
 class Qmat(C.Structure):
     _fields_ = [("type", C.c_int), ("n_rows", C.c_int), ("n_cols", C.c_int), ("n_pairs", C.c_int),
-                ("qs", vp), ("d", vp), ("cached", C.c_int)]
+                ("qs", vp), ("d", vp), ("cached", C.c_int),
+                ("tq", vp), ("td", vp)]
 
 
 class Pro(C.Structure):

@@ -21,7 +21,8 @@ class Panel(C.Structure):
 
 class QMat(C.Structure):
     _fields_ = [("type", C.c_int), ("n_rows", C.c_int), ("n_cols", C.c_int), ("n_pairs", C.c_int),
-                ("qs", vp), ("d", vp), ("cached", C.c_int)]
+                ("qs", vp), ("d", vp), ("cached", C.c_int),
+                ("tq", vp), ("td", vp)]
 
 
 class Epi(C.Structure):

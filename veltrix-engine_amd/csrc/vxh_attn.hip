@@ -860,58 +860,9 @@ __global__ __launch_bounds__(ATT_THREADS) __attribute__((amdgpu_waves_per_eu(3))
 #define CMB_THREADS 256
 #define CMB_BATCH 12   // chunks whose loads a thread issues together (one round trip per batch)
 
-// Panel of row m of att (XP variant): the last head of the row to finish
-// reads the row back (after an agent-scope acquire) and writes its fp16 hi/lo
-// panel with one power-of-two scale (every chunk entry of the row).
-__device__ void vx_att_row_panel(const float *att, int d, int M, int m, uint4 *pan, float *rs,
-                                 int rs_ld)
-{
-    __shared__ float red[CMB_THREADS / 64];
-    __shared__ float s_in;
-    float am = 0.0f;
-    for (int c = 8 * threadIdx.x; c < d; c += 8 * CMB_THREADS)
-        for (int k = 0; k < 8; k++)
-            am = fmaxf(am, fabsf(att[c + k]));
-    am = vx_wave_max64(am);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = am;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        float a = red[0];
-        for (int i = 1; i < CMB_THREADS / 64; i++) a = fmaxf(a, red[i]);
-        float si = 1.0f, so = 1.0f;
-        if (a > 0.0f && isfinite(a)) {
-            int ex;
-            frexpf(a, &ex);
-            si = ldexpf(1.0f, 14 - ex);
-            so = ldexpf(1.0f, ex - 14);
-        }
-        for (int c = 0; c < rs_ld; c++) rs[m * rs_ld + c] = so;
-        s_in = si;
-    }
-    __syncthreads();
-    const float sc = s_in;
-    for (int c = 8 * threadIdx.x; c < d; c += 8 * CMB_THREADS) {
-        float v[8];
-        for (int k = 0; k < 8; k++)
-            v[k] = att[c + k] * sc;
-        vx_half8 hi, lo;
-        for (int k = 0; k < 8; k++) {
-            _Float16 a = (_Float16)v[k];
-            hi[k] = a;
-            lo[k] = (_Float16)(v[k] - (float)a);
-        }
-        const int g = c / 8, b = g >> 2, h = (g >> 1) & 1, s = g & 1;
-        const size_t base = ((size_t)(b * 2 + s) * 2 + h) * (2 * M);
-        pan[base + m] = __builtin_bit_cast(uint4, hi);
-        pan[base + M + m] = __builtin_bit_cast(uint4, lo);
-    }
-}
-
-template <bool XP>
 __global__ __launch_bounds__(CMB_THREADS) void vx_attention_combine_kernel(
     const float *__restrict__ part, int M, int n_heads, int n_kv, int hd, int n_chunks,
-    float *__restrict__ out, int ld_out, unsigned *cnt, uint4 *pan, float *rs, int rs_ld,
-    double *clr, long n_clr)
+    float *__restrict__ out, int ld_out, double *clr, long n_clr)
 {
     __shared__ float4 s_acc[CMB_THREADS];
     if (clr) {
@@ -981,34 +932,7 @@ __global__ __launch_bounds__(CMB_THREADS) void vx_attention_combine_kernel(
         }
         const float inv = 1.0f / (lt + 1e-10f);
         float *o = out + (size_t)m * ld_out + (size_t)head * hd + 4 * d4;
-        if (XP) {
-            // written through to device scope: the row's last head reads it
-            __hip_atomic_store(o + 0, at.x * inv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(o + 1, at.y * inv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(o + 2, at.z * inv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(o + 3, at.w * inv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        } else {
-            *(float4 *)o = make_float4(at.x * inv, at.y * inv, at.z * inv, at.w * inv);
-        }
-    }
-    if constexpr (XP) {
-        __shared__ int s_last;
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            // one counter per 256-byte line
-            unsigned *c = cnt + (size_t)m * 64;
-            // acquire-release: publishes this head's rows, sees the other heads'
-            const unsigned old = __hip_atomic_fetch_add(c, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-            s_last = old + 1 == (unsigned)n_heads;
-            if (s_last) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        __syncthreads();
-        if (s_last) {
-            // drop stale cached lines: the other heads wrote through to device scope
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-            vx_att_row_panel(out + (size_t)m * ld_out, n_heads * hd, M, m, pan, rs, rs_ld);
-        }
+        *(float4 *)o = make_float4(at.x * inv, at.y * inv, at.z * inv, at.w * inv);
     }
 }
 
@@ -1070,7 +994,7 @@ static void vx_attention_mfma_launch(const float *q, bool qkv, const vx_qkv_args
 static int vx_attention_run(const float *q, const vx_qkv_args *qa, long n_clr, int M, int n_past,
                             int n_ctx, int n_heads, int n_kv_heads, int head_dim, int cap, float *kc,
                             float *vc, float *out, int ld_out, vxh_workspace *ws,
-                            unsigned *row_counters, vxh_xpanel *xp, int parts_only, int *n_chunks_out,
+                            int parts_only, int *n_chunks_out,
                             vxh_stream s, int kv_half = 0)
 {
     if (kv_half && (!qa || (head_dim != 64 && head_dim != 128) || M > VX_ATT_MFMA_MAX_M))
@@ -1138,14 +1062,8 @@ static int vx_attention_run(const float *q, const vx_qkv_args *qa, long n_clr, i
     if (n_chunks_out) *n_chunks_out = n_chunks;
     if (parts_only) return VXH_OK;
     double *clr = qa ? (double *)qa->qkv : nullptr;
-    if (xp)
-        vx_attention_combine_kernel<true><<<M * n_heads, CMB_THREADS, 0, vxh_hs(s)>>>(
-            ws->part, M, n_heads, n_kv_heads, head_dim, n_chunks, out, ld_out, row_counters,
-            (uint4 *)xp->data, xp->rs, xp->rs_ld, clr, n_clr);
-    else
-        vx_attention_combine_kernel<false><<<M * n_heads, CMB_THREADS, 0, vxh_hs(s)>>>(
-            ws->part, M, n_heads, n_kv_heads, head_dim, n_chunks, out, ld_out, nullptr, nullptr,
-            nullptr, 0, clr, n_clr);
+    vx_attention_combine_kernel<<<M * n_heads, CMB_THREADS, 0, vxh_hs(s)>>>(
+        ws->part, M, n_heads, n_kv_heads, head_dim, n_chunks, out, ld_out, clr, n_clr);
     VXH_LAUNCHED();
     return VXH_OK;
 }
@@ -1156,7 +1074,7 @@ extern "C" int vxh_attention(const float *q, int M, int n_past, int n_ctx, int n
                              vxh_stream s)
 {
     return vx_attention_run(q, nullptr, 0, M, n_past, n_ctx, n_heads, n_kv_heads, head_dim, cap,
-                            (float *)kc, (float *)vc, out, ld_out, ws, nullptr, nullptr, 0, nullptr, s);
+                            (float *)kc, (float *)vc, out, ld_out, ws, 0, nullptr, s);
 }
 
 static int vx_attention_qkv(double *qkv, int ld_qkv, const double *ss, int ss_K, const float *bq,
@@ -1184,7 +1102,7 @@ static int vx_attention_qkv(double *qkv, int ld_qkv, const double *ss, int ss_K,
     qa.cs = cos_tab;
     qa.sn = sin_tab;
     return vx_attention_run(nullptr, &qa, (long)M * ld_qkv, M, n_past, n_ctx, n_heads, n_kv_heads,
-                            head_dim, cap, kc, vc, out, ld_out, ws, nullptr, nullptr, n_chunks_out != nullptr,
+                            head_dim, cap, kc, vc, out, ld_out, ws, n_chunks_out != nullptr,
                             n_chunks_out, s, kv_half);
 }
 
@@ -1234,19 +1152,6 @@ extern "C" int vxh_attention_parts_qkv_f16(double *qkv, int ld_qkv, const double
     return vx_attention_qkv(qkv, ld_qkv, ss, ss_K, bq, bk, bv, cos_tab, sin_tab, n_pos, M, n_past, n_ctx,
                             n_heads, n_kv_heads, head_dim, cap, (float *)kc, (float *)vc, nullptr, 0, ws,
                             n_chunks, s, 1);
-}
-
-extern "C" int vxh_attention_xpanel(const float *q, int M, int n_past, int n_ctx, int n_heads,
-                                    int n_kv_heads, int head_dim, int cap, const float *kc,
-                                    const float *vc, float *out, int ld_out, vxh_workspace *ws,
-                                    unsigned *row_counters, vxh_xpanel *p, vxh_stream s)
-{
-    if (!p || !row_counters || p->K != n_heads * head_dim)
-        return vxh_fail(VXH_ERR_PARAM, "attention_xpanel: panel K %d, need %d", p ? p->K : -1,
-                        n_heads * head_dim);
-    p->M = M;
-    return vx_attention_run(q, nullptr, 0, M, n_past, n_ctx, n_heads, n_kv_heads, head_dim, cap,
-                            (float *)kc, (float *)vc, out, ld_out, ws, row_counters, p, 0, nullptr, s);
 }
 
 __global__ void vx_add_rows_kernel(float *__restrict__ y, int ldy, const float *__restrict__ x,

@@ -817,7 +817,7 @@ extern "C" int vxh_gemm_acc_timed(const vxh_qmat *W, const vxh_panel *X, int M, 
         return vx_f32_dispatch(W, M, a, vxh_hs(s), (hipEvent_t)start, (hipEvent_t)stop);
     }
     if (path == VXH_PATH_DOT) return vx_dot_dispatch(W, M, a, vxh_hs(s), (hipEvent_t)start, (hipEvent_t)stop);
-    return vx_dispatch<VX_EPI_NONE>(W, M, X->avx2, a, vxh_hs(s), (hipEvent_t)start, (hipEvent_t)stop);
+    return vx_dispatch<>(W, M, X->avx2, a, vxh_hs(s), (hipEvent_t)start, (hipEvent_t)stop);
 }
 
 extern "C" int vxh_gemm_acc(const vxh_qmat *W, const vxh_panel *X, int M, double *acc, int ld_acc,

@@ -1,8 +1,7 @@
 // Shared device code of the skinny-M dequant GEMM: operand unpacking, the
-// MFMA kernel template and its launchers, and the row helpers the panel
-// producers use.  Included by vxh_gemm.hip (plain GEMM), vxh_fused.hip
-// (GEMM with a fused epilogue) and vxh_pro_*.hip (GEMM that builds its own
-// panel slice).
+// MFMA kernel templates and their launchers, and the row helpers the panel
+// producers use.  Included by vxh_gemm.hip (plain GEMM) and vxh_pro*.hip
+// (GEMM that builds its own panel slice).
 #pragma once
 
 #include <string.h>
@@ -108,33 +107,7 @@ struct vx_ppw_set {
     static constexpr int target = 1600;
 };
 
-// Fused-epilogue arguments (vxh_fused.hip): the last workgroup to finish a
-// super-group of output rows runs the epilogue on its final sums.
-enum { VX_EPI_NONE = 0, VX_EPI_STORE = 1, VX_EPI_RESID = 2, VX_EPI_SWIGLU = 3, VX_EPI_ROPE = 4 };
-#define VX_CHUNK 1024   // panel columns per power-of-two scale chunk (fused path, SwiGLU panel)
-
-#define VX_CNT_STRIDE 64   // words between arrival counters (256 bytes)
-
-struct vx_epi_args {
-    unsigned *cnt;          // arrival counters, VX_CNT_STRIDE words apart (zero between
-                            // launches): n_sg super-groups, then one per tile group
-    int n_sg;
-    int sg_groups;          // workgroup tile groups (4 tiles) per super-group
-    uint4 *pan;             // RESID, SWIGLU: panel written for the next GEMM
-    float *pan_rs;          // [M][pan_rs_ld] output scales of its chunks
-    int pan_rs_ld;
-    const float *w;         // RESID: weight of the next RMSNorm (NULL = ones)
-    double *ss;             // RESID: [M] sum of squares of the updated rows
-    float *x;               // RESID: residual rows; STORE: output rows
-    int ldx;
-    float *h;               // SWIGLU: optional fp32 copy of h
-    int ldh;
-    float thr;              // SWIGLU gate threshold
-    int last_only;          // STORE: only row M-1, written as row 0
-    int n_past, n_ctx, n_heads, n_kv, hd;   // ROPE
-    const float *bq, *bk, *bv, *cs, *sn;
-    float *q_out, *kc, *vc;
-};
+#define VX_CHUNK 1024   // panel columns per power-of-two scale chunk (SwiGLU panel)
 
 // Prologue kinds (vxh_pro*.hip): instead of reading a panel that a row kernel
 // wrote, the workgroup builds its own K slice of the panel from the rows the
@@ -183,13 +156,12 @@ struct vx_gemm_args {
     const float *gate;
     int ld_gate;
     float thr;
-    vx_epi_args e;
     vx_pro_args p;
+    // verify-batch kernel (vx_vg_kernel): the 64-row tiled copy of the matrix
+    const void *tq, *td;
+    uint32_t tq_bytes, td_bytes, pan_bytes;
+    int n_t64, n_blk;
 };
-
-// Defined in vxh_fused.hip for EPI != VX_EPI_NONE.
-template <int EPI, int M>
-__device__ void vx_gemm_epilogue(const vx_gemm_args &a, int sg, uint4 *lds, int lds_units);
 
 // ---------------------------------------------------------------------------
 // prologue kinds: building the panel slice in the GEMM
@@ -409,27 +381,26 @@ __device__ __forceinline__ uint4 vx_load_w(const uint4 *p, int cached)
 // workgroup halve those rebuilds: 22016x4096 at M = 9 20.6 -> 18.6 us,
 // 12288x4096 13.2 -> 12.8 us), 4 otherwise (Q8_0 11008x4096 15.2 -> 16.7 us
 // and the 16-pair logits GEMM 26.7 -> 27.5 us with 8).
-template <int QT, int M, bool AVX2, int PPW, int EPI, int PRO>
+template <int QT, int M, bool AVX2, int PPW, int PRO>
 struct vx_nwv {
     static constexpr int v =
-        PRO == VX_PRO_RESID && QT == 2 && M >= 5 && PPW == 8 && EPI == VX_EPI_NONE && !AVX2 ? 8 : 4;
+        PRO == VX_PRO_RESID && QT == 2 && M >= 5 && PPW == 8 && !AVX2 ? 8 : 4;
 };
 
 // QT: 2 = Q4_0, 8 = Q8_0.
-template <int QT, int M, bool AVX2, int PPW, int EPI = VX_EPI_NONE, int PRO = VX_PRO_PANEL>
-__global__ __launch_bounds__((64 * vx_nwv<QT, M, AVX2, PPW, EPI, PRO>::v)) void vx_gemm_kernel(vx_gemm_args a)
+template <int QT, int M, bool AVX2, int PPW, int PRO = VX_PRO_PANEL>
+__global__ __launch_bounds__((64 * vx_nwv<QT, M, AVX2, PPW, PRO>::v)) void vx_gemm_kernel(vx_gemm_args a)
 {
-    constexpr int NWV = vx_nwv<QT, M, AVX2, PPW, EPI, PRO>::v;   // wavefronts, one tile each
+    constexpr int NWV = vx_nwv<QT, M, AVX2, PPW, PRO>::v;   // wavefronts, one tile each
     constexpr int NT = 64 * NWV;                          // threads
-    static_assert(NWV == 4 || (EPI == VX_EPI_NONE && !AVX2 && PRO != VX_PRO_ATTN),
-                  "epilogues, AVX2 corrections and the attention prologue assume 4 wavefronts");
+    static_assert(NWV == 4 || (!AVX2 && PRO != VX_PRO_ATTN),
+                  "AVX2 corrections and the attention prologue assume 4 wavefronts");
     // With 8 wavefronts per workgroup the compiler may give a wavefront at
     // most 256 registers and, seeing no AGPR use, selects the VGPR-destination
     // MFMA form, whose destinations it overlaps with their own A/B sources
     // (results have been wrong with that form here).  An AGPR clobber keeps
     // the AGPR-destination form.
     if constexpr (NWV > 4) asm volatile("" ::: "a0");
-    static_assert(EPI == VX_EPI_NONE || PRO == VX_PRO_PANEL, "fused epilogues read panels");
     static_assert(!AVX2 || PRO == VX_PRO_PANEL, "AVX2-lane corrections come with panels");
     constexpr bool PANEL = PRO == VX_PRO_PANEL;
     constexpr int NS = vx_mcfg<M>::NS;
@@ -721,47 +692,419 @@ __global__ __launch_bounds__((64 * vx_nwv<QT, M, AVX2, PPW, EPI, PRO>::v)) void 
                                    __HIP_MEMORY_SCOPE_AGENT);
         }
     }
-    if constexpr (EPI != VX_EPI_NONE) {
-        // Last arriver of the super-group, counted in two levels so that few
-        // workgroups meet on one counter: every wave waits for its own
-        // atomics to complete (they are performed at device scope), one
-        // thread counts the workgroup into its tile group (n_splits
-        // arrivals); the last of those counts the tile group into the
-        // super-group.  Both counts are acquire-release at agent scope, so
-        // each arrival releases its workgroup's sums and the last one, with
-        // the acquire fence below, sees every partial sum of the super-group
-        // under the memory model (not only through write-through caches).
-        // Counters sit VX_CNT_STRIDE words apart (one per 256-byte line) and
-        // are reset by their last arriver.
-        __shared__ int s_last;
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        const int sg = grp / a.e.sg_groups;
-        if (threadIdx.x == 0) {
-            const int n_groups = (a.n_tiles + 3) / 4;
-            unsigned *c1 = a.e.cnt + (size_t)(a.e.n_sg + grp) * VX_CNT_STRIDE;
-            int last = __hip_atomic_fetch_add(c1, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) + 1 ==
-                       (unsigned)a.n_splits;
-            if (last) {
-                __hip_atomic_store(c1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                unsigned *c2 = a.e.cnt + (size_t)sg * VX_CNT_STRIDE;
-                const int groups = min(a.e.sg_groups, n_groups - sg * a.e.sg_groups);
-                last = __hip_atomic_fetch_add(c2, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) + 1 ==
-                       (unsigned)groups;
-                if (last) __hip_atomic_store(c2, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------------------
+// Verify-batch GEMM (M = 5..16): v_mfma_f32_16x16x32_f16 on 64-row tiles
+// ---------------------------------------------------------------------------
+// The weights are the B operand: one MFMA multiplies the 16 activation slots
+// (the rows' fp16 hi parts; a second MFMA chains the lo parts into the same
+// accumulator) by 16 weight rows x one whole Q4_0/Q8_0 block (K = 32), so the
+// four results a lane holds (activation rows 4G..4G+3 of one weight row) all
+// take the scale of one block: 16 scale FMAs per 64 rows and block, and the
+// MFMA results land in VGPRs (no accumulator-register reads).  Weights come
+// from the matrix's 64-row tiled copy (vxh_qmat.tq/td) through buffer loads
+// whose per-block offset is wave-uniform.
+//
+// Workgroup = NT tiles x NK consecutive K ranges of KB blocks, one wavefront
+// each.  Its panel slice (NK*KB blocks, the vx_gemm_kernel LDS layout) is
+// staged in LDS -- copied from a panel or built by a prologue kind -- except
+// for a plain panel with one tile per workgroup, whose wavefronts read their
+// slice from HBM with the weights.  Each wavefront scales its sums, waves
+// along K add theirs in LDS in wave order, and the workgroup adds the total
+// into the fp64 accumulator (one atomic per output and workgroup).
+
+// MFMA sources stay live past the MFMAs of a block: a VGPR-destination MFMA
+// whose destination overlaps its own A/B registers computes wrong values,
+// and the compiler reuses a source that dies at the MFMA as its destination
+// unless something reads the source afterwards.  The asm also reads the
+// results, so it cannot move above the MFMAs.
+#define VX_MFMA_KEEP4(D0, D1, D2, D3, A0, A1, B0, B1, B2, B3)                                   \
+    asm volatile("" : "+v"(D0), "+v"(D1), "+v"(D2), "+v"(D3)                                  \
+                 : "v"(A0), "v"(A1), "v"(B0), "v"(B1), "v"(B2), "v"(B3))
+
+typedef float vx_f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int vx_u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int vx_u32x2 __attribute__((ext_vector_type(2)));
+
+// vx_unpack_q4 with the high-nibble offset held in a register (a literal
+// operand is re-materialised per block)
+__device__ __forceinline__ vx_half8 vx_unpack_q4r(uint32_t q, uint32_t magic, uint32_t off16w)
+{
+    const uint32_t q8 = q >> 8;
+    vx_half2 a = __builtin_bit_cast(vx_half2, vx_and_or(q, 0x000F000Fu, magic));
+    vx_half2 b = __builtin_bit_cast(vx_half2, vx_and_or(q, 0x00F000F0u, magic));
+    vx_half2 c = __builtin_bit_cast(vx_half2, vx_and_or(q8, 0x000F000Fu, magic));
+    vx_half2 d = __builtin_bit_cast(vx_half2, vx_and_or(q8, 0x00F000F0u, magic));
+    const vx_half2 off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+    const vx_half2 sc = {(_Float16)0.0625f, (_Float16)0.0625f};
+    const vx_half2 off16 = __builtin_bit_cast(vx_half2, off16w);
+    a = a + off;
+    b = b * sc + off16;
+    c = c + off;
+    d = d * sc + off16;
+    vx_half8 r = {a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
+    return r;
+}
+
+template <int QT, int M, int NT, int NK, int KB, int RING, int PRO>
+__global__ __launch_bounds__(64 * NT * NK) __attribute__((amdgpu_waves_per_eu(2))) void vx_vg_kernel(vx_gemm_args a)
+{
+    static_assert(M >= 2 && M <= 16 && KB % 2 == 0 && RING >= 1 && RING <= KB, "vg: shape");
+    static_assert(PRO == VX_PRO_PANEL || PRO == VX_PRO_ROWS || PRO == VX_PRO_RESID || PRO == VX_PRO_SWIGLU,
+                  "vg: prologue kind");
+    constexpr int NW = NT * NK, NTH = 64 * NW;
+    constexpr bool PANEL = PRO == VX_PRO_PANEL;
+    constexpr bool ALDS = !(PANEL && NT == 1);   // slice staged in LDS
+    constexpr int NS = 2 * M;
+    constexpr int PPW = NK * KB / 2;             // block pairs of the workgroup's K range
+    constexpr int UNITS = PPW * 8 * NS;
+    constexpr int UPT = ALDS ? (UNITS + NTH - 1) / NTH : 1;
+    constexpr int WPB = QT == 2 ? 1 : 2;         // 16-byte weight loads per lane and block
+    __shared__ uint4 lds[ALDS ? UPT * NTH : 1];
+    __shared__ float lrs[PANEL ? 1 : M];
+    __shared__ float red[NK > 1 ? (NK - 1) * NT * 16 * 64 : 1];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int t = wave % NT, kq = wave / NT;
+    const int tg = blockIdx.x / a.n_splits, split = blockIdx.x % a.n_splits;
+    const int tile = tg * NT + t;
+    const bool tile_ok = tile < a.n_t64;
+    const int tc = tile_ok ? tile : a.n_t64 - 1;
+    const int p0 = split * PPW;
+    const int np = min(PPW, a.n_pairs - p0);
+    const int wb0 = 2 * p0 + kq * KB;                  // this wavefront's first block
+    const int nbk = max(0, min(KB, a.n_blk - wb0));     // and its block count
+    const int bcl = min(wb0, a.n_blk - 1);
+    const int nbl = max(nbk, 1);
+    const int G = lane >> 4, mrow = min(lane & 15, M - 1);
+    uint32_t magic, off16;
+    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
+    asm volatile("v_mov_b32 %0, 0xd480d480" : "=v"(off16));   // -72 (fp16) twice
+
+    // 0. prologue kinds: this workgroup's share of the accumulator to clear
+    if constexpr (!PANEL) {
+        if (a.p.clr) {
+            const long per = (a.p.n_clr + gridDim.x - 1) / gridDim.x;
+            const long b = (long)blockIdx.x * per, e = min(b + per, a.p.n_clr);
+            for (long i = b + threadIdx.x; i < e; i += NTH) a.p.clr[i] = 0.0;
+        }
+    }
+    // 1. the slice's panel units or source rows, ahead of the weights
+    const int units = np * 8 * NS;
+    uint4 pv[PANEL && ALDS ? UPT : 1];
+    if constexpr (PANEL && ALDS) {
+        const uint4 *psrc = a.panel + (size_t)p0 * 8 * NS;
+#pragma unroll
+        for (int j = 0; j < UPT; j++) pv[j] = psrc[min(j * NTH + (int)threadIdx.x, units - 1)];
+    }
+    constexpr int RW = PANEL ? 1 : (M + NW - 1) / NW;
+    constexpr int GL = PANEL ? 1 : (PPW * 8 + 63) / 64;
+    constexpr bool PRELOAD = !PANEL && RW * GL <= 4;
+    const int ng = np * 8, k0 = p0 * 64;
+    vx_pro_raw raw[PRELOAD ? RW : 1][PRELOAD ? GL : 1];
+    if constexpr (PRELOAD) {
+#pragma unroll
+        for (int rr = 0; rr < RW; rr++) {
+            const int m = wave + NW * rr;
+            if (m >= M) continue;
+#pragma unroll
+            for (int j = 0; j < GL; j++) {
+                const int g = lane + 64 * j;
+                if (g < ng && k0 + 8 * g < a.p.K) vx_pro_load<PRO>(a.p, m, k0 + 8 * g, raw[rr][j]);
             }
-            s_last = last;
+        }
+    }
+    // 2. the first RING blocks of weights and scales (and of the slice when
+    // it is read from HBM)
+    const __amdgpu_buffer_rsrc_t rwq = __builtin_amdgcn_make_buffer_rsrc((void *)a.tq, (short)0, (int)a.tq_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rwd = __builtin_amdgcn_make_buffer_rsrc((void *)a.td, (short)0, (int)a.td_bytes, 0x00020000);
+    const uint32_t wbase = ((uint32_t)tc * a.n_blk + bcl) * (1024u * WPB);
+    const uint32_t sbase = ((uint32_t)tc * a.n_blk + bcl) * 128u;
+    const uint32_t wlo = lane * 16u, slo = (lane & 15) * 8u;
+    const int cpol = a.wcache ? 0 : 2;   // nt unless the matrix is marked cached
+    uint4 w[RING][WPB];
+    uint2 sc[RING];
+    uint4 arh[ALDS ? 1 : RING], arl[ALDS ? 1 : RING];
+    const __amdgpu_buffer_rsrc_t rpa = __builtin_amdgcn_make_buffer_rsrc((void *)a.panel, (short)0, (int)a.pan_bytes, 0x00020000);
+    const uint32_t alo = ((((G & 1) * 2 + (G >> 1)) * NS) + mrow) * 16u;
+    const uint32_t abase = (uint32_t)bcl * 4u * NS * 16u;
+#define VX_VG_WLD(bi, q)                                                                                   \
+    ({                                                                                                     \
+        const vx_u32x4 v_ = cpol ? __builtin_amdgcn_raw_buffer_load_b128(rwq, wlo, wbase + (uint32_t)(bi) * (1024u * WPB) + (q) * 1024u, 2) \
+                                 : __builtin_amdgcn_raw_buffer_load_b128(rwq, wlo, wbase + (uint32_t)(bi) * (1024u * WPB) + (q) * 1024u, 0); \
+        make_uint4(v_.x, v_.y, v_.z, v_.w);                                                                \
+    })
+#define VX_VG_SLD(bi)                                                                                      \
+    ({                                                                                                     \
+        const vx_u32x2 v_ = __builtin_amdgcn_raw_buffer_load_b64(rwd, slo, sbase + (uint32_t)(bi) * 128u, 0); \
+        make_uint2(v_.x, v_.y);                                                                            \
+    })
+#define VX_VG_ALD(bi, hl)                                                                                  \
+    ({                                                                                                     \
+        const vx_u32x4 v_ = __builtin_amdgcn_raw_buffer_load_b128(rpa, alo, abase + (uint32_t)(bi) * 4u * NS * 16u + (hl) * M * 16u, 0); \
+        make_uint4(v_.x, v_.y, v_.z, v_.w);                                                                \
+    })
+#pragma unroll
+    for (int i = 0; i < RING; i++) {
+        const int bi = min(i, nbl - 1);
+#pragma unroll
+        for (int q = 0; q < WPB; q++) w[i][q] = VX_VG_WLD(bi, q);
+        sc[i] = VX_VG_SLD(bi);
+        if constexpr (!ALDS) {
+            arh[i] = VX_VG_ALD(bi, 0);
+            arl[i] = VX_VG_ALD(bi, 1);
+        }
+    }
+    // 3. the LDS slice
+    if constexpr (ALDS) {
+        if constexpr (PANEL) {
+#pragma unroll
+            for (int j = 0; j < UPT; j++) lds[j * NTH + threadIdx.x] = pv[j];
+        } else {
+            const bool lead = tg == 0;
+#pragma unroll
+            for (int rr = 0; rr < RW; rr++) {
+                const int m = wave + NW * rr;
+                if (m >= M) continue;
+                const float rin = (PRO == VX_PRO_SWIGLU && a.p.ss_in) ? vx_rms_inv((float)a.p.ss_in[m], a.p.ss_K)
+                                                                      : 1.0f;
+                float v[GL][8];
+                float ss = 0.0f, amax = 0.0f;
+#pragma unroll
+                for (int j = 0; j < GL; j++) {
+                    const int g = lane + 64 * j, e0 = k0 + 8 * g;
+#pragma unroll
+                    for (int kk = 0; kk < 8; kk++) v[j][kk] = 0.0f;
+                    if (g < ng && e0 < a.p.K) {
+                        vx_pro_raw r;
+                        if constexpr (PRELOAD) r = raw[rr][j];
+                        else vx_pro_load<PRO>(a.p, m, e0, r);
+                        float *xo = (lead && a.p.x_out) ? a.p.x_out + (size_t)m * a.p.ld_xout + e0 : nullptr;
+                        vx_pro_values<PRO>(a.p, r, rin, xo, v[j], ss);
+                    }
+#pragma unroll
+                    for (int kk = 0; kk < 8; kk++) amax = fmaxf(amax, fabsf(v[j][kk]));
+                }
+                amax = vx_wave_max64(amax);
+                float rs;
+                const float scl = vx_row_scale(amax, &rs);
+                if (lane == 0) lrs[m] = rs;
+                if (PRO != VX_PRO_SWIGLU && lead && a.p.ss) {
+                    ss = vx_wave_sum64(ss);
+                    if (lane == 0)
+                        __hip_atomic_fetch_add(&a.p.ss[m], (double)ss, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+#pragma unroll
+                for (int j = 0; j < GL; j++) {
+                    const int g = lane + 64 * j;
+                    if (g >= ng) continue;
+                    vx_half8 hi, lo;
+#pragma unroll
+                    for (int kk = 0; kk < 8; kk++) {
+                        const float xv = v[j][kk] * scl;
+                        const _Float16 th = (_Float16)xv;
+                        hi[kk] = th;
+                        lo[kk] = (_Float16)(xv - (float)th);
+                    }
+                    const int b = g >> 2, h2 = (g >> 1) & 1, s2 = g & 1;
+                    const int base = ((b * 2 + s2) * 2 + h2) * NS;
+                    lds[base + m] = __builtin_bit_cast(uint4, hi);
+                    lds[base + M + m] = __builtin_bit_cast(uint4, lo);
+                }
+            }
         }
         __syncthreads();
-        if (!s_last) return;
-        // drop this XCD's cached lines so that plain loads see the device-
-        // scope sums (and the other workgroups' device-scope stores)
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-        vx_gemm_epilogue<EPI, M>(a, sg, lds, UPT * NT);
+    }
+
+    // 4. the K range: per block 4 (Q4_0) or 8 (Q8_0) dwords of weights unpack
+    // into the four row groups' B operands, eight MFMAs, sixteen scale FMAs
+    vx_f32x4 acc[4];
+#pragma unroll
+    for (int rg = 0; rg < 4; rg++) acc[rg] = vx_f32x4{0.f, 0.f, 0.f, 0.f};
+    const vx_f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+    const int lsel = ((G & 1) * 2 + (G >> 1)) * NS + mrow;
+#pragma unroll
+    for (int i = 0; i < KB; i++) {
+        uint4 wv[WPB];
+#pragma unroll
+        for (int q = 0; q < WPB; q++) wv[q] = w[i % RING][q];
+        const uint2 sv = sc[i % RING];
+        uint4 ahv, alv;
+        if constexpr (ALDS) {
+            const int u = (kq * KB + i) * 4 * NS + lsel;
+            ahv = lds[u];
+            alv = lds[u + M];
+        } else {
+            ahv = arh[i % RING];
+            alv = arl[i % RING];
+        }
+        if (i + RING < KB) {
+            const int bi = min(i + RING, nbl - 1);
+#pragma unroll
+            for (int q = 0; q < WPB; q++) w[i % RING][q] = VX_VG_WLD(bi, q);
+            sc[i % RING] = VX_VG_SLD(bi);
+            if constexpr (!ALDS) {
+                arh[i % RING] = VX_VG_ALD(bi, 0);
+                arl[i % RING] = VX_VG_ALD(bi, 1);
+            }
+        }
+        if (i < nbk) {
+            const vx_half8 A0 = __builtin_bit_cast(vx_half8, ahv);
+            const vx_half8 A1 = __builtin_bit_cast(vx_half8, alv);
+            vx_half8 B0, B1, B2, B3;
+            if constexpr (QT == 2) {
+                B0 = vx_unpack_q4r(wv[0].x, magic, off16);
+                B1 = vx_unpack_q4r(wv[0].y, magic, off16);
+                B2 = vx_unpack_q4r(wv[0].z, magic, off16);
+                B3 = vx_unpack_q4r(wv[0].w, magic, off16);
+            } else {
+                B0 = vx_unpack_q8(wv[0].x, wv[0].y, magic);
+                B1 = vx_unpack_q8(wv[0].z, wv[0].w, magic);
+                B2 = vx_unpack_q8(wv[WPB - 1].x, wv[WPB - 1].y, magic);
+                B3 = vx_unpack_q8(wv[WPB - 1].z, wv[WPB - 1].w, magic);
+            }
+            vx_f32x4 D0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, B0, zero4, 0, 0, 0);
+            vx_f32x4 D1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, B1, zero4, 0, 0, 0);
+            vx_f32x4 D2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, B2, zero4, 0, 0, 0);
+            vx_f32x4 D3 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0, B3, zero4, 0, 0, 0);
+            D0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, B0, D0, 0, 0, 0);
+            D1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, B1, D1, 0, 0, 0);
+            D2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, B2, D2, 0, 0, 0);
+            D3 = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1, B3, D3, 0, 0, 0);
+            VX_MFMA_KEEP4(D0, D1, D2, D3, A0, A1, B0, B1, B2, B3);
+            const float d0 = vx_half_bits_to_float(sv.x & 0xFFFFu);
+            const float d1 = vx_half_bits_to_float(sv.x >> 16);
+            const float d2 = vx_half_bits_to_float(sv.y & 0xFFFFu);
+            const float d3 = vx_half_bits_to_float(sv.y >> 16);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                acc[0][r] = fmaf(d0, D0[r], acc[0][r]);
+                acc[1][r] = fmaf(d1, D1[r], acc[1][r]);
+                acc[2][r] = fmaf(d2, D2[r], acc[2][r]);
+                acc[3][r] = fmaf(d3, D3[r], acc[3][r]);
+            }
+        }
+    }
+#undef VX_VG_WLD
+#undef VX_VG_SLD
+#undef VX_VG_ALD
+
+    // 5. output scale of each row (the slice's power of two, the synthetic
+    // scale, the deferred norm), the sum along K, the fp64 add.  A K range
+    // lies inside one panel scale chunk (checked by the launcher).
+    const int chunk = (bcl / 2) / a.rs_chunk;
+    float osc[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int mr = min(4 * G + r, M - 1);
+        osc[r] = (PANEL ? a.rscale[mr * a.rs_ld + chunk] : lrs[mr]) * a.scale;
+    }
+    if (a.ss) {
+        double ssv[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) ssv[r] = a.ss[min(4 * G + r, M - 1)];
+#pragma unroll
+        for (int r = 0; r < 4; r++) osc[r] *= vx_rms_inv((float)ssv[r], a.ss_K);
+    }
+#pragma unroll
+    for (int rg = 0; rg < 4; rg++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[rg][r] *= osc[r];
+    if constexpr (NK > 1) {
+        if (kq > 0) {
+#pragma unroll
+            for (int rg = 0; rg < 4; rg++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) red[(((kq - 1) * NT + t) * 16 + rg * 4 + r) * 64 + lane] = acc[rg][r];
+        }
+        __syncthreads();
+        if (kq != 0) return;
+#pragma unroll
+        for (int q = 1; q < NK; q++)
+#pragma unroll
+            for (int rg = 0; rg < 4; rg++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) acc[rg][r] += red[(((q - 1) * NT + t) * 16 + rg * 4 + r) * 64 + lane];
+    }
+    if (!tile_ok) return;
+    bool keep[4][4];
+#pragma unroll
+    for (int rg = 0; rg < 4; rg++)
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            keep[rg][r] = 4 * G + r < M && tile * 64 + rg * 16 + (lane & 15) < a.n_out;
+    if (a.gate) {
+        float gv[4][4];
+#pragma unroll
+        for (int rg = 0; rg < 4; rg++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int n = min(tile * 64 + rg * 16 + (lane & 15), a.n_out - 1);
+                gv[rg][r] = a.gate[(size_t)min(4 * G + r, M - 1) * a.ld_gate + n];
+            }
+#pragma unroll
+        for (int rg = 0; rg < 4; rg++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) keep[rg][r] = keep[rg][r] && !(fabsf(gv[rg][r]) < a.thr);
+    }
+#pragma unroll
+    for (int rg = 0; rg < 4; rg++) {
+        const int n = tile * 64 + rg * 16 + (lane & 15);
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            if (!keep[rg][r]) continue;
+            __hip_atomic_fetch_add(&a.acc[(size_t)(4 * G + r) * a.ld_acc + n], (double)acc[rg][r], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
 }
 
-template <int QT, int M, bool AVX2, int PPW, int EPI, int PRO>
+template <int QT, int M, int NT, int NK, int KB, int RING, int PRO>
+static int vx_launch_vg(const vxh_qmat *W, vx_gemm_args &a, hipStream_t st, hipEvent_t e0, hipEvent_t e1)
+{
+    constexpr int PPW = NK * KB / 2;
+    a.n_pairs = W->n_pairs;
+    a.n_blk = W->n_cols / 32;
+    a.n_t64 = (W->n_rows + 63) / 64;
+    a.n_splits = (W->n_pairs + PPW - 1) / PPW;
+    a.tq = W->tq;
+    a.td = W->td;
+    a.tq_bytes = (uint32_t)((size_t)a.n_t64 * a.n_blk * (QT == 2 ? 1024u : 2048u));
+    a.td_bytes = (uint32_t)((size_t)a.n_t64 * a.n_blk * 128u);
+    a.pan_bytes = (uint32_t)((size_t)W->n_pairs * 8 * 2 * M * 16);
+    if (PRO == VX_PRO_PANEL && a.rs_ld > 1 && a.rs_chunk % PPW)
+        return vxh_fail(VXH_ERR_PARAM, "gemm: K range of %d pairs crosses a %d-pair scale chunk", PPW, a.rs_chunk);
+    const int groups = (a.n_t64 + NT - 1) / NT;
+    if (e0 || e1)   // events recorded by the dispatch itself around the kernel
+        hipExtLaunchKernelGGL(vx_vg_kernel<QT, M, NT, NK, KB, RING, PRO>, dim3(groups * a.n_splits),
+                              dim3(64 * NT * NK), 0, st, e0, e1, 0, a);
+    else
+        vx_vg_kernel<QT, M, NT, NK, KB, RING, PRO><<<groups * a.n_splits, 64 * NT * NK, 0, st>>>(a);
+    VXH_LAUNCHED();
+    return VXH_OK;
+}
+
+// Work split of a verify-batch GEMM (measured on MI355X at M = 9, plain
+// panel input, kernel durations): one tile per workgroup with four
+// wavefronts along K of 4 blocks each for a plain panel (4096x4096 5.6-5.9
+// us against 6.2-6.4 for vx_gemm_kernel, 12288x4096 9.3-9.6 against
+// 11.9-12.2, 4096x11008 9.2-9.4 against 12.4, 22016x4096 14.3-14.5 against
+// 16.0-16.6); the prologue kinds share their slice over four tiles (their
+// sources are re-read per workgroup), 16 blocks per wavefront, and the
+// widest matrices take 32-block ranges with an 8-block ring (32000x4096
+// 17.5 against 21.0).
+template <int QT, int M, int PRO>
+static int vx_launch_verify(const vxh_qmat *W, vx_gemm_args &a, hipStream_t st, hipEvent_t e0, hipEvent_t e1)
+{
+    const int t64 = (W->n_rows + 63) / 64;
+    if (t64 >= 400) return vx_launch_vg<QT, M, 4, 1, 32, 8, PRO>(W, a, st, e0, e1);
+    if constexpr (PRO == VX_PRO_PANEL) return vx_launch_vg<QT, M, 1, 4, 4, 4, PRO>(W, a, st, e0, e1);
+    return vx_launch_vg<QT, M, 4, 1, 16, 4, PRO>(W, a, st, e0, e1);
+}
+
+template <int QT, int M, bool AVX2, int PPW, int PRO>
 static int vx_launch_ppw(const vxh_qmat *W, vx_gemm_args &a, hipStream_t st, hipEvent_t e0,
                          hipEvent_t e1)
 {
@@ -771,26 +1114,32 @@ static int vx_launch_ppw(const vxh_qmat *W, vx_gemm_args &a, hipStream_t st, hip
     if (PRO == VX_PRO_PANEL && a.rs_ld > 1 && a.rs_chunk % PPW)
         return vxh_fail(VXH_ERR_PARAM, "gemm: K slice of %d pairs crosses a %d-pair scale chunk", PPW,
                         a.rs_chunk);
-    constexpr int NWV = vx_nwv<QT, M, AVX2, PPW, EPI, PRO>::v;
+    constexpr int NWV = vx_nwv<QT, M, AVX2, PPW, PRO>::v;
     const int groups = (a.n_tiles + NWV - 1) / NWV;
     if (e0 || e1)   // events recorded by the dispatch itself around the kernel
-        hipExtLaunchKernelGGL(vx_gemm_kernel<QT, M, AVX2, PPW, EPI, PRO>, dim3(groups * a.n_splits),
+        hipExtLaunchKernelGGL(vx_gemm_kernel<QT, M, AVX2, PPW, PRO>, dim3(groups * a.n_splits),
                               dim3(64 * NWV), 0, st, e0, e1, 0, a);
     else
-        vx_gemm_kernel<QT, M, AVX2, PPW, EPI, PRO><<<groups * a.n_splits, 64 * NWV, 0, st>>>(a);
+        vx_gemm_kernel<QT, M, AVX2, PPW, PRO><<<groups * a.n_splits, 64 * NWV, 0, st>>>(a);
     VXH_LAUNCHED();
     return VXH_OK;
 }
 
-template <int QT, int M, bool AVX2, int EPI, int PRO>
+// Verify batches (M >= 5, exact panels or prologue kinds) take vx_vg_kernel
+// on the matrix's 64-row tiled copy; decode rows (M <= 4: latency-bound
+// launches, where vx_vg_kernel measured no faster) and AVX2-lane panels take
+// vx_gemm_kernel.
+template <int QT, int M, bool AVX2, int PRO>
 static int vx_launch_gemm(const vxh_qmat *W, vx_gemm_args &a, hipStream_t st, hipEvent_t e0,
                           hipEvent_t e1)
 {
+    if constexpr (M >= 5 && !AVX2 && PRO != VX_PRO_ATTN)
+        if (W->tq && W->td) return vx_launch_verify<QT, M, PRO>(W, a, st, e0, e1);
     typedef vx_ppw_set<QT, M> S;
     const long groups = (W->n_rows / 32 + 3) / 4;
     const int cand[3] = {S::v0, S::v1, S::v2};
     int pick = S::n - 1;
-    if (QT == 2 && M >= 5 && M <= 12 && EPI == VX_EPI_NONE && (PRO == VX_PRO_PANEL || PRO == VX_PRO_ROWS)) {
+    if (QT == 2 && M >= 5 && M <= 12 && (PRO == VX_PRO_PANEL || PRO == VX_PRO_ROWS)) {
         // verify batches (Q4_0) from a plain panel or rows: the 16-pair slice
         // whenever it still gives every CU more than one workgroup (measured
         // on MI355X at M = 9: 4096x11008 and 32000x4096 4-10% faster than 8
@@ -803,47 +1152,47 @@ static int vx_launch_gemm(const vxh_qmat *W, vx_gemm_args &a, hipStream_t st, hi
         for (int i = 0; i < S::n; i++)
             if (groups * ((W->n_pairs + cand[i] - 1) / cand[i]) <= S::target) { pick = i; break; }
     }
-    if (pick == 0) return vx_launch_ppw<QT, M, AVX2, S::v0, EPI, PRO>(W, a, st, e0, e1);
-    if (pick == 1) return vx_launch_ppw<QT, M, AVX2, S::v1, EPI, PRO>(W, a, st, e0, e1);
-    return vx_launch_ppw<QT, M, AVX2, S::v2, EPI, PRO>(W, a, st, e0, e1);
+    if (pick == 0) return vx_launch_ppw<QT, M, AVX2, S::v0, PRO>(W, a, st, e0, e1);
+    if (pick == 1) return vx_launch_ppw<QT, M, AVX2, S::v1, PRO>(W, a, st, e0, e1);
+    return vx_launch_ppw<QT, M, AVX2, S::v2, PRO>(W, a, st, e0, e1);
 }
 
-template <int M, int EPI, int PRO>
+template <int M, int PRO>
 static int vx_dispatch_m(const vxh_qmat *W, int avx2, vx_gemm_args &a, hipStream_t st, hipEvent_t e0,
                          hipEvent_t e1)
 {
     if (W->type != 2 && W->type != 8)
         return vxh_fail(VXH_ERR_UNSUPPORTED, "matrix type %d: this GEMM takes Q4_0 and Q8_0", W->type);
     if (W->type == 2) {
-        if constexpr (EPI == VX_EPI_NONE && PRO == VX_PRO_PANEL)
-            if (avx2) return vx_launch_gemm<2, M, true, EPI, PRO>(W, a, st, e0, e1);
-        return vx_launch_gemm<2, M, false, EPI, PRO>(W, a, st, e0, e1);
+        if constexpr (PRO == VX_PRO_PANEL)
+            if (avx2) return vx_launch_gemm<2, M, true, PRO>(W, a, st, e0, e1);
+        return vx_launch_gemm<2, M, false, PRO>(W, a, st, e0, e1);
     }
     if (avx2) return vxh_fail(VXH_ERR_UNSUPPORTED, "AVX2-lane panels apply to Q4_0 only");
-    return vx_launch_gemm<8, M, false, EPI, PRO>(W, a, st, e0, e1);
+    return vx_launch_gemm<8, M, false, PRO>(W, a, st, e0, e1);
 }
 
 // M = 1..16 to the templates
-template <int EPI, int PRO = VX_PRO_PANEL>
+template <int PRO = VX_PRO_PANEL>
 static int vx_dispatch(const vxh_qmat *W, int M, int avx2, vx_gemm_args &a, hipStream_t st, hipEvent_t e0,
                        hipEvent_t e1)
 {
     switch (M) {
-    case 1: return vx_dispatch_m<1, EPI, PRO>(W, avx2, a, st, e0, e1);
-    case 2: return vx_dispatch_m<2, EPI, PRO>(W, avx2, a, st, e0, e1);
-    case 3: return vx_dispatch_m<3, EPI, PRO>(W, avx2, a, st, e0, e1);
-    case 4: return vx_dispatch_m<4, EPI, PRO>(W, avx2, a, st, e0, e1);
-    case 5: return vx_dispatch_m<5, EPI, PRO>(W, avx2, a, st, e0, e1);
-    case 6: return vx_dispatch_m<6, EPI, PRO>(W, avx2, a, st, e0, e1);
-    case 7: return vx_dispatch_m<7, EPI, PRO>(W, avx2, a, st, e0, e1);
-    case 8: return vx_dispatch_m<8, EPI, PRO>(W, avx2, a, st, e0, e1);
-    case 9: return vx_dispatch_m<9, EPI, PRO>(W, avx2, a, st, e0, e1);
-    case 10: return vx_dispatch_m<10, EPI, PRO>(W, avx2, a, st, e0, e1);
-    case 11: return vx_dispatch_m<11, EPI, PRO>(W, avx2, a, st, e0, e1);
-    case 12: return vx_dispatch_m<12, EPI, PRO>(W, avx2, a, st, e0, e1);
-    case 13: return vx_dispatch_m<13, EPI, PRO>(W, avx2, a, st, e0, e1);
-    case 14: return vx_dispatch_m<14, EPI, PRO>(W, avx2, a, st, e0, e1);
-    case 15: return vx_dispatch_m<15, EPI, PRO>(W, avx2, a, st, e0, e1);
-    default: return vx_dispatch_m<16, EPI, PRO>(W, avx2, a, st, e0, e1);
+    case 1: return vx_dispatch_m<1, PRO>(W, avx2, a, st, e0, e1);
+    case 2: return vx_dispatch_m<2, PRO>(W, avx2, a, st, e0, e1);
+    case 3: return vx_dispatch_m<3, PRO>(W, avx2, a, st, e0, e1);
+    case 4: return vx_dispatch_m<4, PRO>(W, avx2, a, st, e0, e1);
+    case 5: return vx_dispatch_m<5, PRO>(W, avx2, a, st, e0, e1);
+    case 6: return vx_dispatch_m<6, PRO>(W, avx2, a, st, e0, e1);
+    case 7: return vx_dispatch_m<7, PRO>(W, avx2, a, st, e0, e1);
+    case 8: return vx_dispatch_m<8, PRO>(W, avx2, a, st, e0, e1);
+    case 9: return vx_dispatch_m<9, PRO>(W, avx2, a, st, e0, e1);
+    case 10: return vx_dispatch_m<10, PRO>(W, avx2, a, st, e0, e1);
+    case 11: return vx_dispatch_m<11, PRO>(W, avx2, a, st, e0, e1);
+    case 12: return vx_dispatch_m<12, PRO>(W, avx2, a, st, e0, e1);
+    case 13: return vx_dispatch_m<13, PRO>(W, avx2, a, st, e0, e1);
+    case 14: return vx_dispatch_m<14, PRO>(W, avx2, a, st, e0, e1);
+    case 15: return vx_dispatch_m<15, PRO>(W, avx2, a, st, e0, e1);
+    default: return vx_dispatch_m<16, PRO>(W, avx2, a, st, e0, e1);
     }
 }

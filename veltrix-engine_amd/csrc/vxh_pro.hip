@@ -109,11 +109,11 @@ extern "C" int vxh_gemm_pro(const vxh_qmat *W, int M, const vxh_pro *p, double *
     hipStream_t st = vxh_hs(s);
     hipEvent_t e0 = (hipEvent_t)start, e1 = (hipEvent_t)stop;
     switch (p->kind) {
-    case VXH_PRO_ROWS: return vx_dispatch<VX_EPI_NONE, VX_PRO_ROWS>(W, M, 0, a, st, e0, e1);
+    case VXH_PRO_ROWS: return vx_dispatch<VX_PRO_ROWS>(W, M, 0, a, st, e0, e1);
     case VXH_PRO_RESID: return vx_gemm_pro_resid(W, M, a, st, e0, e1);
     case VXH_PRO_ATTN:
-        if (M == 1) return vx_dispatch_m<1, VX_EPI_NONE, VX_PRO_ATTN>(W, 0, a, st, e0, e1);
-        return vx_dispatch_m<2, VX_EPI_NONE, VX_PRO_ATTN>(W, 0, a, st, e0, e1);
+        if (M == 1) return vx_dispatch_m<1, VX_PRO_ATTN>(W, 0, a, st, e0, e1);
+        return vx_dispatch_m<2, VX_PRO_ATTN>(W, 0, a, st, e0, e1);
     default: return vx_gemm_pro_swiglu(W, M, a, st, e0, e1);
     }
 }

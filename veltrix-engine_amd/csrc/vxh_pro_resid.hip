@@ -5,5 +5,5 @@
 int vx_gemm_pro_resid(const vxh_qmat *W, int M, vx_gemm_args &a, hipStream_t st, hipEvent_t e0,
                       hipEvent_t e1)
 {
-    return vx_dispatch<VX_EPI_NONE, VX_PRO_RESID>(W, M, 0, a, st, e0, e1);
+    return vx_dispatch<VX_PRO_RESID>(W, M, 0, a, st, e0, e1);
 }

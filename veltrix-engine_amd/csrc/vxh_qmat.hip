@@ -36,13 +36,27 @@ extern "C" int vxh_qmat_alloc(vxh_qmat *m, int type, int n_rows, int n_cols)
     size_t tiles = (size_t)m->n_rows / 32;
     size_t qs_bytes = tiles * m->n_pairs * (type == 2 ? 1024u : 2048u);
     size_t d_bytes = tiles * m->n_pairs * 32u * 4u;
+    // the 64-row tiled copy (GEMMs of 5..16 rows); its buffer loads take
+    // 32-bit offsets
+    const size_t t64 = ((size_t)m->n_rows + 63) / 64, nb = (size_t)n_cols / 32;
+    size_t tq_bytes = t64 * nb * (type == 2 ? 1024u : 2048u);
+    size_t td_bytes = t64 * nb * 128u;
+    if (tq_bytes > 0xFFFFFFFFull)
+        return vxh_fail(VXH_ERR_UNSUPPORTED, "qmat_alloc: %d x %d matrix exceeds 4 GiB", n_rows, n_cols);
     int rc = vxh_malloc(&m->qs, qs_bytes);
-    if (rc) return rc;
-    rc = vxh_malloc(&m->d, d_bytes);
-    if (rc) { vxh_free(m->qs); m->qs = nullptr; return rc; }
+    if (rc == VXH_OK) rc = vxh_malloc(&m->d, d_bytes);
+    if (rc == VXH_OK) rc = vxh_malloc(&m->tq, tq_bytes);
+    if (rc == VXH_OK) rc = vxh_malloc(&m->td, td_bytes);
+    if (rc) {
+        vxh_free(m->qs); vxh_free(m->d); vxh_free(m->tq); vxh_free(m->td);
+        memset(m, 0, sizeof(*m));
+        return rc;
+    }
     // padding rows/blocks must read as d = 0
     VXH_CHECK(hipMemset(m->d, 0, d_bytes));
     VXH_CHECK(hipMemset(m->qs, 0, qs_bytes));
+    VXH_CHECK(hipMemset(m->td, 0, td_bytes));
+    VXH_CHECK(hipMemset(m->tq, 0, tq_bytes));
     VXH_CHECK(hipDeviceSynchronize());
     return VXH_OK;
 }
@@ -51,6 +65,8 @@ extern "C" int vxh_qmat_free(vxh_qmat *m)
 {
     vxh_free(m->qs);
     vxh_free(m->d);
+    vxh_free(m->tq);
+    vxh_free(m->td);
     memset(m, 0, sizeof(*m));
     return VXH_OK;
 }
@@ -144,6 +160,30 @@ __global__ void vx_repack_kernel(const uint8_t *__restrict__ src, int type, int 
     dpl[((size_t)T * n_pairs + p) * 32 + j] = dd;
 }
 
+// The 64-row tiled copy: one thread per (logical row, block).
+__global__ void vx_repack_t64_kernel(const uint8_t *__restrict__ src, int type, int n_rows, int nb, int group,
+                                     int group_stride, int row_offset, uint32_t *__restrict__ tq,
+                                     uint16_t *__restrict__ td)
+{
+    long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (long)n_rows * nb) return;
+    const int r = (int)(idx / nb), b = (int)(idx % nb);
+    const int pr = vx_phys_row(r, group, group_stride, row_offset);
+    const int T = pr / 64, g = (pr % 64) / 16, n = pr % 16;
+    const uint8_t *blkp = src + ((size_t)r * nb + b) * vx_block_bytes(type);
+    const size_t tb = (size_t)T * nb + b;
+    td[(tb * 16 + n) * 4 + g] = ((const uint16_t *)blkp)[0];
+    for (int G = 0; G < 4; G++) {
+        if (type == 2) {
+            tq[(tb * 64 + G * 16 + n) * 4 + g] = vx_permute_q4_dword(vx_ld32_a2(blkp + 2 + 4 * G));
+        } else {
+            uint32_t *dst = tq + ((tb * 2 + (g >> 1)) * 64 + G * 16 + n) * 4 + (g & 1) * 2;
+            dst[0] = vx_permute_q8_dword(vx_ld32_a2(blkp + 2 + 8 * G));
+            dst[1] = vx_permute_q8_dword(vx_ld32_a2(blkp + 2 + 8 * G + 4));
+        }
+    }
+}
+
 __global__ void vx_unrepack_kernel(uint8_t *__restrict__ dstb, int type, int n_rows, int nb,
                                    int n_pairs, int group, int group_stride, int row_offset,
                                    const uint32_t *__restrict__ qs,
@@ -223,6 +263,13 @@ extern "C" int vxh_qmat_set_rows(vxh_qmat *m, const void *src, int src_on_device
         vx_repack_kernel<<<(unsigned)((n + 255) / 256), 256, 0, vxh_hs(s)>>>(
             (const uint8_t *)dsrc, m->type, n_rows, nb, m->n_pairs, group, group_stride, row_offset,
             (uint32_t *)m->qs, (uint32_t *)m->d);
+        VXH_LAUNCHED();
+        if (m->tq) {
+            const long nt = (long)n_rows * nb;
+            vx_repack_t64_kernel<<<(unsigned)((nt + 255) / 256), 256, 0, vxh_hs(s)>>>(
+                (const uint8_t *)dsrc, m->type, n_rows, nb, group, group_stride, row_offset, (uint32_t *)m->tq,
+                (uint16_t *)m->td);
+        }
     }
     VXH_LAUNCHED();
     if (stage) {

@@ -178,16 +178,13 @@ static void dev_free(vx_dev *d)
     vxh_free(d->q); vxh_free(d->att); vxh_free(d->logits);
     vxh_free(d->acc_qkv); vxh_free(d->acc_gu); vxh_free(d->acc_lg);
     vxh_free(d->stats); vxh_free(d->acc_out);
-    vxh_free(d->ss); vxh_free(d->hrows); vxh_free(d->cnt); vxh_free(d->cnt_row);
+    vxh_free(d->ss);
     vxh_free(d->x2); vxh_free(d->acc_y);
     vxh_free(d->pf_tok); vxh_free(d->pf_x); vxh_free(d->pf_xn); vxh_free(d->pf_qkv);
     vxh_free(d->pf_q); vxh_free(d->pf_att); vxh_free(d->pf_gu); vxh_free(d->pf_h); vxh_free(d->pf_px);
     vxh_workspace_free(&d->pf_ws);
     vxh_panel_free(&d->pan_d);
     vxh_panel_free(&d->pan_f);
-    vxh_xpanel_free(&d->xp_att);
-    vxh_xpanel_free(&d->xp_x);
-    vxh_xpanel_free(&d->xp_h);
     vxh_workspace_free(&d->ws);
     prof_free(d);
     if (d->stream) vxh_stream_destroy(d->stream);
@@ -250,16 +247,8 @@ static vx_error dev_alloc_common(vx_model *m)
     TRY(vxh_malloc((void **)&d->acc_out, sizeof(int) * (B + 4)));
     TRY(vxh_panel_alloc(&d->pan_d, B, d->d));
     TRY(vxh_panel_alloc(&d->pan_f, B, d->F));
-    TRY(vxh_xpanel_alloc(&d->xp_att, B, d->d));
-    TRY(vxh_xpanel_alloc(&d->xp_x, B, d->d));
-    TRY(vxh_xpanel_alloc(&d->xp_h, B, d->F));
-    TRY(vxh_malloc((void **)&d->hrows, sizeof(float) * B * (size_t)d->F));
-    TRY(vxh_malloc((void **)&d->cnt, sizeof(unsigned) * VX_N_COUNTERS));
-    TRY(vxh_malloc((void **)&d->cnt_row, sizeof(unsigned) * B * 64));
     TRY(vxh_malloc((void **)&d->x2, sizeof(float) * B * d->d));
     TRY(vxh_malloc((void **)&d->acc_y, sizeof(double) * B * (size_t)d->d));
-    TRY(vxh_fill_f32((float *)d->cnt, 0.0f, VX_N_COUNTERS, d->stream));
-    TRY(vxh_fill_f32((float *)d->cnt_row, 0.0f, (size_t)B * 64, d->stream));
     return VX_OK;
 }
 
@@ -666,7 +655,7 @@ vx_error vx_model_set_options(vx_model *m, const vx_model_options *opt)
     if (!d || !opt) return VX_ERR_PARAM;
     if (opt->q4_kernel != VX_Q4_EXACT && opt->q4_kernel != VX_Q4_AVX2_LANES) return VX_ERR_PARAM;
     if (opt->attn_cap < 0) return VX_ERR_PARAM;
-    if (opt->fused < VX_FUSED_NONE || opt->fused > VX_FUSED_PROLOGUE || opt->pro_max_rows < 0)
+    if ((opt->fused != VX_FUSED_NONE && opt->fused != VX_FUSED_PROLOGUE) || opt->pro_max_rows < 0)
         return VX_ERR_PARAM;
     if (opt->kv_half != 0 && opt->kv_half != 1) return VX_ERR_PARAM;
     if (opt->prefill_min_rows < 0) return VX_ERR_PARAM;
@@ -825,138 +814,6 @@ static vx_error zero_acc(vx_dev *d)
     TRY(vxh_fill_f32((float *)d->acc_gu, 0.0f, 2 * (size_t)B * d->ld_gu, s));
     TRY(vxh_fill_f32((float *)d->acc_lg, 0.0f, 2 * (size_t)B * d->ld_lg, s));
     TRY(vxh_fill_f32((float *)d->acc_y, 0.0f, 2 * (size_t)B * d->d, s));
-    TRY(vxh_fill_f32((float *)d->cnt, 0.0f, VX_N_COUNTERS, s));
-    TRY(vxh_fill_f32((float *)d->cnt_row, 0.0f, (size_t)B * 64, s));
-    d->acc_dirty = 0;
-    return VX_OK;
-}
-
-/* The fused path applies when every GEMM output is a whole number of
- * 32-row tiles, every layer has an output projection and the Q4_0 kernel is
- * the exact one (the AVX2-lane tails need the separate row kernels). */
-static int fused_ok(const vx_dev *d)
-{
-    if (d->opt.fused != VX_FUSED_EPILOGUE || d->opt.q4_kernel != VX_Q4_EXACT || d->has_f32) return 0;
-    if ((d->d + 2 * d->kvd) % 32 || d->hd % 8 || d->F % 32) return 0;
-    for (int l = 0; l < d->n_layers; l++)
-        if (!d->layers[l].has_o) return 0;
-    return 1;
-}
-
-static vx_error fgemm(vx_dev *d, const vxh_qmat *W, const vxh_xpanel *X, int M, double *acc, int ld_acc,
-                      int n_out, int cls, int rows_logical, const vxh_fepi *ep)
-{
-    vxh_event e0, e1;
-    vx_error e = prof_slot(d, W, M, n_out, cls, rows_logical, &e0, &e1);
-    if (e != VX_OK) return e;
-    TRY(vxh_gemm_fused(W, X, M, acc, ld_acc, n_out, scale_for(d, W->type), ep, e0, e1, d->stream));
-    return VX_OK;
-}
-
-/* Fused forward: per layer QKV(+RoPE/KV) -> attention(+O panel) ->
- * O(+residual, FFN-norm panel) -> gate/up(+SwiGLU panel) -> down(+residual,
- * next norm panel); the RMSNorms are applied by the consuming GEMMs from the
- * sums of squares their producers accumulate. */
-static vx_error forward_fused(vx_model *m, int M, int n_past, int logits_mode)
-{
-    vx_dev *d = vx_dev_of(m);
-    const int dd = d->d, kvd = d->kvd, F = d->F, V = d->V, L = d->n_layers;
-    const int B = VX_MAX_BATCH;
-    vxh_stream s = d->stream;
-    vx_error e;
-#define SS(l, j) (d->ss + ((size_t)(l) * 2 + (j)) * B)
-    if ((d->acc_dirty || d->acc_x_rows) && (e = zero_acc(d)) != VX_OK) return e;
-    d->acc_dirty = 1;
-    TRY(vxh_fill_f32((float *)d->ss, 0.0f, 2 * (size_t)(L + 1) * 2 * B, s));
-    if (d->has_embd) TRY(vxh_qmat_gather_rows(&d->embd, d->tok, M, vx_get_synthetic_weight_scale(), d->x, dd, s));
-    else TRY(vxh_fill_f32(d->x, 0.0f, (size_t)M * dd, s));
-    const float *w_out = d->has_out_norm ? d->out_norm : NULL;
-    d->xp_x.ss = L > 0 ? SS(0, 0) : SS(L, 0);
-    TRY(vxh_rows_xpanel(d->x, dd, M, dd, L > 0 ? d->layers[0].attn_norm : w_out, &d->xp_x, s));
-
-    vxh_fepi ep;
-    for (int l = 0; l < L; l++) {
-        vx_dev_layer *Ld = &d->layers[l];
-        float *kc = m->k_cache + (size_t)l * d->n_ctx_alloc * kvd;
-        float *vc = m->v_cache + (size_t)l * d->n_ctx_alloc * kvd;
-        /* q|k|v = W x_norm; RoPE, KV cache rows and q in the epilogue */
-        memset(&ep, 0, sizeof(ep));
-        ep.kind = VXH_FEPI_ROPE;
-        ep.counters = d->cnt;
-        ep.n_counters = VX_N_COUNTERS;
-        ep.n_past = n_past;
-        ep.n_ctx = d->n_ctx_alloc;
-        ep.n_pos = d->n_pos;
-        ep.n_heads = d->n_heads;
-        ep.n_kv_heads = d->n_kv;
-        ep.head_dim = d->hd;
-        ep.bq = Ld->bq; ep.bk = Ld->bk; ep.bv = Ld->bv;
-        ep.cos_tab = d->rope_cos; ep.sin_tab = d->rope_sin;
-        ep.q_out = d->q; ep.k_cache = kc; ep.v_cache = vc;
-        if ((e = fgemm(d, &Ld->wqkv, &d->xp_x, M, d->acc_qkv, d->ld_qkv, dd + 2 * kvd, VX_PROF_QKV,
-                       dd + 2 * kvd, &ep)))
-            return e;
-        /* attention; its combine writes the output projection's panel */
-        d->xp_att.ss = NULL;
-        TRY(vxh_attention_xpanel(d->q, M, n_past, d->n_ctx_alloc, d->n_heads, d->n_kv, d->hd,
-                                 d->opt.attn_cap, kc, vc, d->att, dd, &d->ws, d->cnt_row, &d->xp_att, s));
-        /* x += W_o att; the FFN norm's panel of x */
-        memset(&ep, 0, sizeof(ep));
-        ep.kind = VXH_FEPI_RESID;
-        ep.counters = d->cnt;
-        ep.n_counters = VX_N_COUNTERS;
-        ep.out_panel = &d->xp_x;
-        ep.norm_w = Ld->ffn_norm;
-        ep.x = d->x;
-        ep.ldx = dd;
-        d->xp_x.ss = SS(l, 1);
-        if ((e = fgemm(d, &Ld->wo, &d->xp_att, M, d->acc_x, dd, dd, VX_PROF_O, dd, &ep))) return e;
-        /* gate/up of the normed x; SwiGLU -> h panel */
-        memset(&ep, 0, sizeof(ep));
-        ep.kind = VXH_FEPI_SWIGLU;
-        ep.counters = d->cnt;
-        ep.n_counters = VX_N_COUNTERS;
-        ep.out_panel = &d->xp_h;
-        ep.n_h = F;
-        ep.h = d->hrows;
-        ep.ldh = F;
-        ep.thr = d->opt.ffn_gate_threshold;
-        d->xp_h.ss = NULL;
-        if ((e = fgemm(d, &Ld->wgu, &d->xp_x, M, d->acc_gu, d->ld_gu, d->ld_gu, VX_PROF_GATEUP, 2 * F,
-                       &ep)))
-            return e;
-        /* x += W_down h; the next norm's panel of x */
-        memset(&ep, 0, sizeof(ep));
-        ep.kind = VXH_FEPI_RESID;
-        ep.counters = d->cnt;
-        ep.n_counters = VX_N_COUNTERS;
-        ep.out_panel = &d->xp_x;
-        ep.norm_w = l + 1 < L ? d->layers[l + 1].attn_norm : w_out;
-        ep.x = d->x;
-        ep.ldx = dd;
-        d->xp_x.ss = l + 1 < L ? SS(l + 1, 0) : SS(L, 0);
-        if ((e = fgemm(d, &Ld->wd, &d->xp_h, M, d->acc_x, dd, dd, VX_PROF_DOWN, dd, &ep))) return e;
-    }
-
-    if (logits_mode != VX_LOGITS_NONE) {
-        const int rows = logits_mode == VX_LOGITS_LAST ? 1 : M;
-        const int orows = d->has_out ? d->out_rows : 0;
-        if (orows < V) TRY(vxh_fill_rows(d->logits, V, rows, orows, V - orows, -1e30f, s));
-        if (d->has_out) {
-            /* the output norm (if any) is applied from its sums of squares */
-            d->xp_x.ss = d->has_out_norm ? SS(L, 0) : NULL;
-            memset(&ep, 0, sizeof(ep));
-            ep.kind = VXH_FEPI_STORE;
-            ep.counters = d->cnt;
-            ep.n_counters = VX_N_COUNTERS;
-            ep.y = d->logits;
-            ep.ldy = V;
-            ep.last_row_only = logits_mode == VX_LOGITS_LAST;
-            if ((e = fgemm(d, &d->out, &d->xp_x, M, d->acc_lg, d->ld_lg, orows, VX_PROF_OUTPUT, orows, &ep)))
-                return e;
-        }
-    }
-#undef SS
     d->acc_dirty = 0;
     return VX_OK;
 }
@@ -1171,7 +1028,6 @@ vx_error vx_dev_forward(vx_model *m, int M, int n_past, int logits_mode)
     }
     if (pro_ok(d, M)) return forward_pro(m, M, n_past, logits_mode);
     if (d->opt.kv_half) return VX_ERR_UNSUPPORTED;   /* fp16 caches: prologue path only */
-    if (fused_ok(d)) return forward_fused(m, M, n_past, logits_mode);
     const int dd = d->d, kvd = d->kvd, F = d->F, V = d->V, n_ctx = d->n_ctx_alloc;
     const int avx2 = d->opt.q4_kernel == VX_Q4_AVX2_LANES;
     const float thr = d->opt.ffn_gate_threshold;

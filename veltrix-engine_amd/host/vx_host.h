@@ -15,7 +15,6 @@
 
 #define VX_MAX_BATCH 16
 #define VX_PF_ROWS 512             /* rows of one large-M prefill chunk */
-#define VX_N_COUNTERS (64 * 2048)  /* GEMM arrival counters, 64 words apart */
 
 /* ---- errors ----------------------------------------------------------------- */
 void vx_set_error(const char *fmt, ...);
@@ -93,15 +92,10 @@ typedef struct vx_dev {
     int *acc_out;                      /* [2 + 16]                                  */
     /* options */
     vx_model_options opt;
-    /* fused path: GEMM inputs as x-panels (the attention output, the normed
-     * residual stream, h), per-layer RMSNorm sums of squares
-     * ss[(l * 2 + j) * 16 + m] (j = 0 attention norm, 1 FFN norm; l = L is
-     * the output norm) and the last-arriver counters (zero between uses) */
-    vxh_xpanel xp_att, xp_x, xp_h;
+    /* per-layer RMSNorm sums of squares ss[(l * 2 + j) * 16 + m] (j = 0
+     * attention norm, 1 FFN norm; l = L is the output norm), added by the
+     * prologue GEMMs and applied to their products */
     double *ss;                        /* [(L+1)][2][16]; acc_x follows it in one allocation */
-    float *hrows;                      /* [16][F] SwiGLU output of the fused path    */
-    unsigned *cnt;                     /* [VX_N_COUNTERS] GEMM arrival counters      */
-    unsigned *cnt_row;                 /* [16 * 64] attention rows, 64 words apart   */
     /* prologue path: the second residual buffer (the residual alternates
      * between x and x2 inside a layer) and the attention projection's
      * accumulator (acc_x holds the down projection's) */
