@@ -336,8 +336,10 @@ int vxh_acc_store_norm(double *acc, int ld_acc, int M, int n, float *y, int ldy,
  *
  * vxh_rows_panel: fp32 rows X[M][ldx] (16-byte aligned, ldx % 4 == 0,
  * K % 32 == 0) converted once into the large-M GEMM's activation operand:
- * fp16 hi + lo of every element, laid out as the GEMM's LDS stages
- * ([64-row group][64-column pair][16 KiB]); vxh_rows_panel_bytes(M, K) bytes.
+ * each row scaled by a power of two 2^-e (e from its largest magnitude),
+ * fp16 hi + lo of every scaled element, laid out as the GEMM's LDS stages
+ * ([64-row group][64-column pair][16 KiB]), then the M row factors 2^e;
+ * vxh_rows_panel_bytes(M, K) bytes.
  *
  * vxh_gemm_rows: Y[m][n] = (R ? R[m][n] : 0) + scale * sum_k X[m][k] W[n][k]
  * for m < M (any M >= 1), n < n_out, from the rows panel of X (built with

@@ -172,3 +172,46 @@ def test_integration_snippet_compiles_and_links(P, tmp_path):
                         str(src), "-o", str(tmp_path / "app"), "-L", libdir, "-lveltrix_amd",
                         "-Wl,-rpath," + libdir], capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
+
+
+def test_attention_refuses_caches_past_32_bit_offsets(P):
+    """The attention kernels address a layer's cache rows with 32-bit byte
+    offsets; a layer of 4 GiB or more is refused on the host, before any
+    launch (and before the arguments are touched), at the size where fp32
+    and fp16 caches reach 2^32 bytes."""
+    P.vxh_attention.restype = C.c_int
+    P.vxh_attention.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p]
+    # 2^18 rows x 4096 fp32 = 2^32 bytes: one byte past the last 32-bit offset
+    rc = P.vxh_attention(None, 1, 0, 1 << 18, 32, 32, 128, 0, None, None, None, 4096, None, None)
+    assert rc == -5, rc                   # VXH_ERR_UNSUPPORTED
+    assert b"4 GiB" in P.vxh_last_error()
+    P.vxh_attention_qkv_f16.restype = C.c_int
+    P.vxh_attention_qkv_f16.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_void_p,
+                                        C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int,
+                                        C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p,
+                                        C.c_int, C.c_void_p, C.c_void_p]
+    # fp16: 2^19 rows x 4096 halves = 2^32 bytes; the q|k|v sums must look valid to reach the check
+    buf = (C.c_double * 16)()
+    rc = P.vxh_attention_qkv_f16(C.addressof(buf), 4096 * 3, None, 0, None, None, None, None, None, 1 << 20, 1, 0,
+                                 1 << 19, 32, 32, 128, 0, C.addressof(buf), C.addressof(buf), None, 4096, None, None)
+    assert rc == -5, (rc, P.vxh_last_error())
+    assert b"4 GiB" in P.vxh_last_error()
+
+
+def test_parity_helper_row_budget():
+    """The parity bar's fallback: an element beyond 1e-4 + 1e-3|oracle| passes
+    only within the oracle's own worst fp32 error of its row."""
+    rng = np.random.default_rng(3)
+    exact = rng.normal(0, 100, (4, 50))
+    exact[:, 0] = 1e-3                                  # near-zero results
+    oracle = exact + rng.normal(0, 3e-4, exact.shape)   # fp32-sum-sized errors
+    budget = np.abs(oracle - exact).max(axis=1)
+    gpu = exact.copy()
+    gpu[:, 0] = exact[:, 0] + 0.9 * budget              # off the bar, inside the budget
+    assert N.parity(gpu, oracle, exact)[0]
+    gpu[2, 0] = exact[2, 0] + 1.1 * budget[2]           # outside the row's budget
+    assert not N.parity(gpu, oracle, exact)[0]
+    gpu = oracle + 2e-4                                 # within the bar wherever |oracle| > 0.1
+    gpu[:, 0] = oracle[:, 0] + 1.0                      # a dropped term
+    assert not N.parity(gpu, oracle, exact)[0]

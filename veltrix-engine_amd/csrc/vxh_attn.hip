@@ -418,6 +418,34 @@ __device__ __forceinline__ void vx_kv_store4(float *base, size_t i, float4 v)
         *(float4 *)(base + i) = v;
 }
 
+// In the VGPR form, an MFMA whose destination overlaps one of its own A/B
+// source registers computes wrong values; the compiler gives a chain's MFMA a
+// destination of its own and may place it on a source that dies at that
+// MFMA.  These empty asms keep every source of the chains live until all of
+// their MFMAs have issued (they also read and write the accumulators, so they
+// cannot move above them); no instruction is emitted.
+template <int NJ>
+__device__ __forceinline__ void vx_keep_past_o(vx_f32x4 (&O)[NJ], float4 v4)
+{
+    static_assert(NJ == 4 || NJ == 8, "P.V chains of head_dim 64 or 128");
+    const vx_f32x4 v = __builtin_bit_cast(vx_f32x4, v4);
+    if constexpr (NJ == 8)
+        asm volatile("" : "+v"(O[0]), "+v"(O[1]), "+v"(O[2]), "+v"(O[3]), "+v"(O[4]), "+v"(O[5]), "+v"(O[6]),
+                     "+v"(O[7]) : "v"(v));
+    else
+        asm volatile("" : "+v"(O[0]), "+v"(O[1]), "+v"(O[2]), "+v"(O[3]) : "v"(v));
+}
+
+template <int NJ>
+__device__ __forceinline__ void vx_keep_past_o(vx_f32x4 (&O)[NJ], float v)
+{
+    if constexpr (NJ == 8)
+        asm volatile("" : "+v"(O[0]), "+v"(O[1]), "+v"(O[2]), "+v"(O[3]), "+v"(O[4]), "+v"(O[5]), "+v"(O[6]),
+                     "+v"(O[7]) : "v"(v));
+    else
+        asm volatile("" : "+v"(O[0]), "+v"(O[1]), "+v"(O[2]), "+v"(O[3]) : "v"(v));
+}
+
 template <bool QKV, int HD, bool KH = false, int NCW = 1, int NPG = 2, bool MERGE = false, bool NT = false>
 __device__ __forceinline__ void vx_attention_mfma_body(
     const float *__restrict__ q, int M, int n_past, int n_ctx, int n_heads, int n_kv, int cap,
@@ -680,6 +708,10 @@ __device__ __forceinline__ void vx_attention_mfma_body(
                 S[pg] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[pg][j].z, qv[j].z, S[pg], 0, 0, 0);
                 S[pg] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[pg][j].w, qv[j].w, S[pg], 0, 0, 0);
             }
+#pragma unroll
+            for (int j = 0; j < NJ; j++)
+                asm volatile("" : "+v"(S[pg]) : "v"(__builtin_bit_cast(vx_f32x4, kr[pg][j])),
+                             "v"(__builtin_bit_cast(vx_f32x4, qv[j])));
         }
         if (cc + 1 < NCW) load_k(tc + CH);        // the next chunk's K behind this chunk's V
         if constexpr (!V_EARLY) load_v(tc);
@@ -726,17 +758,21 @@ __device__ __forceinline__ void vx_attention_mfma_body(
         }
         rm = nm;
 
-        // P.V
+        // P.V; each step's sources stay live past its MFMAs (vx_keep_past_o)
 #pragma unroll
         for (int pg = 0; pg < NPG; pg++)
 #pragma unroll
-            for (int st = 0; st < 4; st++)
+            for (int st = 0; st < 4; st++) {
 #pragma unroll
                 for (int c = 0; c < NJ; c++) {
                     const float4 v4 = vr[pg][st][c / 4];
                     const float a = (c % 4) == 0 ? v4.x : (c % 4) == 1 ? v4.y : (c % 4) == 2 ? v4.z : v4.w;
                     O[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, p[pg][st], O[c], 0, 0, 0);
                 }
+#pragma unroll
+                for (int u = 0; u < NV4; u++) vx_keep_past_o<NJ>(O, vr[pg][st][u]);
+                vx_keep_past_o<NJ>(O, p[pg][st]);
+            }
     }
     int pidx = ch, np = nw;    // this partial's index, partials per query
     if constexpr (MERGE) {
@@ -812,7 +848,7 @@ __device__ __forceinline__ void vx_attention_mfma_body(
 //   positions for the output projection to combine).
 template <int HD, bool QKV>
 struct vx_att_cfg {
-    static constexpr int NCW = HD == 128 && !QKV ? 2 : 1;
+    static constexpr int NCW = 1;
     static constexpr int NPG = QKV ? 1 : 2;
     static constexpr bool MERGE = QKV;
     static constexpr int WCH = NCW * NPG * 16;
@@ -1005,6 +1041,10 @@ static int vx_attention_run(const float *q, const vx_qkv_args *qa, long n_clr, i
     if (head_dim % 4 || head_dim > ATT_MAX_HD)
         return vxh_fail(VXH_ERR_UNSUPPORTED, "attention: head_dim %d (multiple of 4, <= %d)",
                         head_dim, ATT_MAX_HD);
+    // the kernels address a layer's cache rows with 32-bit byte offsets
+    if ((uint64_t)n_ctx * n_kv_heads * head_dim * (kv_half ? 2u : 4u) > 0xFFFFFFFFull)
+        return vxh_fail(VXH_ERR_UNSUPPORTED, "attention: a layer's cache (%d rows of %d) exceeds 4 GiB", n_ctx,
+                        n_kv_heads * head_dim);
     int last = n_past + M - 1 < n_ctx ? n_past + M - 1 : n_ctx - 1;
     int ctx = last + 1;
     if (cap > 0 && ctx > cap) ctx = cap;

@@ -1086,22 +1086,29 @@ static int vx_launch_vg(const vxh_qmat *W, vx_gemm_args &a, hipStream_t st, hipE
     return VXH_OK;
 }
 
-// Work split of a verify-batch GEMM (measured on MI355X at M = 9, plain
-// panel input, kernel durations): one tile per workgroup with four
-// wavefronts along K of 4 blocks each for a plain panel (4096x4096 5.6-5.9
-// us against 6.2-6.4 for vx_gemm_kernel, 12288x4096 9.3-9.6 against
-// 11.9-12.2, 4096x11008 9.2-9.4 against 12.4, 22016x4096 14.3-14.5 against
-// 16.0-16.6); the prologue kinds share their slice over four tiles (their
-// sources are re-read per workgroup), 16 blocks per wavefront, and the
-// widest matrices take 32-block ranges with an 8-block ring (32000x4096
-// 17.5 against 21.0).
+// Work split of a verify-batch GEMM, measured on MI355X at M = 9 with the
+// inputs of the verify forward (kernel durations, weights rotated past the
+// Infinity Cache, fp64 atomics included):
+//   plain panel (down, 4096x11008): one tile per workgroup, four wavefronts
+//     along K of 8 blocks, 8-block ring: 10.5-10.7 us (vx_gemm_kernel 12.4);
+//   rows (attention output, 4096x4096): two tiles x four K ranges of 4
+//     blocks: 6.5 us (6.8);
+//   residual + norm prologue, 32000x4096 (logits): four tiles, 32-block
+//     ranges, 6-block ring: 23.0 us (26.8).
+// The residual prologue on narrower matrices stays with vx_gemm_kernel
+// (returns 1): every workgroup rebuilds its slice from x, the fp64 pending
+// sums and the norm weight, and the 8-wavefront 32-row tiles of that kernel
+// hide it better (12288x4096 12.7 us against 12.9-20 for every split tried
+// here, 22016x4096 18.3 against 18.4-31).
 template <int QT, int M, int PRO>
 static int vx_launch_verify(const vxh_qmat *W, vx_gemm_args &a, hipStream_t st, hipEvent_t e0, hipEvent_t e1)
 {
     const int t64 = (W->n_rows + 63) / 64;
-    if (t64 >= 400) return vx_launch_vg<QT, M, 4, 1, 32, 8, PRO>(W, a, st, e0, e1);
-    if constexpr (PRO == VX_PRO_PANEL) return vx_launch_vg<QT, M, 1, 4, 4, 4, PRO>(W, a, st, e0, e1);
-    return vx_launch_vg<QT, M, 4, 1, 16, 4, PRO>(W, a, st, e0, e1);
+    if constexpr (PRO == VX_PRO_PANEL) return vx_launch_vg<QT, M, 1, 4, 8, 8, PRO>(W, a, st, e0, e1);
+    if constexpr (PRO == VX_PRO_ROWS) return vx_launch_vg<QT, M, 2, 4, 4, 2, PRO>(W, a, st, e0, e1);
+    if constexpr (PRO == VX_PRO_RESID)
+        if (t64 >= 400) return vx_launch_vg<QT, M, 4, 1, 32, 6, PRO>(W, a, st, e0, e1);
+    return 1;
 }
 
 template <int QT, int M, bool AVX2, int PPW, int PRO>
@@ -1125,16 +1132,20 @@ static int vx_launch_ppw(const vxh_qmat *W, vx_gemm_args &a, hipStream_t st, hip
     return VXH_OK;
 }
 
-// Verify batches (M >= 5, exact panels or prologue kinds) take vx_vg_kernel
-// on the matrix's 64-row tiled copy; decode rows (M <= 4: latency-bound
-// launches, where vx_vg_kernel measured no faster) and AVX2-lane panels take
-// vx_gemm_kernel.
+// Verify batches (M >= 5) from a plain panel or rows, and the widest residual
+// GEMMs, take vx_vg_kernel on the matrix's 64-row tiled copy; decode rows
+// (M <= 4: latency-bound launches, where vx_vg_kernel measured no faster:
+// 2560x2048 3.7 -> 3.8 us, 11264x2048 5.3 -> 5.5), the other residual
+// prologues and AVX2-lane panels take vx_gemm_kernel.
 template <int QT, int M, bool AVX2, int PRO>
 static int vx_launch_gemm(const vxh_qmat *W, vx_gemm_args &a, hipStream_t st, hipEvent_t e0,
                           hipEvent_t e1)
 {
     if constexpr (M >= 5 && !AVX2 && PRO != VX_PRO_ATTN)
-        if (W->tq && W->td) return vx_launch_verify<QT, M, PRO>(W, a, st, e0, e1);
+        if (W->tq && W->td) {
+            const int rc = vx_launch_verify<QT, M, PRO>(W, a, st, e0, e1);
+            if (rc <= 0) return rc;
+        }
     typedef vx_ppw_set<QT, M> S;
     const long groups = (W->n_rows / 32 + 3) / 4;
     const int cand[3] = {S::v0, S::v1, S::v2};

@@ -28,6 +28,7 @@ struct vx_pf_args {
     const uint32_t *wd;
     int n_tiles, n_pairs, K;
     const uint4 *px;   // rows panel (vxh_rows_panel): [row group][pair][PF_STAGE units]
+    const float *rs;   // [M] power-of-two row scales of the panel
     int M;
     float *y;
     int ldy, n_out;
@@ -169,51 +170,75 @@ __global__ __launch_bounds__(256) void vx_pf_gemm_kernel(vx_pf_args a)
         for (int r = 0; r < 16; r++) {
             const int row = m0 + mt * 32 + 8 * (r / 4) + 4 * h + (r % 4);
             if (row >= a.M) continue;
-            float v = D[mt][r] * a.scale;
+            float v = (D[mt][r] * a.rs[row]) * a.scale;   // the row scale is a power of two
             if (a.r) v = a.r[(size_t)row * a.ldr + n] + v;
             a.y[(size_t)row * a.ldy + n] = v;
         }
     }
 }
 
-// Rows panel: fp32 rows x[M][ldx] as the GEMM's LDS stages, one thread per
-// (hi, lo) unit pair u of a (row group rg, pair p): u = ((mt*2 + blk)*2 + s)*64
-// + ln covers row 64 rg + 32 mt + ln % 32, elements 64 p + 32 blk + 16 (ln/32)
-// + 8 s .. + 7; hi = fp16(x), lo = fp16(x - hi).  Rows past M and columns past
-// K are zeros.
-__global__ void vx_pf_panel_kernel(const float *__restrict__ x, int ldx, int M, int K, int n_pairs,
-                                   uint4 *__restrict__ px)
+// Rows panel: fp32 rows x[M][ldx] as the GEMM's LDS stages.  Unit u of a
+// (row group rg, pair p) stage, u = ((mt*2 + blk)*2 + s)*64 + ln, holds row
+// 64 rg + 32 mt + ln % 32, elements 64 p + 32 blk + 16 (ln/32) + 8 s .. + 7,
+// as hi = fp16(x') and (64 units further) lo = fp16(x' - hi).  One workgroup
+// per row: x' = x 2^-e with e from the row's largest magnitude (vx_row_scale:
+// |x'| < 1), so no element overflows fp16 and a row of small values keeps
+// the low parts' bits; rs[row] = 2^e goes back in in the GEMM epilogue,
+// exactly.  Rows past M (up to the 64-row group) and columns past K are
+// zeros.
+__global__ __launch_bounds__(256) void vx_pf_panel_kernel(const float *__restrict__ x, int ldx, int M, int K,
+                                                          int n_pairs, uint4 *__restrict__ px, float *__restrict__ rs)
 {
-    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    const int rg = blockIdx.y;
-    if (idx >= (long)n_pairs * (PF_STAGE / 2)) return;
-    const int p = (int)(idx / (PF_STAGE / 2)), u = (int)(idx % (PF_STAGE / 2));
-    const int ln = u & 63, s = (u >> 6) & 1, blk = (u >> 7) & 1, mt = u >> 8;
-    const int row = rg * PF_BM + mt * 32 + (ln & 31);
-    const int k = 64 * p + 32 * blk + 16 * (ln >> 5) + 8 * s;
-    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    if (row < M && k < K) {   // K % 32 == 0: a block is wholly in range or out
-        const float4 a = *(const float4 *)(x + (size_t)row * ldx + k);
-        const float4 b = *(const float4 *)(x + (size_t)row * ldx + k + 4);
-        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-    }
-    vx_half8 hi, lo;
+    const int row = blockIdx.x;
+    const int rg = row / PF_BM, mt = (row % PF_BM) / 32, l32 = row % 32;
+    const bool live = row < M;
+    const float *xr = x + (size_t)(live ? row : 0) * ldx;
+    __shared__ float red[4];
+    float amax = 0.0f;
+    if (live)
+        for (int k = 8 * threadIdx.x; k < K; k += 8 * 256) {
+            const float4 a = *(const float4 *)(xr + k), b = *(const float4 *)(xr + k + 4);
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))));
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
+        }
+    amax = vx_wave_max64(amax);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float rsv;
+    const float sc = live ? vx_row_scale(amax, &rsv) : 1.0f;
+    if (live && threadIdx.x == 0) rs[row] = rsv;
+    for (int k = 8 * threadIdx.x; k < n_pairs * 64; k += 8 * 256) {
+        float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (live && k < K) {   // K % 32 == 0: a block is wholly in range or out
+            const float4 a = *(const float4 *)(xr + k), b = *(const float4 *)(xr + k + 4);
+            v[0] = a.x * sc; v[1] = a.y * sc; v[2] = a.z * sc; v[3] = a.w * sc;
+            v[4] = b.x * sc; v[5] = b.y * sc; v[6] = b.z * sc; v[7] = b.w * sc;
+        }
+        vx_half8 hi, lo;
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-        const _Float16 t = (_Float16)v[e];
-        hi[e] = t;
-        lo[e] = (_Float16)(v[e] - (float)t);
+        for (int e = 0; e < 8; e++) {
+            const _Float16 t = (_Float16)v[e];
+            hi[e] = t;
+            lo[e] = (_Float16)(v[e] - (float)t);
+        }
+        const int p = k / 64, blk = (k / 32) & 1, half = (k / 16) & 1, s = (k / 8) & 1;
+        uint4 *o = px + ((size_t)rg * n_pairs + p) * PF_STAGE + ((mt * 2 + blk) * 2 + s) * 128 + l32 + 32 * half;
+        o[0] = __builtin_bit_cast(uint4, hi);
+        o[64] = __builtin_bit_cast(uint4, lo);
     }
-    uint4 *o = px + ((size_t)rg * n_pairs + p) * PF_STAGE + (u >> 6) * 128 + ln;
-    o[0] = __builtin_bit_cast(uint4, hi);
-    o[64] = __builtin_bit_cast(uint4, lo);
+}
+
+// the row scales follow the stages (16-byte aligned)
+static size_t vx_pf_stage_bytes(int M, int K)
+{
+    return (size_t)((M + PF_BM - 1) / PF_BM) * ((K + 63) / 64) * PF_STAGE * sizeof(uint4);
 }
 
 extern "C" size_t vxh_rows_panel_bytes(int M, int K)
 {
     if (M < 1 || K < 1) return 0;
-    return (size_t)((M + PF_BM - 1) / PF_BM) * ((K + 63) / 64) * PF_STAGE * sizeof(uint4);
+    return vx_pf_stage_bytes(M, K) + ((size_t)M * sizeof(float) + 15) / 16 * 16;
 }
 
 extern "C" int vxh_rows_panel(const float *X, int ldx, int M, int K, void *px, vxh_stream s)
@@ -221,9 +246,9 @@ extern "C" int vxh_rows_panel(const float *X, int ldx, int M, int K, void *px, v
     if (!X || !px || M < 1 || K < 32 || K % 32 || ldx < K || ldx % 4 || ((uintptr_t)X & 15) || ((uintptr_t)px & 15))
         return vxh_fail(VXH_ERR_PARAM, "rows_panel: M %d K %d ldx %d", M, K, ldx);
     const int n_pairs = (K + 63) / 64;
-    const long per_rg = (long)n_pairs * (PF_STAGE / 2);
-    const dim3 grid((unsigned)((per_rg + 255) / 256), (unsigned)((M + PF_BM - 1) / PF_BM));
-    vx_pf_panel_kernel<<<grid, 256, 0, vxh_hs(s)>>>(X, ldx, M, K, n_pairs, (uint4 *)px);
+    const unsigned rows = (unsigned)((M + PF_BM - 1) / PF_BM * PF_BM);
+    vx_pf_panel_kernel<<<rows, 256, 0, vxh_hs(s)>>>(X, ldx, M, K, n_pairs, (uint4 *)px,
+                                                     (float *)((char *)px + vx_pf_stage_bytes(M, K)));
     VXH_LAUNCHED();
     return VXH_OK;
 }
@@ -243,6 +268,7 @@ extern "C" int vxh_gemm_rows(const vxh_qmat *W, const void *px, int M, float *Y,
     a.n_pairs = W->n_pairs;
     a.K = W->n_cols;
     a.px = (const uint4 *)px;
+    a.rs = (const float *)((const char *)px + vx_pf_stage_bytes(M, W->n_cols));
     a.M = M;
     a.y = Y;
     a.ldy = ldy;

@@ -291,6 +291,11 @@ vx_error vx_dev_ensure_kv(vx_model *m)
     }
     size_t per = (size_t)(d->n_layers > 0 ? d->n_layers : 1) * n_ctx * d->kvd;
     const size_t esz = d->opt.kv_half ? 2 : sizeof(float);   /* kvd is even: whole floats */
+    if ((size_t)n_ctx * d->kvd * esz > 0xFFFFFFFFull) {
+        /* the attention kernels address a layer's rows with 32-bit offsets */
+        vx_set_error("KV cache of %d positions x %d exceeds 4 GiB per layer", n_ctx, d->kvd);
+        return VX_ERR_UNSUPPORTED;
+    }
     TRY(vxh_malloc((void **)&m->k_cache, per * esz));
     TRY(vxh_malloc((void **)&m->v_cache, per * esz));
     TRY(vxh_fill_f32(m->k_cache, 0.0f, per * esz / sizeof(float), d->stream));
@@ -682,17 +687,7 @@ vx_error vx_model_set_options(vx_model *m, const vx_model_options *opt)
         m->cache_len = 0;
         d->kv_gen++;
     }
-    d->opt = *opt;
-    if (cap_changed && d->pf_ready) {
-        /* the prefill attention workspace is sized for the cap: rebuilt on next use */
-        TRY(vxh_stream_sync(d->stream));
-        vxh_workspace_free(&d->pf_ws);
-        vxh_free(d->pf_tok); vxh_free(d->pf_x); vxh_free(d->pf_xn); vxh_free(d->pf_qkv);
-        vxh_free(d->pf_q); vxh_free(d->pf_att); vxh_free(d->pf_gu); vxh_free(d->pf_h); vxh_free(d->pf_px);
-        d->pf_tok = NULL; d->pf_x = d->pf_xn = d->pf_qkv = d->pf_q = d->pf_att = d->pf_gu = d->pf_h = NULL;
-        d->pf_px = NULL;
-        d->pf_ready = 0;
-    }
+    d->opt = *opt;   /* the prefill workspace follows the cap on its next use (pf_alloc) */
     if (cap_changed && m->k_cache) return dev_alloc_workspace(d, d->n_ctx_alloc, d->opt.attn_cap);
     return VX_OK;
 }
@@ -1108,6 +1103,17 @@ static int pf_ok(const vx_dev *d)
 
 static vx_error pf_alloc(vx_dev *d)
 {
+    if (d->pf_ready && (d->pf_ws_ctx != d->n_ctx_alloc || d->pf_ws_cap != d->opt.attn_cap)) {
+        /* a cache allocated again for another n_ctx, or another cap: the
+         * attention workspace is sized for both */
+        TRY(vxh_stream_sync(d->stream));
+        vxh_workspace_free(&d->pf_ws);
+        size_t an = vxh_attention_workspace_floats(VX_PF_ROWS, d->n_ctx_alloc, d->opt.attn_cap, d->n_heads,
+                                                   d->n_kv, d->hd);
+        TRY(vxh_workspace_alloc(&d->pf_ws, 32, an));
+        d->pf_ws_ctx = d->n_ctx_alloc;
+        d->pf_ws_cap = d->opt.attn_cap;
+    }
     if (d->pf_ready) return VX_OK;
     const size_t R = VX_PF_ROWS;
     TRY(vxh_malloc((void **)&d->pf_tok, sizeof(int) * R));
@@ -1122,6 +1128,8 @@ static vx_error pf_alloc(vx_dev *d)
     size_t an = vxh_attention_workspace_floats(VX_PF_ROWS, d->n_ctx_alloc, d->opt.attn_cap, d->n_heads, d->n_kv,
                                                d->hd);
     TRY(vxh_workspace_alloc(&d->pf_ws, 32, an));
+    d->pf_ws_ctx = d->n_ctx_alloc;
+    d->pf_ws_cap = d->opt.attn_cap;
     d->pf_ready = 1;
     return VX_OK;
 }

@@ -106,6 +106,7 @@ typedef struct vx_dev {
      * gate/up rows, SwiGLU rows, each [VX_PF_ROWS][...] fp32, and the
      * attention workspace for that many rows */
     int pf_ready;
+    int pf_ws_ctx, pf_ws_cap;          /* n_ctx_alloc and attn_cap pf_ws was sized for */
     int *pf_tok;
     float *pf_x, *pf_xn, *pf_qkv, *pf_q, *pf_att, *pf_gu, *pf_h;
     void *pf_px;                       /* rows panel of the GEMM input (vxh_rows_panel) */
