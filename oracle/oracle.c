@@ -455,7 +455,7 @@ float or_round_half(float x)
 }
 
 static void attention(or_model *m, const float *q, const float *k, const float *v,
-                      float *out, int layer, float *scores)
+                      float *out, int layer, float *scores_all)
 {
     int hd = m->n_head_dim, nh = m->n_heads, nkv = m->n_kv_heads;
     int kvd = nkv * hd;
@@ -476,7 +476,10 @@ static void attention(or_model *m, const float *q, const float *k, const float *
     int cs = cache_size;
     if (m->attn_cap > 0 && cs > m->attn_cap) cs = m->attn_cap;
     float scale = 1.0f / sqrtf((float)hd);
+    /* heads are independent: each has its own scores row */
+    #pragma omp parallel for schedule(static)
     for (int h = 0; h < nh; h++) {
+        float *scores = scores_all + (size_t)h * (size_t)(max_ctx + 8);
         const float *qh = q + (size_t)h * hd;
         int kvh = nkv == 1 ? 0 : h * nkv / nh;
         for (int t = 0; t < cs; t++) {
@@ -582,7 +585,7 @@ static int forward_impl(or_model *m, const int *tokens, int n, float *logits, in
     float *g = (float *)calloc((size_t)F + 8, sizeof(float));
     float *u = (float *)calloc((size_t)F + 8, sizeof(float));
     float *ones = (float *)malloc(sizeof(float) * (big + 8));
-    float *scores = (float *)malloc(sizeof(float) * (size_t)(max_ctx + 8));
+    float *scores = (float *)malloc(sizeof(float) * (size_t)nh * (size_t)(max_ctx + 8));
     if (!tmp || !x || !xo || !xn || !ntmp || !q || !kk || !vv || !ao || !g || !u || !ones || !scores) {
         free(tmp); free(x); free(xo); free(xn); free(ntmp); free(q); free(kk); free(vv);
         free(ao); free(g); free(u); free(ones); free(scores);
@@ -662,14 +665,302 @@ static int forward_impl(or_model *m, const int *tokens, int n, float *logits, in
     return 0;
 }
 
+/* ===================================================================== */
+/* layer-major forward (same results as forward_impl, faster)             */
+/* ===================================================================== */
+
+/* forward_impl runs each token through every layer before the next token,
+ * dequantising every matrix once per token.  The functions below run a
+ * chunk of tokens one layer at a time: each matrix is dequantised once per
+ * chunk and multiplied with all of the chunk's tokens, with the token index
+ * in the lanes of a GCC vector.  Every lane performs, for its (row, token),
+ * the same sequence of fp32 operations as f32_row, the attention of token t
+ * at layer l runs after tokens < t wrote their rows of layer l, and the
+ * elementwise steps run per token in the same order as forward_impl: the
+ * results are bit-identical to forward_impl's (or_forward_tokenwise), which
+ * tests/test_oracle_forward.py checks.  The x86 lane mode (its 4-float
+ * tails) is served by forward_impl only. */
+typedef float or_v8 __attribute__((vector_size(32)));
+#define OR_LANES 16        /* tokens per lane block: two vectors */
+#define OR_CHUNK 256       /* tokens per layer-major chunk */
+
+/* Dequantisation split over rows; every element is computed as in
+ * dequant_any. */
+static void dequant_rows_par(const or_mat *w, float *dst, int rows, int cols, float scale)
+{
+    if (w->type == OR_TYPE_F32) { memcpy(dst, w->data, sizeof(float) * (size_t)rows * cols); return; }
+    if (cols % 32) { dequant_any(w->type, w->data, dst, (size_t)rows * cols, scale); return; }
+    size_t bsz = w->type == OR_TYPE_Q4_0 ? 18 : 34;
+    int nb = cols / 32;
+    #pragma omp parallel for schedule(static)
+    for (int i = 0; i < rows; i++)
+        dequant_any(w->type, (const uint8_t *)w->data + (size_t)i * nb * bsz, dst + (size_t)i * cols,
+                    (size_t)cols, scale);
+}
+
+/* f32_row of one matrix row against 16 tokens: xb holds the tokens' vectors
+ * as [k][16]. */
+static void f32_row_lanes(const float *a, const float *xb, int cols, float *out)
+{
+    or_v8 s0 = {0}, s1 = {0};
+    int j = 0;
+    for (; j + 4 <= cols; j += 4) {
+        const or_v8 *x = (const or_v8 *)(xb + (size_t)j * OR_LANES);
+        or_v8 a0 = {a[j], a[j], a[j], a[j], a[j], a[j], a[j], a[j]};
+        or_v8 a1 = {a[j + 1], a[j + 1], a[j + 1], a[j + 1], a[j + 1], a[j + 1], a[j + 1], a[j + 1]};
+        or_v8 a2 = {a[j + 2], a[j + 2], a[j + 2], a[j + 2], a[j + 2], a[j + 2], a[j + 2], a[j + 2]};
+        or_v8 a3 = {a[j + 3], a[j + 3], a[j + 3], a[j + 3], a[j + 3], a[j + 3], a[j + 3], a[j + 3]};
+        or_v8 g0 = a0 * x[0] + a1 * x[2];
+        or_v8 g1 = a0 * x[1] + a1 * x[3];
+        g0 = g0 + a2 * x[4];
+        g1 = g1 + a2 * x[5];
+        g0 = g0 + a3 * x[6];
+        g1 = g1 + a3 * x[7];
+        s0 = s0 + g0;
+        s1 = s1 + g1;
+    }
+    for (; j < cols; j++) {
+        const or_v8 *x = (const or_v8 *)(xb + (size_t)j * OR_LANES);
+        or_v8 aj = {a[j], a[j], a[j], a[j], a[j], a[j], a[j], a[j]};
+        s0 = s0 + aj * x[0];
+        s1 = s1 + aj * x[1];
+    }
+    memcpy(out, &s0, 32);
+    memcpy(out + 8, &s1, 32);
+}
+
+/* The chunk's tokens X[t][.] (row stride ldx) in lane blocks [tb][k][16],
+ * zero past n. */
+static void to_lanes(const float *X, int ldx, int n, int cols, float *xb)
+{
+    int ntb = (n + OR_LANES - 1) / OR_LANES;
+    for (int tb = 0; tb < ntb; tb++)
+        for (int k = 0; k < cols; k++)
+            for (int l = 0; l < OR_LANES; l++) {
+                int t = tb * OR_LANES + l;
+                xb[((size_t)tb * cols + k) * OR_LANES + l] = t < n ? X[(size_t)t * ldx + k] : 0.0f;
+            }
+}
+
+/* apply_mat (not in place) for n tokens: Y[t][i] = f32_row(A_i, X[t]), or 0
+ * where gate[t][i] is below thr. */
+static void apply_mat_tokens(const or_model *m, const or_mat *w, const float *X, int ldx, int n, float *Y,
+                             int ldy, int rows, int cols, const float *gate, int ldg, float thr, float *A,
+                             float *xb)
+{
+    if (!w || !w->data) {
+        for (int t = 0; t < n; t++) memset(Y + (size_t)t * ldy, 0, sizeof(float) * (size_t)rows);
+        return;
+    }
+    dequant_rows_par(w, A, rows, cols, m->wscale);
+    to_lanes(X, ldx, n, cols, xb);
+    int ntb = (n + OR_LANES - 1) / OR_LANES;
+    #pragma omp parallel for schedule(dynamic, 1)
+    for (int ib = 0; ib < rows; ib += 8)
+        for (int tb = 0; tb < ntb; tb++)
+            for (int i = ib; i < ib + 8 && i < rows; i++) {
+                float o[OR_LANES];
+                f32_row_lanes(A + (size_t)i * cols, xb + (size_t)tb * cols * OR_LANES, cols, o);
+                for (int l = 0; l < OR_LANES; l++) {
+                    int t = tb * OR_LANES + l;
+                    if (t >= n) break;
+                    Y[(size_t)t * ldy + i] = (gate && fabsf(gate[(size_t)t * ldg + i]) < thr) ? 0.0f : o[l];
+                }
+            }
+}
+
+/* apply_mat in place for n tokens: row i of token t reads token t's vector
+ * (cols elements) with rows < i already overwritten; xb has room for
+ * max(rows, cols) elements per token. */
+static void apply_mat_tokens_inplace(const or_model *m, const or_mat *w, float *X, int ldx, int n, int rows,
+                                     int cols, float *A, float *xb)
+{
+    int w_ld = rows > cols ? rows : cols;
+    dequant_rows_par(w, A, rows, cols, m->wscale);
+    int ntb = (n + OR_LANES - 1) / OR_LANES;
+    #pragma omp parallel for schedule(dynamic, 1)
+    for (int tb = 0; tb < ntb; tb++) {
+        float *blk = xb + (size_t)tb * w_ld * OR_LANES;
+        for (int k = 0; k < w_ld; k++)
+            for (int l = 0; l < OR_LANES; l++) {
+                int t = tb * OR_LANES + l;
+                blk[(size_t)k * OR_LANES + l] = t < n ? X[(size_t)t * ldx + k] : 0.0f;
+            }
+        for (int i = 0; i < rows; i++) {
+            float o[OR_LANES];
+            f32_row_lanes(A + (size_t)i * cols, blk, cols, o);
+            memcpy(blk + (size_t)i * OR_LANES, o, sizeof o);
+        }
+        for (int l = 0; l < OR_LANES; l++) {
+            int t = tb * OR_LANES + l;
+            if (t >= n) break;
+            for (int i = 0; i < rows; i++) X[(size_t)t * ldx + i] = blk[(size_t)i * OR_LANES + l];
+        }
+    }
+}
+
+static int forward_chunk(or_model *m, const int *tokens, int n, int t_base, float *logits, int all, float *A,
+                         float *xb, float *wk)
+{
+    int d = m->n_embd, hd = m->n_head_dim, nh = m->n_heads, nkv = m->n_kv_heads;
+    int kvd = nkv * hd, F = m->n_ff, V = m->n_vocab, qd = nh * hd;
+    int big = d > F ? d : F;
+    if (qd > big) big = qd;
+    int max_ctx = m->n_ctx < 1 ? 4096 : m->n_ctx;
+    /* per-token state, token-major: [n][ld] */
+    int ld = big + 8;
+    float *X = wk, *XO = X + (size_t)n * ld, *XN = XO + (size_t)n * ld, *Q = XN + (size_t)n * ld;
+    float *K = Q + (size_t)n * ld, *Vv = K + (size_t)n * ld, *AO = Vv + (size_t)n * ld;
+    float *G = AO + (size_t)n * ld, *U = G + (size_t)n * ld, *T = U + (size_t)n * ld;
+    float *ntmp = T + (size_t)n * ld, *ones = ntmp + ld, *scores = ones + ld;
+    int *rope_pos = (int *)malloc(sizeof(int) * (size_t)n), *att_pos = (int *)malloc(sizeof(int) * (size_t)n);
+    if (!rope_pos || !att_pos) { free(rope_pos); free(att_pos); return -3; }
+    for (int i = 0; i < ld; i++) ones[i] = 1.0f;
+    /* the cache positions forward_impl's attention() uses, clamp included */
+    int c = m->cache_len;
+    for (int t = 0; t < n; t++) {
+        rope_pos[t] = c;
+        att_pos[t] = c >= max_ctx ? max_ctx - 1 : c;
+        c = att_pos[t] + 1;
+    }
+    for (int t = 0; t < n; t++) embed(m, tokens[t], X + (size_t)t * ld, A);
+    for (int l = 0; l < m->n_layers; l++) {
+        for (int t = 0; t < n; t++) {
+            float *xo = XO + (size_t)t * ld, *xn = XN + (size_t)t * ld, *x = X + (size_t)t * ld;
+            memcpy(xo, x, sizeof(float) * (size_t)d);
+            memcpy(xn, x, sizeof(float) * (size_t)d);
+            apply_norm(xn, ntmp, m->attn_norm ? m->attn_norm[l] : NULL, d, ones);
+        }
+        apply_mat_tokens(m, &m->wq[l], XN, ld, n, Q, ld, qd, d, NULL, 0, 0.0f, A, xb);
+        apply_mat_tokens(m, &m->wk[l], XN, ld, n, K, ld, kvd, d, NULL, 0, 0.0f, A, xb);
+        apply_mat_tokens(m, &m->wv[l], XN, ld, n, Vv, ld, kvd, d, NULL, 0, 0.0f, A, xb);
+        for (int t = 0; t < n; t++) {
+            float *q = Q + (size_t)t * ld, *kk = K + (size_t)t * ld, *vv = Vv + (size_t)t * ld;
+            if (m->bq && m->bq[l]) for (int i = 0; i < qd; i++) q[i] += m->bq[l][i];
+            if (m->bk && m->bk[l]) for (int i = 0; i < kvd; i++) kk[i] += m->bk[l][i];
+            if (m->bv && m->bv[l]) for (int i = 0; i < kvd; i++) vv[i] += m->bv[l][i];
+            or_rope(q, kk, rope_pos[t], nh, nkv, hd, 0, m->rope_theta);
+            m->cache_len = att_pos[t];
+            attention(m, q, kk, vv, AO + (size_t)t * ld, l, scores);
+        }
+        if (m->wo[l].data) {
+            if (m->attn_o_inplace) {
+                apply_mat_tokens_inplace(m, &m->wo[l], AO, ld, n, d, qd, A, xb);
+            } else {
+                apply_mat_tokens(m, &m->wo[l], AO, ld, n, Q, ld, d, qd, NULL, 0, 0.0f, A, xb);
+                for (int t = 0; t < n; t++)
+                    memcpy(AO + (size_t)t * ld, Q + (size_t)t * ld, sizeof(float) * (size_t)d);
+            }
+        }
+        for (int t = 0; t < n; t++) {
+            float *x = X + (size_t)t * ld, *xo = XO + (size_t)t * ld, *xn = XN + (size_t)t * ld;
+            float *ao = AO + (size_t)t * ld;
+            for (int i = 0; i < d; i++) x[i] = xo[i] + ao[i];
+            memcpy(xo, x, sizeof(float) * (size_t)d);
+            memcpy(xn, x, sizeof(float) * (size_t)d);
+            apply_norm(xn, ntmp, m->ffn_norm ? m->ffn_norm[l] : NULL, d, ones);
+        }
+        apply_mat_tokens(m, &m->wg[l], XN, ld, n, G, ld, F, d, NULL, 0, 0.0f, A, xb);
+        for (int t = 0; t < n; t++) or_silu(G + (size_t)t * ld, F);
+        apply_mat_tokens(m, &m->wu[l], XN, ld, n, U, ld, F, d, G, ld, m->gate_thr, A, xb);
+        for (int t = 0; t < n; t++) {
+            float *g = G + (size_t)t * ld, *u = U + (size_t)t * ld, *xn = XN + (size_t)t * ld;
+            int ti = t_base + t;
+            if (m->gate_near || m->gate_near_idx) gate_log(m, g, F, ti, l);
+            for (int f = 0; f < m->flip && f < OR_MAX_FLIPS; f++)
+                if (m->flip_tok[f] == ti && m->flip_layer[f] == l && m->flip_col[f] >= 0 && m->flip_col[f] < F)
+                    gate_flip(m, &m->wu[l], xn, g, u, F, d, T + (size_t)t * ld, m->flip_col[f]);
+            for (int i = 0; i < F; i++) g[i] = g[i] * u[i];
+        }
+        apply_mat_tokens(m, &m->wd[l], G, ld, n, AO, ld, d, F, NULL, 0, 0.0f, A, xb);
+        for (int t = 0; t < n; t++) {
+            float *x = X + (size_t)t * ld, *xo = XO + (size_t)t * ld, *ao = AO + (size_t)t * ld;
+            for (int i = 0; i < d; i++) x[i] = xo[i] + ao[i];
+        }
+    }
+    m->cache_len = c;
+    /* logits: every token, or the last one of the call */
+    int t0 = all ? 0 : n - 1;
+    if (!all && !logits) { free(rope_pos); free(att_pos); return 0; }
+    int nl = n - t0;
+    for (int t = t0; t < n; t++) {
+        float *xf = XN + (size_t)t * ld;
+        memcpy(xf, X + (size_t)t * ld, sizeof(float) * (size_t)d);
+        if (m->has_out_norm) apply_norm(xf, ntmp, m->out_norm, d, ones);
+    }
+    for (int t = t0; t < n; t++) {
+        float *lg = all ? logits + (size_t)(t_base + t) * V : logits;
+        for (int i = 0; i < V; i++) lg[i] = -1e30f;
+    }
+    if (m->output.data) {
+        int orows = m->output.rows;
+        int ocols = m->output.cols > 0 ? m->output.cols : d;
+        if (orows > 0 && orows <= V)
+            apply_mat_tokens(m, &m->output, XN + (size_t)t0 * ld, ld, nl, all ? logits + (size_t)(t_base + t0) * V
+                                                                              : logits,
+                             V, orows, ocols, NULL, 0, 0.0f, A, xb);
+    }
+    free(rope_pos);
+    free(att_pos);
+    return 0;
+}
+
+static int forward_layers(or_model *m, const int *tokens, int n, float *logits, int all)
+{
+    int d = m->n_embd, hd = m->n_head_dim, nh = m->n_heads, F = m->n_ff;
+    if (d <= 0 || d > 8192) return -4;
+    if (n <= 0) return 0;
+    int big = d > F ? d : F;
+    if (nh * hd > big) big = nh * hd;
+    size_t tmpn = 0;
+    const or_mat *all_m[7];
+    for (int l = 0; l < m->n_layers; l++) {
+        all_m[0] = &m->wq[l]; all_m[1] = &m->wk[l]; all_m[2] = &m->wv[l]; all_m[3] = &m->wo[l];
+        all_m[4] = &m->wg[l]; all_m[5] = &m->wu[l]; all_m[6] = &m->wd[l];
+        for (int i = 0; i < 7; i++)
+            if (all_m[i]->data) {
+                size_t e = (size_t)all_m[i]->rows * all_m[i]->cols;
+                if (e > tmpn) tmpn = e;
+            }
+    }
+    if (m->output.data && (size_t)m->output.rows * m->output.cols > tmpn)
+        tmpn = (size_t)m->output.rows * m->output.cols;
+    if ((size_t)(m->tok_embd.cols + 32) > tmpn) tmpn = (size_t)m->tok_embd.cols + 32;
+    int max_ctx = m->n_ctx < 1 ? 4096 : m->n_ctx;
+    int chunk = n < OR_CHUNK ? n : OR_CHUNK;
+    size_t ld = (size_t)big + 8;
+    float *A = (float *)malloc(sizeof(float) * (tmpn + 64));
+    float *xb = (float *)aligned_alloc(64, sizeof(float) * (size_t)((chunk + OR_LANES - 1) / OR_LANES) *
+                                               OR_LANES * ld);
+    float *wk = (float *)calloc(11 * (size_t)chunk * ld + 2 * ld + (size_t)nh * (size_t)(max_ctx + 8),
+                                sizeof(float));
+    int rc = (A && xb && wk) ? 0 : -3;
+    for (int t0 = 0; t0 < n && rc == 0; t0 += chunk) {
+        int nc = n - t0 < chunk ? n - t0 : chunk;
+        int last = t0 + nc == n;
+        rc = forward_chunk(m, tokens + t0, nc, t0, all ? logits : (last ? logits : NULL), all, A, xb, wk);
+    }
+    free(A);
+    free(xb);
+    free(wk);
+    return rc;
+}
+
 int or_forward(or_model *m, const int *tokens, int n, float *logits)
 {
-    return forward_impl(m, tokens, n, logits, 0);
+    if (m->q4_mode == OR_Q4_AVX2LANES) return forward_impl(m, tokens, n, logits, 0);
+    return forward_layers(m, tokens, n, logits, 0);
 }
 
 int or_forward_all(or_model *m, const int *tokens, int n, float *logits_all)
 {
-    return forward_impl(m, tokens, n, logits_all, 1);
+    if (m->q4_mode == OR_Q4_AVX2LANES) return forward_impl(m, tokens, n, logits_all, 1);
+    return forward_layers(m, tokens, n, logits_all, 1);
+}
+
+int or_forward_tokenwise(or_model *m, const int *tokens, int n, float *logits, int all)
+{
+    return forward_impl(m, tokens, n, logits, all);
 }
 
 /* ===================================================================== */

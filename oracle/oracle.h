@@ -106,11 +106,17 @@ typedef struct {
 float or_round_half(float x);
 
 /* Sequential single-token forwards over tokens[0..n); writes the last token's
- * logits (src/model.c:391-628).  Returns 0 or a negative error. */
+ * logits (src/model.c:391-628).  Returns 0 or a negative error.  In the
+ * OR_Q4_EXACT mode the tokens run layer-major in chunks (each matrix
+ * dequantised once per chunk, tokens in vector lanes) with results
+ * bit-identical to the token-major or_forward_tokenwise. */
 int or_forward(or_model *m, const int *tokens, int n, float *logits);
 /* Teacher-forced: logits for EVERY token (row i = logits after token i), i.e.
  * n calls of the reference forward with n_tokens = 1. */
 int or_forward_all(or_model *m, const int *tokens, int n, float *logits_all);
+/* The token-major restatement (one token through every layer, then the
+ * next): all = 0 is or_forward, all = 1 or_forward_all. */
+int or_forward_tokenwise(or_model *m, const int *tokens, int n, float *logits, int all);
 
 /* ---- acceptance: textbook speculative sampling on softmax probabilities
  * (the reference compares raw logits, src/speculative.c:167, :205) ------ */

@@ -116,6 +116,7 @@ def oracle():
         L.or_rope.argtypes = [f32p, f32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float]
         L.or_forward.argtypes = [C.POINTER(OrModel), i32p, C.c_int, f32p]
         L.or_forward_all.argtypes = [C.POINTER(OrModel), i32p, C.c_int, f32p]
+        L.or_forward_tokenwise.argtypes = [C.POINTER(OrModel), i32p, C.c_int, f32p, C.c_int]
         L.or_argmax.restype = C.c_int
         L.or_argmax.argtypes = [f32p, C.c_int]
         L.or_softmax_temp.argtypes = [f32p, C.c_int, C.c_float, f32p]
@@ -366,13 +367,17 @@ class DevBuf:
 
 def parity(gpu, oracle, exact, atol=1e-4, rtol=1e-3):
     """The floating-point parity bar.  Elementwise |gpu - oracle| <= atol +
-    rtol*|oracle|; where the oracle's own fp32 rounding error against the fp64
-    exact value already exceeds that bar (large-magnitude dot products with
-    near-zero results), the element passes only if the GPU is at least as
-    close to the exact value as the oracle is.  Returns (ok, n_fallback)."""
+    rtol*|oracle|.  Where the oracle's own fp32 rounding error against the
+    fp64 exact value already exceeds that bar (large dot products with
+    near-zero results), the element passes only if the GPU's error against
+    the exact value is within the oracle's own worst error on the same output
+    row (the same K, the same input vector): the GPU is then as accurate as
+    the reference's fp32 sum is on that row.  Returns (ok, n_fallback)."""
     g = np.asarray(gpu, np.float64)
     o = np.asarray(oracle, np.float64)
     e = np.asarray(exact, np.float64)
     ok_bar = np.abs(g - o) <= atol + rtol * np.abs(o)
-    ok_fb = np.abs(g - e) <= np.abs(o - e)
+    oerr = np.abs(o - e)
+    budget = oerr.max(axis=-1, keepdims=True) if oerr.ndim else oerr
+    ok_fb = np.abs(g - e) <= np.maximum(oerr, budget)
     return bool(np.all(ok_bar | ok_fb)), int(np.count_nonzero(~ok_bar))

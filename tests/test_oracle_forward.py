@@ -182,3 +182,74 @@ def test_oracle_avx2_lane_forward_matches_reference_avx2_gemv_build(tmp_path, ca
         assert O.or_forward(ex.ptr, np.array([t], np.int32), 1, exact[i]) == 0
     assert np.abs(exact - ref_logits).max() > 1e-3
 
+
+
+LAYER_MAJOR_CASES = [
+    # layers, d, heads, kv, ff, vocab, matrix type, tokens, n_ctx, cap, attn_o_inplace, kv_half, biases
+    (2, 64, 4, 2, 128, 96, GGML_Q4_0, 40, 4096, 4096, 0, 0, False),
+    (2, 64, 4, 2, 128, 96, GGML_Q4_0, 40, 4096, 4096, 1, 0, True),
+    (1, 64, 2, 1, 128, 48, GGML_Q4_0, 37, 20, 10, 0, 0, False),     # context clamp and cap
+    (2, 96, 3, 3, 192, 64, GGML_Q8_0, 23, 4096, 0, 0, 1, True),     # fp16 KV rows
+    (1, 64, 4, 4, 96, 40, GGML_F32, 17, 4096, 4096, 1, 0, False),
+    (1, 32, 2, 1, 64, 24, GGML_Q4_0, 300, 512, 4096, 0, 0, False),  # two 256-token chunks
+]
+
+
+@pytest.mark.parametrize("case", LAYER_MAJOR_CASES)
+def test_layer_major_forward_is_bit_identical(tmp_path, case):
+    """or_forward / or_forward_all run a call's tokens layer by layer
+    (matrices dequantised once per chunk, tokens in vector lanes); they must
+    give the token-major restatement's results bit for bit: logits, every
+    cache row, cache_len, the gate-hook records and inverted gate decisions,
+    from an empty cache and from a partly filled one."""
+    L, d, h, kv, ff, V, mt, n, n_ctx, cap, inplace, kvh, biases = case
+    rng = np.random.default_rng(sum(case[:8]) + 5)
+    path = str(tmp_path / "m.gguf")
+    raw = llama_gguf(path, rng, L, d, h, kv, ff, V, std=0.05, norm_random=True, emb_type=mt, out_type=mt,
+                     matrix_type=mt)
+    if biases:
+        kvd = kv * (d // h)
+        for l in range(L):
+            raw[f"blk.{l}.attn_q.bias"] = rng.normal(0, 0.1, d).astype(np.float32)
+            raw[f"blk.{l}.attn_k.bias"] = rng.normal(0, 0.1, kvd).astype(np.float32)
+            raw[f"blk.{l}.attn_v.bias"] = rng.normal(0, 0.1, kvd).astype(np.float32)
+    tokens = rng.integers(0, V, n).astype(np.int32)
+
+    def model():
+        return OracleModel(raw, L, d, h, kv, ff, V, n_ctx=n_ctx, attn_cap=cap, attn_o_inplace=inplace,
+                           kv_half=kvh, gate_thr=0.01)
+
+    def run(fn_all, om, toks, all_rows):
+        near = np.zeros((len(toks), L), np.float32)
+        idx = np.zeros((len(toks), L), np.int32)
+        om.m.gate_near, om.m.gate_near_idx = near.ctypes.data, idx.ctypes.data
+        om.m.flip = 2
+        om.m.flip_tok[0], om.m.flip_layer[0], om.m.flip_col[0] = 1, 0, 3
+        om.m.flip_tok[1], om.m.flip_layer[1], om.m.flip_col[1] = len(toks) - 1, L - 1, 7
+        out = np.zeros((len(toks), V) if all_rows else V, np.float32)
+        assert fn_all(om, toks, out, all_rows) == 0
+        om.m.gate_near, om.m.gate_near_idx, om.m.flip = None, None, 0
+        return out, near, idx
+
+    def batched(om, toks, out, a):
+        return (O.or_forward_all if a else O.or_forward)(om.ptr, toks, len(toks), out)
+
+    def tokenwise(om, toks, out, a):
+        return O.or_forward_tokenwise(om.ptr, toks, len(toks), out, a)
+
+    for all_rows in (True, False):
+        for split in (0, n // 3):
+            res = []
+            for fn in (batched, tokenwise):
+                om = model()
+                if split:   # a partly filled cache, written by the other restatement
+                    pre = np.zeros(V, np.float32)
+                    other = tokenwise if fn is batched else batched
+                    assert other(om, tokens[:split], pre, False) == 0
+                r = run(fn, om, tokens[split:], all_rows)
+                res.append(r + (om.k_cache.copy(), om.v_cache.copy(), om.cache_len))
+            (a, an, ai, ak, av, al), (b, bn, bi, bk, bv, bl) = res
+            assert al == bl
+            assert np.array_equal(a, b), (all_rows, split, np.abs(a - b).max())
+            assert np.array_equal(ak, bk) and np.array_equal(av, bv)
+            assert np.array_equal(an, bn) and np.array_equal(ai, bi)
