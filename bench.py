@@ -20,7 +20,17 @@ roofline: the verify dequant-GEMMs of the target (M = k+1 rows), timed with
 HIP events that the dispatch records on the target's stream around every 7th
 GEMM launch of each class, in a separate instrumented pass of the same
 workload after the timed steps; achieved = algorithmic bytes (Q4_0 weight
-blocks + fp32 activations in + fp32 results out) / event time.
+blocks + fp32 activations in + fp32 results out) / event time, where the time
+includes the SwiGLU panel launch that prepares the down projection's input.
+
+config also carries flat scalar figures: per verify GEMM class its average
+launch time and HBM fraction (verify_<class>_us / _frac), the mix with and
+without the SwiGLU panel, the draft's M = 1 GEMM fraction from the same
+instrumented pass, and -- measured on the GPU after the timed work, without
+the reference CPU legs of --mode configs -- the 4096x4096 Q4_0 M = 5 GEMM
+(c1_gemm_us / _frac) and single verify steps of the 22L d2048 model at 512
+positions (c3_verify_step_ms) and of the 28L d3584 V152064 model at 8192
+positions (c5_verify_step_ms, with the acceptance kernels' c5_accept_ms).
 
 cpu_baseline: the reference engine's own x86 build (oracle/_ref, built from
 its sources by oracle/Makefile) on this host's cores: single-token forwards
@@ -323,20 +333,38 @@ def run_spec(args):
     # stride that walks through the 32 layers; a launch with events costs
     # ~18 us of host time, so this pass is not the one timed above)
     P.vx_model_set_profiling(tm, args.prof_every)
+    P.vx_model_set_profiling(dm, args.prof_every)
     P.vxh_device_sync()
     tot_p, elapsed_p = decode_steps([4243 + i for i in range(args.prof_steps)])
-    prof = (N.VxGemmProfile * 5)()
+    prof = (N.VxGemmProfile * N.VX_PROF_N)()
+    prof_d = (N.VxGemmProfile * N.VX_PROF_N)()
     P.vx_model_get_profile(tm, prof)
+    P.vx_model_get_profile(dm, prof_d)
     P.vx_model_set_profiling(tm, 0)
+    P.vx_model_set_profiling(dm, 0)
     log(f"instrumented pass: {args.prof_steps * args.tokens / elapsed_p:.1f} tok/s over {args.prof_steps} steps")
-    names = ["qkv", "attn_out", "gate_up", "down", "output"]
-    ms = sum(p.ms for p in prof)
-    byt = sum(p.bytes for p in prof)
-    launches = sum(p.launches for p in prof)
+    names = ["qkv", "attn_out", "gate_up", "down", "output", "swiglu_panel"]
+    gemm = prof[:5]
+    ms_gemm = sum(p.ms for p in gemm)
+    ms = ms_gemm + prof[5].ms           # the SwiGLU panel feeding down counted in the mix
+    byt = sum(p.bytes for p in gemm)
+    launches = sum(p.launches for p in gemm)
     achieved = byt / (ms * 1e-3) / 1e9 if ms > 0 else 0.0
+    achieved_gemm = byt / (ms_gemm * 1e-3) / 1e9 if ms_gemm > 0 else 0.0
+    ms_d = sum(p.ms for p in prof_d[:5])
+    draft_gbs = sum(p.bytes for p in prof_d[:5]) / (ms_d * 1e-3) / 1e9 if ms_d > 0 else 0.0
     breakdown = {nm: {"launches": p.launches, "avg_us": round(1e3 * p.ms / max(p.launches, 1), 2),
                       "GB/s": round(p.bytes / (p.ms * 1e-3) / 1e9, 1) if p.ms > 0 else None}
                  for nm, p in zip(names, prof)}
+    flat = {}
+    for nm, p in zip(names, prof):
+        flat[f"verify_{nm}_us"] = round(1e3 * p.ms / max(p.launches, 1), 2)
+        if nm != "swiglu_panel":
+            flat[f"verify_{nm}_frac"] = round(p.bytes / (p.ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4) if p.ms > 0 else None
+    flat["verify_gemm_mix_frac"] = round(achieved / PEAK_HBM_GBS, 4)
+    flat["verify_gemm_only_frac"] = round(achieved_gemm / PEAK_HBM_GBS, 4)
+    flat["draft_gemm_frac"] = round(draft_gbs / PEAK_HBM_GBS, 4)
+    flat["draft_gemm_avg_us"] = round(1e3 * ms_d / max(sum(p.launches for p in prof_d[:5]), 1), 2)
     log(f"decode: {value:.1f} tok/s; rounds {tot['rounds']}, accepted {tot['accepted']}/{tot['drafted']}; "
         f"verify {tot['verify_ms']:.1f} ms, draft {tot['draft_ms']:.1f} ms over {args.steps} steps")
     log("verify GEMMs:", json.dumps(breakdown))
@@ -349,6 +377,15 @@ def run_spec(args):
     P.vx_speculative_destroy(st)
     P.vx_model_destroy(tm)
     P.vx_model_destroy(dm)
+    if not args.no_configs:
+        # the other configurations' figures (GPU only, after the timed work)
+        L = _bind_gemm(N, P)
+        c1 = _configs_gemm(N, P, L, args, None, 0, cases=[("C1", 4096, 4096, 2, 5)])[0]
+        c3 = _configs_verify(N, P, L, "C3", C3_SHAPE, 512, 4, 0.0, 2, 10, None, 0)
+        c5 = _configs_verify(N, P, L, "C5", C5_SHAPE, 8192, 8, 1.0, 8, 5, None, 0)
+        flat.update({"c1_gemm_us": c1["gemm_us"], "c1_gemm_frac": c1["frac"],
+                     "c3_verify_step_ms": c3["verify_step_ms"], "c3_accept_ms": c3["accept_ms"],
+                     "c5_verify_step_ms": c5["verify_step_ms"], "c5_accept_ms": c5["accept_ms"]})
     line = {
         "metric": "accepted tok/s (7B-shape Q4_0, k=8); verify dequant-GEMM HBM GB/s % of peak",
         "value": round(value, 3),
@@ -374,6 +411,7 @@ def run_spec(args):
             "verify_ms_per_round": round(tot["verify_ms"] / max(tot["rounds"], 1), 3),
             "draft_ms_per_round": round(tot["draft_ms"] / max(tot["rounds"], 1), 3),
             "prefill_s": round(prefill_s, 3),
+            **flat,
             "verify_gemms": breakdown,
         },
         "roofline": {
@@ -383,9 +421,11 @@ def run_spec(args):
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
             "traffic": read_traffic(),
-            "kernel": (f"vx_gemm_kernel (Q4_0, M={args.k + 1}), every {args.prof_every}th verify GEMM launch "
-                       f"of each class (kernel-execution events), in a separate instrumented pass of "
-                       f"{args.prof_steps} steps after the timed ones"),
+            "kernel": (f"verify dequant-GEMMs at M={args.k + 1} (Q4_0: vx_vg_kernel for attn_out, down and "
+                       f"the output matrix, vx_gemm_kernel for qkv and gate_up) with the SwiGLU panel launch "
+                       f"that feeds down counted in the time; every {args.prof_every}th launch of each class "
+                       f"(kernel-execution events), in a separate instrumented pass of {args.prof_steps} "
+                       f"steps after the timed ones"),
             "launches": launches,
             "avg_launch_us": round(1e3 * ms / max(launches, 1), 3),
             "bytes_per_launch": round(byt / max(launches, 1)),
@@ -698,13 +738,13 @@ def _cpu_gemv_ms(N, R, qt, rows, cols, reps=3):
     return 1e3 * float(np.median(times[1:]))
 
 
-def _configs_gemm(N, P, L, args, R, threads):
+def _configs_gemm(N, P, L, args, R, threads, cases=None):
     """C1 / C2: Y[M][rows] = X[M][cols] . W^T from device-resident fp32 rows,
     W rotated over > 300 MB.  gemm_us: the GEMM kernel alone (vxh_gemm_pro,
     panel built from the fp32 rows in its prologue, fp64 accumulator);
     op_us: GEMM + the store kernel that rounds the accumulator to the fp32
     result and clears it (vxh_acc_store)."""
-    cases = [("C1", 4096, 4096, 2, 5)] + [
+    cases = cases or [("C1", 4096, 4096, 2, 5)] + [
         ("C2", r, c, t, m) for (r, c) in ((11008, 4096), (4096, 11008)) for t in (2, 8) for m in (1, 5, 9)]
     out = []
     cpu_cache = {}
@@ -761,7 +801,7 @@ def _configs_verify(N, P, L, name, shape, ctx, k, T, emb_type, reps, R, threads)
     """One verify step of k drafts against ctx prefilled positions: the
     target forward of k+1 tokens through the public entry point
     (vx_model_verify, all k+1 logit rows copied to the host), and the
-    acceptance kernels on those logits (vxh_row_stats + vxh_accept; greedy
+    acceptance kernels on those logits (vxh_row_stats_mc + vxh_accept_mc; greedy
     at T = 0, else sampled with seeded uniforms against random draft logits
     whose nucleus descriptors vxh_sample wrote).  Medians over reps steps,
     each rolled back to ctx with vx_model_kv_truncate."""
@@ -806,11 +846,16 @@ def _configs_verify(N, P, L, name, shape, ctx, k, T, emb_type, reps, R, threads)
         assert L.vxh_sample(C.c_void_p(dD.ptr.value + 4 * j * V), V, T, 1.0, du.ptr, dtok.ptr,
                             C.c_void_p(dnuc.ptr.value + 32 * j), None) == 0, L.vxh_last_error()
 
+    ws = N.VxhVocabWs()
+    assert L.vxh_vocab_ws_alloc(C.byref(ws), k + 1) == 0, L.vxh_last_error()
+
     def accept():
-        L.vxh_row_stats(dL.ptr, V, k + 1, V, T, dstats.ptr, None)
-        L.vxh_accept(dL.ptr, V, V, dstats.ptr, dD.ptr, V, V, dnuc.ptr, ddr.ptr, k, T, du.ptr, dout.ptr, None)
+        L.vxh_row_stats_mc(dL.ptr, V, k + 1, V, T, dstats.ptr, C.byref(ws), None)
+        L.vxh_accept_mc(dL.ptr, V, V, dstats.ptr, dD.ptr, V, V, dnuc.ptr, ddr.ptr, k, T, du.ptr, dout.ptr,
+                        C.byref(ws), None)
     accept()
     acc_ms = _time_loop(L, 50, accept) / 50
+    L.vxh_vocab_ws_free(C.byref(ws))
     res = dout.get(np.int32, k + 3)
     for b in (dL, dD, dstats, dnuc, ddr, du, dtok, dout):
         b.free()
@@ -871,6 +916,8 @@ def main():
     ap.add_argument("--fetch", help="traffic mode: counter CSV of the FETCH_SIZE run")
     ap.add_argument("--write", help="traffic mode: counter CSV of the WRITE_SIZE run")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="spec mode: skip the C1 GEMM and C3/C5 verify-step figures")
     ap.add_argument("--kv-half", action="store_true",
                     help="spec mode: both models with the flagged fp16 KV cache (not the headline)")
     ap.add_argument("--prof-steps", type=int, default=2,

@@ -139,8 +139,11 @@ void vx_speculative_set_trace(vx_speculative_state *state, int *drafts, int *emi
  * matrix class is bracketed by two HIP events that the dispatch records
  * around the kernel on the model's stream (n = 1: every launch; 0: off);
  * vx_model_get_profile folds the elapsed times per class.  bytes are
- * algorithmic: weight blocks + fp32 activations in + fp32 results out. */
-enum { VX_PROF_QKV = 0, VX_PROF_O, VX_PROF_GATEUP, VX_PROF_DOWN, VX_PROF_OUTPUT, VX_PROF_N };
+ * algorithmic: weight blocks + fp32 activations in + fp32 results out.
+ * VX_PROF_SWIGLU times the verify batches' SwiGLU panel launch that feeds
+ * the down projection (bytes: the fp64 gate/up sums read and the fp16
+ * hi/lo panel written; no flops). */
+enum { VX_PROF_QKV = 0, VX_PROF_O, VX_PROF_GATEUP, VX_PROF_DOWN, VX_PROF_OUTPUT, VX_PROF_SWIGLU, VX_PROF_N };
 typedef struct {
     int launches;
     double ms;

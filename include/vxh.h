@@ -200,6 +200,11 @@ int vxh_swiglu_panel(double *acc, int ld_acc, int M, int F, float thr, int avx2,
  * AVX2 tail). */
 int vxh_swiglu_panel_norm(double *acc, int ld_acc, int M, int F, float thr, const double *ss_in,
                           int ss_K, double *clear, size_t n_clear, vxh_panel *p, vxh_stream s);
+/* The same with two events (either may be NULL) that the dispatch records
+ * around the kernel, for kernel-execution timing. */
+int vxh_swiglu_panel_norm_timed(double *acc, int ld_acc, int M, int F, float thr, const double *ss_in,
+                                int ss_K, double *clear, size_t n_clear, vxh_panel *p, vxh_event e0,
+                                vxh_event e1, vxh_stream s);
 
 /* ---- skinny-M dequant GEMM ---------------------------------------------------
  * Y[m][n] = sum_k X[m][k] * W[n][k] for m < M, n < N, W quantised, X a panel.
@@ -479,6 +484,34 @@ int vxh_sample_keep(const float *l, int V, float T, float top_p, const float *u_
 int vxh_accept(const float *L, int ldl, int V, const float *stats, const float *D, int ldd,
                int Vd, const float *nuc, const int *drafts, int k, float T, const float *u,
                int *out, vxh_stream s);
+
+/* ---- acceptance on many compute units ------------------------------------------
+ * The same three operations with each row cut into up to 64 chunks of a
+ * multiple of 1024 entries, one workgroup per chunk; the workgroup that
+ * finishes last combines the chunks' partial results (fixed-point masses are
+ * integers: the drawn token does not depend on the chunking).  They replace
+ * the single-workgroup kernels of src/speculative.c:186-233 (vxh_accept),
+ * :35-91 (vxh_sample, top_p >= 1) and the softmax statistics of :44-53.
+ * The workspace holds the partials and completion counters (zeroed at
+ * allocation, left zeroed by every call); one workspace serves one stream at
+ * a time.  vxh_sample_keep_mc with top_p < 1 runs vxh_sample_keep;
+ * vxh_accept_mc with T > 0 and k = 0 runs vxh_accept.  max_rows bounds R of
+ * vxh_row_stats_mc. */
+typedef struct {
+    void *part;       /* partial results */
+    unsigned *cnt;    /* completion counters */
+    float *stats;     /* the sampler's row statistics */
+    int max_rows;
+} vxh_vocab_ws;
+int vxh_vocab_ws_alloc(vxh_vocab_ws *ws, int max_rows);
+void vxh_vocab_ws_free(vxh_vocab_ws *ws);
+int vxh_row_stats_mc(const float *L, int ldl, int R, int V, float T, float *stats, vxh_vocab_ws *ws,
+                     vxh_stream s);
+int vxh_sample_keep_mc(const float *l, int V, float T, float top_p, const float *u_dev, int *token_out,
+                       float *nuc, float *keep, vxh_vocab_ws *ws, vxh_stream s);
+int vxh_accept_mc(const float *L, int ldl, int V, const float *stats, const float *D, int ldd, int Vd,
+                  const float *nuc, const int *drafts, int k, float T, const float *u, int *out,
+                  vxh_vocab_ws *ws, vxh_stream s);
 
 #ifdef __cplusplus
 }

@@ -241,6 +241,13 @@ class VxSynthSpec(C.Structure):
                 ("embd_type", C.c_int), ("output_type", C.c_int)]
 
 
+class VxhVocabWs(C.Structure):
+    _fields_ = [("part", C.c_void_p), ("cnt", C.c_void_p), ("stats", C.c_void_p), ("max_rows", C.c_int)]
+
+
+VX_PROF_N = 6   # profile classes: qkv, attn_o, gate_up, down, output, SwiGLU panel
+
+
 class VxGemmProfile(C.Structure):
     _fields_ = [("launches", C.c_int), ("ms", C.c_double), ("bytes", C.c_double), ("flops", C.c_double)]
 
@@ -338,6 +345,13 @@ def bind_vxh(L):
     L.vxh_accept.argtypes = [vp, C.c_int, C.c_int, vp, vp, C.c_int, C.c_int, vp, vp, C.c_int,
                              C.c_float, vp, vp, vp]
     L.vxh_stream_sync.argtypes = [vp]
+    L.vxh_vocab_ws_alloc.argtypes = [C.POINTER(VxhVocabWs), C.c_int]
+    L.vxh_vocab_ws_free.argtypes = [C.POINTER(VxhVocabWs)]
+    L.vxh_row_stats_mc.argtypes = [vp, C.c_int, C.c_int, C.c_int, C.c_float, vp, C.POINTER(VxhVocabWs), vp]
+    L.vxh_sample_keep_mc.argtypes = [vp, C.c_int, C.c_float, C.c_float, vp, vp, vp, vp, C.POINTER(VxhVocabWs),
+                                     vp]
+    L.vxh_accept_mc.argtypes = [vp, C.c_int, C.c_int, vp, vp, C.c_int, C.c_int, vp, vp, C.c_int, C.c_float, vp,
+                                vp, C.POINTER(VxhVocabWs), vp]
     return L
 
 

@@ -28,6 +28,7 @@ STRUCTS = {
     "vx_synth_spec": ["seed", "std", "matrix_type", "embd_type", "output_type"],
     "vx_gemm_profile": ["launches", "ms", "bytes", "flops"],
     "vx_speculative_stats": ["rounds", "drafted", "accepted", "emitted", "verify_ms", "draft_ms", "prefill_ms"],
+    "vxh_vocab_ws": ["part", "cnt", "stats", "max_rows"],
 }
 
 
@@ -66,6 +67,7 @@ def mirrors():
         ("vxh_pro", test_gpu_pro.Pro), ("vxh_pro", bench._Pro),
         ("vx_model_options", N.VxModelOptions), ("vx_synth_spec", N.VxSynthSpec),
         ("vx_gemm_profile", N.VxGemmProfile), ("vx_speculative_stats", N.VxSpecStats),
+        ("vxh_vocab_ws", N.VxhVocabWs),
     ]
 
 

@@ -1,5 +1,6 @@
-"""GPU acceptance sampling (vxh_row_stats / vxh_sample / vxh_accept) against
-the oracle on identical logits and uniforms.
+"""GPU acceptance sampling (vxh_row_stats / vxh_sample / vxh_accept, and
+their many-workgroup forms vxh_row_stats_mc / vxh_sample_keep_mc /
+vxh_accept_mc) against the oracle on identical logits and uniforms.
 
 Decisions must be identical.  A difference is accepted only as a certified
 tie: the uniform sits within 1e-5 of the acceptance ratio, or the fixed-point
@@ -27,6 +28,18 @@ def P():
     return L
 
 
+_WS = {}
+
+
+def vocab_ws(P):
+    """One many-workgroup workspace for the module (65 rows)."""
+    if "ws" not in _WS:
+        ws = N.VxhVocabWs()
+        assert P.vxh_vocab_ws_alloc(C.byref(ws), 65) == 0, P.vxh_last_error()
+        _WS["ws"] = ws
+    return _WS["ws"]
+
+
 def fixed(w):
     w = np.asarray(w, np.float64)
     return np.where(w > 0, np.floor(w * 2.0 ** 32 + 0.5), 0).astype(np.uint64)
@@ -45,11 +58,15 @@ def near_boundary(w, u):
     return bool(np.min(np.abs(c - thr)) <= 1e-6 * S + 2)
 
 
-def sample_gpu(P, l, T, top_p, u):
+def sample_gpu(P, l, T, top_p, u, mc=False):
     V = l.shape[0]
     dl, du = N.DevBuf(P, l), N.DevBuf(P, np.array([u], np.float32))
     dt, dn = N.DevBuf(P, nbytes=4), N.DevBuf(P, nbytes=32)
-    assert P.vxh_sample(dl.ptr, V, T, top_p, du.ptr, dt.ptr, dn.ptr, None) == 0, P.vxh_last_error()
+    if mc:
+        assert P.vxh_sample_keep_mc(dl.ptr, V, T, top_p, du.ptr, dt.ptr, dn.ptr, None, C.byref(vocab_ws(P)),
+                                    None) == 0, P.vxh_last_error()
+    else:
+        assert P.vxh_sample(dl.ptr, V, T, top_p, du.ptr, dt.ptr, dn.ptr, None) == 0, P.vxh_last_error()
     tok = int(dt.get(np.int32, 1)[0])
     nuc = dn.get(np.float32, 8)
     for b in (dl, du, dt, dn):
@@ -57,10 +74,12 @@ def sample_gpu(P, l, T, top_p, u):
     return tok, nuc
 
 
+@pytest.mark.parametrize("mc", [False, True])
 @pytest.mark.parametrize("V,T,top_p", [(32000, 0.8, 1.0), (32000, 1.0, 0.9), (5000, 0.7, 0.5),
-                                       (152064, 1.0, 1.0), (152064, 1.0, 0.95), (1000, 0.0, 1.0)])
-def test_sampler_matches_oracle(P, V, T, top_p):
-    print(f"sampler V={V} T={T} top_p={top_p}", flush=True)
+                                       (152064, 1.0, 1.0), (152064, 1.0, 0.95), (1000, 0.0, 1.0),
+                                       (70001, 0.9, 1.0)])
+def test_sampler_matches_oracle(P, V, T, top_p, mc):
+    print(f"sampler V={V} T={T} top_p={top_p} {'many workgroups' if mc else 'one workgroup'}", flush=True)
     rng = np.random.default_rng(V + int(T * 10) + int(top_p * 100))
     ties = boundary = 0
     for trial in range(6):
@@ -69,7 +88,7 @@ def test_sampler_matches_oracle(P, V, T, top_p):
             u = float(np.float32(u))
             q = np.zeros(V, np.float32)
             want = O.or_sample_top_p(l, V, T, top_p, u, q.ctypes.data_as(C.c_void_p))
-            got, nuc = sample_gpu(P, l, T, top_p, u)
+            got, nuc = sample_gpu(P, l, T, top_p, u, mc)
             if got != want:
                 w = np.where(q > 0, q, 0)
                 assert near_boundary(w, u), (trial, u, got, want)
@@ -115,7 +134,7 @@ def test_sample_keep_copies_the_row_and_draws_like_sample(P, V, T, top_p):
         b.free()
 
 
-def run_accept(P, L, D, drafts, T, top_p, u):
+def run_accept(P, L, D, drafts, T, top_p, u, mc=False):
     k = D.shape[0]
     V, Vd = L.shape[1], D.shape[1]
     dL, dD = N.DevBuf(P, L), N.DevBuf(P, D)
@@ -132,9 +151,15 @@ def run_accept(P, L, D, drafts, T, top_p, u):
         nj = C.c_void_p(dnuc.ptr.value + j * 32)
         assert P.vxh_sample(row, Vd, T, top_p, du1.ptr, dtok.ptr, nj, None) == 0
     du = N.DevBuf(P, np.asarray(u, np.float32))
-    assert P.vxh_row_stats(dL.ptr, V, k + 1, V, T, dstats.ptr, None) == 0
-    assert P.vxh_accept(dL.ptr, V, V, dstats.ptr, dD.ptr, Vd, Vd, dnuc.ptr, ddr.ptr, k, T, du.ptr,
-                        dout.ptr, None) == 0, P.vxh_last_error()
+    if mc:
+        ws = C.byref(vocab_ws(P))
+        assert P.vxh_row_stats_mc(dL.ptr, V, k + 1, V, T, dstats.ptr, ws, None) == 0, P.vxh_last_error()
+        assert P.vxh_accept_mc(dL.ptr, V, V, dstats.ptr, dD.ptr, Vd, Vd, dnuc.ptr, ddr.ptr, k, T, du.ptr,
+                               dout.ptr, ws, None) == 0, P.vxh_last_error()
+    else:
+        assert P.vxh_row_stats(dL.ptr, V, k + 1, V, T, dstats.ptr, None) == 0
+        assert P.vxh_accept(dL.ptr, V, V, dstats.ptr, dD.ptr, Vd, Vd, dnuc.ptr, ddr.ptr, k, T, du.ptr,
+                            dout.ptr, None) == 0, P.vxh_last_error()
     out = dout.get(np.int32, k + 3)
     for b in (dL, dD, dstats, dnuc, ddr, du1, dtok, dout, du):
         b.free()
@@ -159,10 +184,11 @@ def oracle_accept(L, D, drafts, T, top_p, u):
     return n, na.value, list(out[:n]), Q
 
 
+@pytest.mark.parametrize("mc", [False, True])
 @pytest.mark.parametrize("V,k,T,top_p", [(32000, 8, 0.8, 1.0), (32000, 4, 1.0, 0.95), (2000, 8, 0.8, 1.0),
                                          (32000, 8, 0.0, 1.0), (152064, 8, 1.0, 1.0)])
-def test_accept_matches_oracle(P, V, k, T, top_p):
-    print(f"accept V={V} k={k} T={T} top_p={top_p}", flush=True)
+def test_accept_matches_oracle(P, V, k, T, top_p, mc):
+    print(f"accept V={V} k={k} T={T} top_p={top_p} {'many workgroups' if mc else 'one workgroup'}", flush=True)
     rng = np.random.default_rng(V + k)
     ties, n_acc_total, n_cases = 0, 0, 12
     for case in range(n_cases):
@@ -178,7 +204,7 @@ def test_accept_matches_oracle(P, V, k, T, top_p):
                 am = int(np.argmax(L[j]))
                 drafts.append(am if rng.random() < 0.8 else (am + 1) % V)
         u = (rng.integers(0, 1 << 24, k + 1) / float(1 << 24)).astype(np.float32)
-        g = run_accept(P, L, D, drafts, T, top_p, u)
+        g = run_accept(P, L, D, drafts, T, top_p, u, mc)
         n, na, toks, Q = oracle_accept(L, D, drafts, T, top_p, u)
         n_acc_total += na
         if (g[0], g[1], g[2]) != (n, na, toks):
@@ -201,6 +227,53 @@ def test_accept_matches_oracle(P, V, k, T, top_p):
         assert 0 < n_acc_total < k * n_cases
 
 
+@pytest.mark.parametrize("V", [32000, 152064, 1500])
+def test_many_workgroup_kernels_equal_one_workgroup_kernels(P, V):
+    """Row statistics (argmax bit-equal; max and sum within fp32 rounding of
+    each other), the draw and the decision of the many-workgroup kernels
+    against the one-workgroup kernels on the same inputs: the same tokens
+    wherever the fixed-point threshold is not within rounding of a token
+    boundary; each launch leaves the workspace's counters at zero for the
+    next (they run back to back here)."""
+    print(f"many vs one workgroup V={V}", flush=True)
+    rng = np.random.default_rng(V)
+    ws = C.byref(vocab_ws(P))
+    R = 9
+    Lg = rng.normal(0, 2.0, (R, V)).astype(np.float32)
+    Lg[3, 7] = Lg[3].max() + 1.0      # a unique maximum early in a row
+    Lg[4, :] = 0.5                    # a flat row: argmax 0
+    dL = N.DevBuf(P, Lg)
+    s1, s2 = N.DevBuf(P, nbytes=4 * 3 * R), N.DevBuf(P, nbytes=4 * 3 * R)
+    for T in (0.8, 0.0):
+        assert P.vxh_row_stats(dL.ptr, V, R, V, T, s1.ptr, None) == 0
+        assert P.vxh_row_stats_mc(dL.ptr, V, R, V, T, s2.ptr, ws, None) == 0, P.vxh_last_error()
+        a, b = s1.get(np.float32, 3 * R).reshape(R, 3), s2.get(np.float32, 3 * R).reshape(R, 3)
+        assert np.array_equal(a[:, 2].view(np.int32), b[:, 2].view(np.int32))
+        assert np.array_equal(a[:, 0], b[:, 0])
+        assert np.allclose(a[:, 1], b[:, 1], rtol=1e-5, atol=0)
+    keep = N.DevBuf(P, nbytes=4 * V)
+    du, dt, dn = N.DevBuf(P, nbytes=4), N.DevBuf(P, nbytes=4), N.DevBuf(P, nbytes=32)
+    same = 0
+    for trial in range(20):
+        u = np.array([rng.integers(0, 1 << 24) / float(1 << 24)], np.float32)
+        P.vxh_upload(du.ptr, u.ctypes.data_as(C.c_void_p), 4, None)
+        row = C.c_void_p(dL.ptr.value + 4 * V * (trial % R))
+        assert P.vxh_sample_keep(row, V, 0.8, 1.0, du.ptr, dt.ptr, dn.ptr, None, None) == 0
+        t1 = int(dt.get(np.int32, 1)[0])
+        assert P.vxh_sample_keep_mc(row, V, 0.8, 1.0, du.ptr, dt.ptr, dn.ptr, keep.ptr, ws, None) == 0
+        t2 = int(dt.get(np.int32, 1)[0])
+        assert np.array_equal(keep.get(np.float32, V), Lg[trial % R])
+        if t1 == t2:
+            same += 1
+        else:
+            p = np.exp((Lg[trial % R].astype(np.float64) - Lg[trial % R].max()) / 0.8)
+            assert near_boundary(p / p.sum(), float(u[0])), (trial, t1, t2)
+    print(f"draws equal: {same} of 20")
+    assert same >= 18
+    for b in (dL, s1, s2, keep, du, dt, dn):
+        b.free()
+
+
 def test_argmax_of_rows_without_a_maximum_is_index_zero(P):
     """A row with no value above -inf (all NaN, all -inf) has no first max;
     the kernels return index 0 (the reference's scan stays on its first
@@ -212,9 +285,13 @@ def test_argmax_of_rows_without_a_maximum_is_index_zero(P):
     assert P.vxh_row_stats(dL.ptr, V, 2, V, 1.0, dstats.ptr, None) == 0, P.vxh_last_error()
     st = dstats.get(np.float32, 6)
     assert st[2:3].view(np.int32)[0] == 0 and st[5:6].view(np.int32)[0] == 0
+    assert P.vxh_row_stats_mc(dL.ptr, V, 2, V, 1.0, dstats.ptr, C.byref(vocab_ws(P)), None) == 0
+    st = dstats.get(np.float32, 6)
+    assert st[2:3].view(np.int32)[0] == 0 and st[5:6].view(np.int32)[0] == 0
     for T in (0.0, 1.0):
         for r in rows:
-            tok, _ = sample_gpu(P, r, T, 1.0, 0.5)
-            assert 0 <= tok < V
+            for mc in (False, True):
+                tok, _ = sample_gpu(P, r, T, 1.0, 0.5, mc)
+                assert 0 <= tok < V
     dL.free()
     dstats.free()

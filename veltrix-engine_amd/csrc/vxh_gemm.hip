@@ -456,6 +456,13 @@ __global__ __launch_bounds__(VX_SWC_THREADS) void vx_swiglu_chunk_kernel(
 extern "C" int vxh_swiglu_panel_norm(double *acc, int ld_acc, int M, int F, float thr, const double *ss_in,
                                      int ss_K, double *clear, size_t n_clear, vxh_panel *p, vxh_stream s)
 {
+    return vxh_swiglu_panel_norm_timed(acc, ld_acc, M, F, thr, ss_in, ss_K, clear, n_clear, p, nullptr, nullptr, s);
+}
+
+extern "C" int vxh_swiglu_panel_norm_timed(double *acc, int ld_acc, int M, int F, float thr, const double *ss_in,
+                                           int ss_K, double *clear, size_t n_clear, vxh_panel *p, vxh_event e0,
+                                           vxh_event e1, vxh_stream s)
+{
     int rc = vx_row_check(p, M, F, "swiglu_panel_norm");
     if (rc) return rc;
     if (ss_in && ss_K < 1) return vxh_fail(VXH_ERR_PARAM, "swiglu_panel_norm: norm length %d", ss_K);
@@ -464,9 +471,14 @@ extern "C" int vxh_swiglu_panel_norm(double *acc, int ld_acc, int M, int F, floa
     p->M = M;
     p->avx2 = 0;
     p->rs_ld = chunks;
-    vx_swiglu_chunk_kernel<<<dim3(chunks, M), VX_SWC_THREADS, 0, vxh_hs(s)>>>(
-        acc, ld_acc, M, F, thr, ss_in, ss_K, (uint4 *)p->data, p->rscale, chunks, n_clear ? clear : nullptr,
-        (long)n_clear);
+    if (e0 || e1)   // events recorded by the dispatch itself around the kernel
+        hipExtLaunchKernelGGL(vx_swiglu_chunk_kernel, dim3(chunks, M), dim3(VX_SWC_THREADS), 0, vxh_hs(s),
+                              (hipEvent_t)e0, (hipEvent_t)e1, 0, acc, ld_acc, M, F, thr, ss_in, ss_K,
+                              (uint4 *)p->data, p->rscale, chunks, n_clear ? clear : nullptr, (long)n_clear);
+    else
+        vx_swiglu_chunk_kernel<<<dim3(chunks, M), VX_SWC_THREADS, 0, vxh_hs(s)>>>(
+            acc, ld_acc, M, F, thr, ss_in, ss_K, (uint4 *)p->data, p->rscale, chunks, n_clear ? clear : nullptr,
+            (long)n_clear);
     VXH_LAUNCHED();
     return VXH_OK;
 }

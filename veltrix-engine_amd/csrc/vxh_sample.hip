@@ -8,6 +8,8 @@
 // max(1, ceil(U*S/2^24)) for the uniform u = U/2^24.  Integer prefix sums do
 // not depend on the summation order, so the GPU and a sequential CPU pick the
 // same token from the same w.
+#include <cstring>
+
 #include "vxh_internal.h"
 
 #define SB 1024   // threads per sampling workgroup
@@ -857,6 +859,516 @@ extern "C" int vxh_accept(const float *L, int ldl, int V, const float *stats, co
         vx_accept_reg_kernel<<<1, SB, 0, vxh_hs(s)>>>(L, ldl, V, stats, D, ldd, Vd, nuc, drafts, k, T, u, out);
     else
         vx_accept_kernel<<<1, SB, 0, vxh_hs(s)>>>(L, ldl, V, stats, D, ldd, Vd, nuc, drafts, k, T, u, out);
+    VXH_LAUNCHED();
+    return VXH_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Multi-workgroup vocab kernels
+// ---------------------------------------------------------------------------
+// A row of V entries is cut into G <= 64 chunks of CH entries (CH a multiple
+// of 1024), one 256-thread workgroup per chunk.  Each workgroup writes its
+// chunk's partial result into the caller's workspace with device-coherent
+// stores, waits until they have completed, and counts itself in with an
+// atomic add; the workgroup that arrives last reads every partial with
+// device-coherent loads, finishes the row in chunk order and sets the
+// counter back to zero for the next launch.  No workgroup ever waits for
+// another (no grid barrier, no co-residency assumption).  Fixed-point masses
+// are integers, so their sums, and the token an inverse CDF lands on, do
+// not depend on the chunking.
+#define MB 256          // threads per workgroup
+#define MC_MAX_G 64     // chunks per row
+
+static int vx_mc_chunk(int V)
+{
+    const int per = (V + 1024 * MC_MAX_G - 1) / (1024 * MC_MAX_G);
+    return 1024 * (per > 0 ? per : 1);
+}
+
+__device__ __forceinline__ void vx_st_coh(uint64_t *p, uint64_t v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t vx_ld_coh(uint64_t *p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// True in the last of G workgroups to arrive.  Every thread waits until its
+// own (device-coherent) stores have completed before the workgroup counts
+// itself in, so the last one's coherent loads see every partial.
+__device__ __forceinline__ bool vx_arrive_last(unsigned *cnt, unsigned G, int *s_last)
+{
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0)
+        *s_last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == G - 1;
+    __syncthreads();
+    return *s_last != 0;
+}
+
+__device__ __forceinline__ void vx_mc_release(unsigned *cnt)
+{
+    if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// 256-thread reductions (4 wavefronts, combined in wave order)
+__device__ __forceinline__ int vx_mb_argmax(float v, int idx, float *rv, int *ri, float *vmax, bool *found)
+{
+    vx_wave_argmax64(v, idx);
+    if ((threadIdx.x & 63) == 0) { rv[threadIdx.x >> 6] = v; ri[threadIdx.x >> 6] = idx; }
+    __syncthreads();
+    float bv = rv[0];
+    int bi = ri[0];
+    for (int i = 1; i < MB / 64; i++)
+        if (rv[i] > bv || (rv[i] == bv && ri[i] < bi)) { bv = rv[i]; bi = ri[i]; }
+    __syncthreads();
+    *vmax = bv;
+    *found = bi != 0x7fffffff;
+    return bi;
+}
+
+__device__ __forceinline__ float vx_mb_sum(float v, float *r)
+{
+    v = vx_wave_sum64(v);
+    if ((threadIdx.x & 63) == 0) r[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float s = r[0];
+    for (int i = 1; i < MB / 64; i++) s += r[i];
+    __syncthreads();
+    return s;
+}
+
+__device__ __forceinline__ uint64_t vx_mb_sum_u64(uint64_t v, uint64_t *r)
+{
+    for (int o = 32; o > 0; o >>= 1) v += vx_shfl_xor_u64(v, o);
+    if ((threadIdx.x & 63) == 0) r[threadIdx.x >> 6] = v;
+    __syncthreads();
+    uint64_t s = 0;
+    for (int i = 0; i < MB / 64; i++) s += r[i];
+    __syncthreads();
+    return s;
+}
+
+// Inverse CDF inside chunk [b, e) given the mass `before` of the chunks
+// ahead of it: thread t sums the masses of its contiguous entries, a
+// workgroup scan places the threshold, and that thread walks its entries.
+// Returns the first index whose inclusive prefix reaches thr (e - 1 if the
+// chunk's masses never reach it).
+template <typename WF>
+__device__ int vx_mb_land(int b, int e, uint64_t before, uint64_t thr, WF W, uint64_t *r, int *res)
+{
+    const int per = (e - b + MB - 1) / MB;
+    const int tb = b + threadIdx.x * per, te = min(tb + per, e);
+    uint64_t mine = 0;
+    for (int v = tb; v < te; v++) mine += W(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint64_t incl = mine;
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint64_t y = vx_shfl_up_u64(incl, o);
+        if (lane >= o) incl += y;
+    }
+    if (lane == 63) r[wave] = incl;
+    if (threadIdx.x == 0) *res = e - 1;
+    __syncthreads();
+    uint64_t off = before;
+    for (int w = 0; w < wave; w++) off += r[w];
+    const uint64_t excl = off + incl - mine;
+    if (mine && excl < thr && excl + mine >= thr) {
+        uint64_t c = excl;
+        for (int v = tb; v < te; v++) {
+            c += W(v);
+            if (c >= thr) { *res = v; break; }
+        }
+    }
+    __syncthreads();
+    const int t = *res;
+    __syncthreads();
+    return t;
+}
+
+// Row statistics, chunked: stats[r] = {max, sum exp((l - max)/T), argmax}.
+// A chunk keeps its own maximum m_c and sum s_c = sum exp((l - m_c)/T); the
+// last workgroup of the row takes the first maximum over the chunks and
+// S = sum_c s_c exp((m_c - M)/T) in chunk order.  A row with no value above
+// -inf gives argmax 0, max l[0] and (T > 0) sum NaN, as one pass over it
+// with that maximum would.  keep (optional, one row): a copy of the row.
+template <bool KEEP>
+__global__ __launch_bounds__(MB) void vx_stats_mc_kernel(const float *__restrict__ L, int ldl, int V, float T,
+                                                         int CH, float *__restrict__ stats, uint64_t *part,
+                                                         unsigned *cnt, float *__restrict__ keep)
+{
+    __shared__ float rv[MB / 64];
+    __shared__ int ri[MB / 64];
+    __shared__ float sm[MC_MAX_G], ss[MC_MAX_G];
+    __shared__ int sa[MC_MAX_G], sf[MC_MAX_G];
+    __shared__ int s_last;
+    const int r = blockIdx.y, c = blockIdx.x, G = gridDim.x;
+    const float *l = L + (size_t)r * ldl;
+    const int b0 = c * CH, b1 = min(b0 + CH, V);
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int v0 = b0 + 4 * (int)threadIdx.x; v0 < b1; v0 += 4 * MB) {
+        float x[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) x[e] = l[min(v0 + e, b1 - 1)];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int v = v0 + e;
+            if (KEEP && v < b1) keep[v] = x[e];
+            const bool better = (v < b1) & ((x[e] > bv) | ((x[e] == bv) & (v < bi)));
+            bv = better ? x[e] : bv;
+            bi = better ? v : bi;
+        }
+    }
+    float mc;
+    bool fc;
+    const int ac = vx_mb_argmax(bv, bi, rv, ri, &mc, &fc);
+    float s = 0.0f;
+    if (T > 0.0f && fc)
+        for (int v = b0 + (int)threadIdx.x; v < b1; v += MB) s += expf((l[v] - mc) / T);
+    s = vx_mb_sum(s, rv);
+    uint64_t *P = part + ((size_t)r * G + c) * 4;
+    if (threadIdx.x == 0) {
+        vx_st_coh(P + 0, (uint64_t)__float_as_uint(mc) | ((uint64_t)(fc ? 1 : 0) << 32));
+        vx_st_coh(P + 1, (uint64_t)__float_as_uint(s));
+        vx_st_coh(P + 2, (uint64_t)(uint32_t)ac);
+    }
+    if (!vx_arrive_last(&cnt[r], (unsigned)G, &s_last)) return;
+    if ((int)threadIdx.x < G) {
+        uint64_t *Q = part + ((size_t)r * G + threadIdx.x) * 4;
+        const uint64_t w0 = vx_ld_coh(Q + 0);
+        sm[threadIdx.x] = __uint_as_float((uint32_t)w0);
+        sf[threadIdx.x] = (int)(w0 >> 32);
+        ss[threadIdx.x] = __uint_as_float((uint32_t)vx_ld_coh(Q + 1));
+        sa[threadIdx.x] = (int)(uint32_t)vx_ld_coh(Q + 2);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float M = -INFINITY;
+        int A = 0x7fffffff;
+        bool found = false;
+        for (int i = 0; i < G; i++)
+            if (sf[i] && (sm[i] > M || (sm[i] == M && sa[i] < A))) { M = sm[i]; A = sa[i]; found = true; }
+        if (!found) { A = 0; M = l[0]; }
+        float S = 0.0f;
+        if (T > 0.0f) {
+            if (found) {
+                for (int i = 0; i < G; i++)
+                    if (sf[i]) S += ss[i] * expf((sm[i] - M) / T);
+            } else {
+                S = __builtin_nanf("");
+            }
+        }
+        stats[r * 3 + 0] = M;
+        stats[r * 3 + 1] = S;
+        stats[r * 3 + 2] = __int_as_float(A);
+    }
+    vx_mc_release(&cnt[r]);
+}
+
+// The draft draw without a nucleus, chunked (vx_sample_reg_kernel's
+// arithmetic): p_v = expf((l_v - max)/T) * inv, inv = 1/(sum + 1e-30) from
+// the row statistics, masses W_v = round(p_v * 2^32), token = inverse CDF.
+__global__ __launch_bounds__(MB) void vx_draw_mc_kernel(const float *__restrict__ l, int V, float T, int CH,
+                                                        const float *__restrict__ stats,
+                                                        const float *__restrict__ u, int *__restrict__ token_out,
+                                                        float *__restrict__ nuc, uint64_t *part, unsigned *cnt)
+{
+    __shared__ uint64_t r64[MB / 64];
+    __shared__ uint64_t tot[MC_MAX_G];
+    __shared__ int s_last, res;
+    __shared__ int s_c;
+    __shared__ uint64_t s_before, s_S, s_thr;
+    const int c = blockIdx.x, G = gridDim.x;
+    const float mx = stats[0], sum = stats[1];
+    const int am = __float_as_int(stats[2]);
+    if (!(T > 0.0f)) {
+        if (c == 0 && threadIdx.x == 0) {
+            token_out[0] = am;
+            nuc[0] = mx; nuc[1] = 0.0f; nuc[2] = -1.0f; nuc[3] = __int_as_float(V - 1);
+            nuc[4] = 0.0f; nuc[5] = __int_as_float(am); nuc[6] = 0.0f; nuc[7] = 0.0f;
+        }
+        return;
+    }
+    const float inv = 1.0f / (sum + 1e-30f);
+    auto W = [&](int v) -> uint64_t { return vx_fixed32(expf((l[v] - mx) / T) * inv); };
+    const int b0 = c * CH, b1 = min(b0 + CH, V);
+    uint64_t t = 0;
+    for (int v = b0 + (int)threadIdx.x; v < b1; v += MB) t += W(v);
+    t = vx_mb_sum_u64(t, r64);
+    if (threadIdx.x == 0) vx_st_coh(part + c, t);
+    if (!vx_arrive_last(cnt, (unsigned)G, &s_last)) return;
+    if ((int)threadIdx.x < G) tot[threadIdx.x] = vx_ld_coh(part + threadIdx.x);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t S = 0;
+        for (int i = 0; i < G; i++) S += tot[i];
+        s_S = S;
+        s_c = -1;
+        if (S > 0) {
+            const uint64_t thr = vx_threshold(u[0], S);
+            uint64_t acc = 0;
+            for (int i = 0; i < G; i++) {
+                if (acc + tot[i] >= thr) { s_c = i; break; }
+                acc += tot[i];
+            }
+            s_before = acc;
+            s_thr = thr;
+        }
+    }
+    __syncthreads();
+    int tok = am;
+    if (s_c >= 0) {
+        const int lb = s_c * CH, le = min(lb + CH, V);
+        tok = vx_mb_land(lb, le, s_before, s_thr, W, r64, &res);
+    }
+    if (threadIdx.x == 0) {
+        token_out[0] = tok;
+        nuc[0] = mx; nuc[1] = inv; nuc[2] = -1.0f; nuc[3] = __int_as_float(V - 1);
+        nuc[4] = (float)((double)s_S / 4294967296.0); nuc[5] = __int_as_float(am);
+        nuc[6] = 0.0f; nuc[7] = 0.0f;
+    }
+    vx_mc_release(cnt);
+}
+
+// The verify decision, chunked (vx_accept_kernel's arithmetic).  Every
+// workgroup runs the k ratio tests (the first failing draft is the decided
+// row j), then sums the fixed-point masses of its chunk of row j -- the
+// residual max(0, p - q) at a rejection, p for the bonus draw -- and, at a
+// rejection, the chunk's first maximum of the residual (the draw when the
+// residual has no mass).  The last workgroup places the threshold.
+__global__ __launch_bounds__(MB) void vx_accept_mc_kernel(const float *__restrict__ L, int ldl, int V,
+                                                          const float *__restrict__ stats,
+                                                          const float *__restrict__ D, int ldd, int Vd,
+                                                          const float *__restrict__ nuc,
+                                                          const int *__restrict__ drafts, int k, float T,
+                                                          const float *__restrict__ u, int *__restrict__ out, int CH,
+                                                          uint64_t *part, unsigned *cnt)
+{
+    __shared__ float rv[MB / 64];
+    __shared__ int ri[MB / 64];
+    __shared__ uint64_t r64[MB / 64];
+    __shared__ uint64_t tot[MC_MAX_G];
+    __shared__ float cmv[MC_MAX_G];
+    __shared__ int cmi[MC_MAX_G];
+    __shared__ int s_last, res, s_j, s_c;
+    __shared__ uint64_t s_before, s_thr;
+    const int c = blockIdx.x, G = gridDim.x;
+    if (!(T > 0.0f)) {
+        // greedy: accept d_j while it is the first argmax of L_j
+        if (c == 0 && threadIdx.x == 0) {
+            int j = 0;
+            for (; j < k; j++) {
+                const int a = __float_as_int(stats[j * 3 + 2]);
+                out[2 + j] = a;
+                if (a != drafts[j]) break;
+            }
+            if (j == k) out[2 + k] = __float_as_int(stats[k * 3 + 2]);
+            out[0] = j < k ? j + 1 : k + 1;
+            out[1] = j;
+        }
+        return;
+    }
+    if (threadIdx.x < 64) {
+        // ratio tests of the drafts on parallel lanes; the first failing one
+        // is where the sequential scan (src/speculative.c:199-200) stops
+        const int lane = threadIdx.x;
+        bool rej = true;
+        if (lane < k) {
+            const float *lj = L + (size_t)lane * ldl;
+            const float mx = stats[lane * 3 + 0], inv = 1.0f / (stats[lane * 3 + 1] + 1e-30f);
+            const int d = drafts[lane];
+            const float pt = (d >= 0 && d < V) ? expf((lj[d] - mx) / T) * inv : 0.0f;
+            const float qd = (d >= 0 && d < Vd) ? vx_draft_q(D + (size_t)lane * ldd, nuc + lane * 8, d, T) : 0.0f;
+            const float alpha = fminf(1.0f, pt / fmaxf(qd, 1e-10f));
+            rej = !(u[lane] < alpha);
+        }
+        const uint64_t bal = __ballot(rej);
+        int j = bal ? __builtin_ctzll(bal) : 64;
+        if (lane == 0) {
+            for (; j < k; j++) {   // only k > 64
+                const float *lj = L + (size_t)j * ldl;
+                const float mx = stats[j * 3 + 0], inv = 1.0f / (stats[j * 3 + 1] + 1e-30f);
+                const int d = drafts[j];
+                const float pt = (d >= 0 && d < V) ? expf((lj[d] - mx) / T) * inv : 0.0f;
+                const float qd = (d >= 0 && d < Vd) ? vx_draft_q(D + (size_t)j * ldd, nuc + j * 8, d, T) : 0.0f;
+                const float alpha = fminf(1.0f, pt / fmaxf(qd, 1e-10f));
+                if (!(u[j] < alpha)) break;
+            }
+            s_j = min(j, k);
+        }
+    }
+    __syncthreads();
+    const int j = s_j;
+    const bool resample = j < k;
+    const float *lj = L + (size_t)j * ldl;
+    const float mx = stats[j * 3 + 0], inv = 1.0f / (stats[j * 3 + 1] + 1e-30f);
+    const float *dj = D + (size_t)min(j, k - 1) * ldd;
+    const vx_nuc nq = vx_nuc_load(nuc + min(j, k - 1) * 8);
+    auto X = [&](int v) -> float {
+        const float p = expf((lj[v] - mx) / T) * inv;
+        if (!resample) return p;
+        const float q = v < Vd ? vx_draft_q_of(dj[v], nq, v, T) : 0.0f;
+        return fmaxf(0.0f, p - q);
+    };
+    auto W = [&](int v) -> uint64_t { return vx_fixed32(X(v)); };
+    const int b0 = c * CH, b1 = min(b0 + CH, V);
+    uint64_t t = 0;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int v = b0 + (int)threadIdx.x; v < b1; v += MB) {
+        const float x = X(v);
+        t += vx_fixed32(x);
+        const bool better = (x > bv) | ((x == bv) & (v < bi));
+        bv = better ? x : bv;
+        bi = better ? v : bi;
+    }
+    t = vx_mb_sum_u64(t, r64);
+    float cv = -INFINITY;
+    bool cf = false;
+    int ci = 0x7fffffff;
+    if (resample) ci = vx_mb_argmax(bv, bi, rv, ri, &cv, &cf);
+    uint64_t *P = part + (size_t)c * 3;
+    if (threadIdx.x == 0) {
+        vx_st_coh(P + 0, t);
+        vx_st_coh(P + 1, (uint64_t)__float_as_uint(cv));
+        vx_st_coh(P + 2, (uint64_t)(uint32_t)ci);
+    }
+    if (!vx_arrive_last(cnt, (unsigned)G, &s_last)) return;
+    if ((int)threadIdx.x < G) {
+        uint64_t *Q = part + (size_t)threadIdx.x * 3;
+        tot[threadIdx.x] = vx_ld_coh(Q + 0);
+        cmv[threadIdx.x] = __uint_as_float((uint32_t)vx_ld_coh(Q + 1));
+        cmi[threadIdx.x] = (int)(uint32_t)vx_ld_coh(Q + 2);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t S = 0;
+        for (int i = 0; i < G; i++) S += tot[i];
+        s_c = -1;
+        if (S > 0) {
+            const uint64_t thr = vx_threshold(u[k], S);
+            uint64_t acc = 0;
+            for (int i = 0; i < G; i++) {
+                if (acc + tot[i] >= thr) { s_c = i; break; }
+                acc += tot[i];
+            }
+            s_before = acc;
+            s_thr = thr;
+        }
+    }
+    __syncthreads();
+    int tok;
+    if (s_c >= 0) {
+        const int lb = s_c * CH, le = min(lb + CH, V);
+        tok = vx_mb_land(lb, le, s_before, s_thr, W, r64, &res);
+    } else if (resample) {
+        // no residual mass: the residual's first maximum over the chunks
+        float M = -INFINITY;
+        int A = 0x7fffffff;
+        for (int i = 0; i < G; i++)
+            if (cmv[i] > M || (cmv[i] == M && cmi[i] < A)) { M = cmv[i]; A = cmi[i]; }
+        tok = A == 0x7fffffff ? 0 : A;
+    } else {
+        tok = __float_as_int(stats[j * 3 + 2]);
+    }
+    if (threadIdx.x == 0) {
+        for (int i = 0; i < j; i++) out[2 + i] = drafts[i];
+        out[2 + j] = tok;
+        out[0] = j + 1;
+        out[1] = j;
+    }
+    vx_mc_release(cnt);
+}
+
+// Workspace: partials [max_rows + 2][MC_MAX_G][4] u64 -- regions 0 ..
+// max_rows-1 for the rows of the statistics, region max_rows for the draw,
+// max_rows + 1 for the decision -- then counters [max_rows + 2] in the same
+// order, then 16 floats of the sampler's row statistics.
+extern "C" int vxh_vocab_ws_alloc(vxh_vocab_ws *ws, int max_rows)
+{
+    if (!ws || max_rows < 1 || max_rows > 1024) return vxh_fail(VXH_ERR_PARAM, "vocab_ws_alloc: max_rows %d", max_rows);
+    memset(ws, 0, sizeof(*ws));
+    const size_t part = ((size_t)max_rows + 2) * MC_MAX_G * 4 * sizeof(uint64_t);
+    const size_t cnt = ((size_t)max_rows + 2) * sizeof(unsigned);
+    const size_t bytes = part + cnt + 16 * sizeof(float);
+    void *p = nullptr;
+    int rc = vxh_malloc(&p, bytes);
+    if (rc) return rc;
+    VXH_CHECK(hipMemset(p, 0, bytes));
+    VXH_CHECK(hipDeviceSynchronize());
+    ws->part = p;
+    ws->cnt = (unsigned *)((char *)p + part);
+    ws->stats = (float *)((char *)p + part + cnt);
+    ws->max_rows = max_rows;
+    return VXH_OK;
+}
+
+extern "C" void vxh_vocab_ws_free(vxh_vocab_ws *ws)
+{
+    if (!ws) return;
+    vxh_free(ws->part);
+    memset(ws, 0, sizeof(*ws));
+}
+
+static int vx_ws_check(const vxh_vocab_ws *ws, int rows, const char *what)
+{
+    if (!ws || !ws->part || rows > ws->max_rows)
+        return vxh_fail(VXH_ERR_PARAM, "%s: workspace for %d rows, %d needed", what, ws ? ws->max_rows : 0, rows);
+    return VXH_OK;
+}
+
+extern "C" int vxh_row_stats_mc(const float *L, int ldl, int R, int V, float T, float *stats, vxh_vocab_ws *ws,
+                                vxh_stream s)
+{
+    if (R <= 0) return VXH_OK;
+    if (V <= 0 || ldl < V) return vxh_fail(VXH_ERR_PARAM, "row_stats_mc: V %d ldl %d", V, ldl);
+    int rc = vx_ws_check(ws, R, "row_stats_mc");
+    if (rc) return rc;
+    const int CH = vx_mc_chunk(V), G = (V + CH - 1) / CH;
+    vx_stats_mc_kernel<false><<<dim3(G, R), MB, 0, vxh_hs(s)>>>(L, ldl, V, T, CH, stats, (uint64_t *)ws->part,
+                                                                ws->cnt, nullptr);
+    VXH_LAUNCHED();
+    return VXH_OK;
+}
+
+extern "C" int vxh_sample_keep_mc(const float *l, int V, float T, float top_p, const float *u_dev, int *token_out,
+                                  float *nuc, float *keep, vxh_vocab_ws *ws, vxh_stream s)
+{
+    if (V <= 0) return vxh_fail(VXH_ERR_PARAM, "sample_mc: V %d", V);
+    if (top_p < 1.0f) return vxh_sample_keep(l, V, T, top_p, u_dev, token_out, nuc, keep, s);
+    int rc = vx_ws_check(ws, 1, "sample_mc");
+    if (rc) return rc;
+    if (keep == l) keep = nullptr;
+    const int CH = vx_mc_chunk(V), G = (V + CH - 1) / CH;
+    uint64_t *part = (uint64_t *)ws->part;
+    // row statistics in row 0's slots, the draw's chunk totals in the region after them
+    if (keep)
+        vx_stats_mc_kernel<true><<<dim3(G, 1), MB, 0, vxh_hs(s)>>>(l, V, V, T, CH, ws->stats, part, ws->cnt, keep);
+    else
+        vx_stats_mc_kernel<false><<<dim3(G, 1), MB, 0, vxh_hs(s)>>>(l, V, V, T, CH, ws->stats, part, ws->cnt,
+                                                                     nullptr);
+    VXH_LAUNCHED();
+    vx_draw_mc_kernel<<<G, MB, 0, vxh_hs(s)>>>(l, V, T, CH, ws->stats, u_dev, token_out, nuc,
+                                               part + (size_t)ws->max_rows * MC_MAX_G * 4,
+                                               ws->cnt + ws->max_rows);
+    VXH_LAUNCHED();
+    return VXH_OK;
+}
+
+extern "C" int vxh_accept_mc(const float *L, int ldl, int V, const float *stats, const float *D, int ldd, int Vd,
+                             const float *nuc, const int *drafts, int k, float T, const float *u, int *out,
+                             vxh_vocab_ws *ws, vxh_stream s)
+{
+    if (k < 0 || V <= 0) return vxh_fail(VXH_ERR_PARAM, "accept_mc: k %d V %d", k, V);
+    if (T > 0.0f && k == 0) return vxh_accept(L, ldl, V, stats, D, ldd, Vd, nuc, drafts, k, T, u, out, s);
+    int rc = vx_ws_check(ws, 1, "accept_mc");
+    if (rc) return rc;
+    const int CH = vx_mc_chunk(V), G = (V + CH - 1) / CH;
+    vx_accept_mc_kernel<<<G, MB, 0, vxh_hs(s)>>>(L, ldl, V, stats, D, ldd, Vd, nuc, drafts, k, T, u, out, CH,
+                                                 (uint64_t *)ws->part + ((size_t)ws->max_rows + 1) * MC_MAX_G * 4,
+                                                 ws->cnt + ws->max_rows + 1);
     VXH_LAUNCHED();
     return VXH_OK;
 }

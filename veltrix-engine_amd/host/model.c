@@ -787,6 +787,25 @@ static vx_error prof_slot(vx_dev *d, const vxh_qmat *W, int M, int n_out, int cl
     return VX_OK;
 }
 
+/* Profiling slot of a SwiGLU panel launch of M rows of F columns. */
+static vx_error prof_slot_panel(vx_dev *d, int M, int F, vxh_event *e0, vxh_event *e1)
+{
+    *e0 = *e1 = NULL;
+    if (!d->prof_on) return VX_OK;
+    if (d->prof_tick[VX_PROF_SWIGLU]++ % d->prof_on) return VX_OK;
+    if (d->prof_n == d->prof_cap) {
+        vx_error e = prof_fold(d);
+        if (e != VX_OK) return e;
+    }
+    int slot = d->prof_n++;
+    d->prof_cls[slot] = VX_PROF_SWIGLU;
+    d->prof_bytes[slot] = 16.0 * M * F + 4.0 * M * F;
+    d->prof_flops[slot] = 0.0;
+    *e0 = d->prof_ev[2 * slot];
+    *e1 = d->prof_ev[2 * slot + 1];
+    return VX_OK;
+}
+
 /* acc[m][n] += scale * (W x_m)[n] for n < n_out (fp64 accumulator). */
 static vx_error gemm(vx_dev *d, const vxh_qmat *W, vxh_panel *P, int M, double *acc, int ld_acc,
                      int n_out, int cls, int rows_logical)
@@ -944,8 +963,10 @@ static vx_error forward_pro(vx_model *m, int M, int n_past, int logits_mode)
             /* verify batches: the SwiGLU panel once per forward (each of the
              * down GEMM's tile groups would rebuild its slice from the fp64
              * gate/up sums); the panel launch clears acc_gu and acc_y */
-            TRY(vxh_swiglu_panel_norm(d->acc_gu, d->ld_gu, M, d->F, d->opt.ffn_gate_threshold, SS(l, 1), dd,
-                                      d->acc_y, (size_t)M * dd, &d->pan_f, s));
+            vxh_event pe0, pe1;
+            if ((e = prof_slot_panel(d, M, d->F, &pe0, &pe1))) return e;
+            TRY(vxh_swiglu_panel_norm_timed(d->acc_gu, d->ld_gu, M, d->F, d->opt.ffn_gate_threshold, SS(l, 1),
+                                            dd, d->acc_y, (size_t)M * dd, &d->pan_f, pe0, pe1, s));
             if ((e = gemm(d, &Ld->wd, &d->pan_f, M, d->acc_x, dd, dd, VX_PROF_DOWN, dd))) return e;
         } else {
             memset(&p, 0, sizeof(p));

@@ -42,6 +42,8 @@ struct vx_speculative_state {
     float *u_verify;    /* device [k+1]                                */
     int *dtok;          /* device [k+1]: t0, d_0 .. d_{k-1}            */
     int *out_dev;       /* device [k+3]                                */
+    vxh_vocab_ws ws_d, ws_t; /* many-workgroup sampling workspaces, one per
+                                model stream (draft draws, verify decision) */
     int *out_host;
     float *uh;
     vx_speculative_stats st;
@@ -80,7 +82,8 @@ vx_speculative_state *vx_speculative_create(vx_model *draft, vx_model *target, i
              vxh_malloc((void **)&s->u_draft, sizeof(float) * (size_t)k) == VXH_OK &&
              vxh_malloc((void **)&s->u_verify, sizeof(float) * (size_t)(k + 1)) == VXH_OK &&
              vxh_malloc((void **)&s->dtok, sizeof(int) * (size_t)(k + 1)) == VXH_OK &&
-             vxh_malloc((void **)&s->out_dev, sizeof(int) * (size_t)(k + 3)) == VXH_OK;
+             vxh_malloc((void **)&s->out_dev, sizeof(int) * (size_t)(k + 3)) == VXH_OK &&
+             vxh_vocab_ws_alloc(&s->ws_d, 1) == VXH_OK && vxh_vocab_ws_alloc(&s->ws_t, k + 1) == VXH_OK;
     s->out_host = (int *)calloc((size_t)(k + 3), sizeof(int));
     s->uh = (float *)calloc((size_t)(k + 1), sizeof(float));
     if (!ok || !s->out_host || !s->uh) {
@@ -95,6 +98,8 @@ void vx_speculative_destroy(vx_speculative_state *s)
     if (!s) return;
     vxh_free(s->D); vxh_free(s->nuc); vxh_free(s->u_draft); vxh_free(s->u_verify);
     vxh_free(s->dtok); vxh_free(s->out_dev);
+    vxh_vocab_ws_free(&s->ws_d);
+    vxh_vocab_ws_free(&s->ws_t);
     free(s->out_host);
     free(s->uh);
     free(s->committed);
@@ -226,8 +231,8 @@ int vx_speculative_decode(vx_speculative_state *s, int *output, int max_tokens)
             for (int i = 0; i < kk; i++) {
                 dd->logits = s->D + (size_t)i * Vd;
                 if (i > 0) CHKE(vx_dev_forward_ids(dm, s->dtok + i, 1, n + i - 1, VX_LOGITS_LAST));
-                CHK(vxh_sample_keep(dd->logits, Vd, T, s->top_p, s->u_draft + i, s->dtok + 1 + i,
-                                    s->nuc + 8 * i, dd->logits, dd->stream));
+                CHK(vxh_sample_keep_mc(dd->logits, Vd, T, s->top_p, s->u_draft + i, s->dtok + 1 + i,
+                                       s->nuc + 8 * i, dd->logits, &s->ws_d, dd->stream));
             }
             dd->logits = dlogits;
             CHK(vxh_stream_sync(dd->stream));
@@ -238,13 +243,13 @@ int vx_speculative_decode(vx_speculative_state *s, int *output, int max_tokens)
         /* verify: one target forward over [t0, d_0 .. d_{kk-1}] */
         CHK(vxh_upload(s->dtok, &t_last, sizeof(int), td->stream));
         CHKE(vx_dev_forward_ids(tm, s->dtok, kk + 1, n - 1, VX_LOGITS_ALL));
-        CHK(vxh_row_stats(td->logits, Vt, kk + 1, Vt, T, td->stats, td->stream));
+        CHK(vxh_row_stats_mc(td->logits, Vt, kk + 1, Vt, T, td->stats, &s->ws_t, td->stream));
         for (int j = 0; j < kk; j++) s->uh[j] = vx_uniform(s->seed, 2, (uint64_t)round * (k + 1) + j);
         /* the resample / bonus draw always uses the stream's slot k */
         s->uh[kk] = vx_uniform(s->seed, 2, (uint64_t)round * (k + 1) + k);
         CHK(vxh_upload(s->u_verify, s->uh, sizeof(float) * (size_t)(kk + 1), td->stream));
-        CHK(vxh_accept(td->logits, Vt, Vt, td->stats, s->D, Vd, Vd, s->nuc, s->dtok + 1, kk, T,
-                       s->u_verify, s->out_dev, td->stream));
+        CHK(vxh_accept_mc(td->logits, Vt, Vt, td->stats, s->D, Vd, Vd, s->nuc, s->dtok + 1, kk, T,
+                          s->u_verify, s->out_dev, &s->ws_t, td->stream));
         CHK(vxh_download(s->out_host, s->out_dev, sizeof(int) * (size_t)(kk + 3), td->stream));
         s->st.verify_ms += vx_now_ms() - tb;
 
