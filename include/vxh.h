@@ -494,7 +494,9 @@ int vxh_accept(const float *L, int ldl, int V, const float *stats, const float *
  * :35-91 (vxh_sample, top_p >= 1) and the softmax statistics of :44-53.
  * The workspace holds the partials and completion counters (zeroed at
  * allocation, left zeroed by every call); one workspace serves one stream at
- * a time.  vxh_sample_keep_mc with top_p < 1 runs vxh_sample_keep;
+ * a time.  vxh_sample_keep_mc with top_p < 1, or with V <= 32768 (rows the
+ * one-workgroup sampler holds in registers, where it is faster), runs
+ * vxh_sample_keep;
  * vxh_accept_mc with T > 0 and k = 0 runs vxh_accept.  max_rows bounds R of
  * vxh_row_stats_mc. */
 typedef struct {

@@ -22,6 +22,19 @@ static bool vx_overlap(const void *a, size_t an, const void *b, size_t bn)
 
 static bool vx_al16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
+// Whether M strided rows [a + m*lda, + na) and M rows [b + m*ldb, + nb) of
+// doubles share an element (rows of two buffers may interleave: the decode
+// forward's per-layer accumulators put every layer's rows side by side).
+static bool vx_overlap_rows(const double *a, size_t lda, size_t na, const double *b, size_t ldb, size_t nb, int M)
+{
+    if (!a || !b || !na || !nb) return false;
+    for (int i = 0; i < M; i++)
+        for (int j = 0; j < M; j++)
+            if (vx_overlap(a + (size_t)i * lda, na * sizeof(double), b + (size_t)j * ldb, nb * sizeof(double)))
+                return true;
+    return false;
+}
+
 extern "C" int vxh_gemm_pro(const vxh_qmat *W, int M, const vxh_pro *p, double *acc, int ld_acc,
                             int n_out, float scale, vxh_event start, vxh_event stop, vxh_stream s)
 {
@@ -66,9 +79,8 @@ extern "C" int vxh_gemm_pro(const vxh_qmat *W, int M, const vxh_pro *p, double *
     }
     if (p->n_clear && !p->clear) return vxh_fail(VXH_ERR_PARAM, "gemm_pro: clear range without a pointer");
     if (p->src) {
-        const size_t src_bytes = ((size_t)(M - 1) * p->ld_src +
-                                  (p->kind == VXH_PRO_SWIGLU ? (K + 15) / 16 * 32 : K)) * sizeof(double);
-        if (vx_overlap(acc, acc_bytes, p->src, src_bytes))
+        const size_t src_n = p->kind == VXH_PRO_SWIGLU ? (K + 15) / 16 * 32 : K;
+        if (vx_overlap_rows(acc, M > 1 ? ld_acc : 0, n_out, p->src, p->ld_src, src_n, M))
             return vxh_fail(VXH_ERR_PARAM, "gemm_pro: acc overlaps the source sums");
     }
     if (vx_overlap(acc, acc_bytes, p->clear, p->n_clear * sizeof(double)))

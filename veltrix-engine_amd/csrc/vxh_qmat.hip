@@ -442,6 +442,10 @@ extern "C" int vxh_qmat_gather_rows_clear(const vxh_qmat *m, const int *dev_ids,
     if (n <= 0) return n_clr > 0 ? vxh_fill_f32((float *)clr, 0.0f, 2 * (size_t)n_clr, s) : VXH_OK;
     int gx = (m->n_cols + 255) / 256;
     if (gx > 64) gx = 64;
+    // enough workgroups that each clears at most 4096 doubles (the gather
+    // loop has nothing to do in the extra ones)
+    const long gc = (n_clr + 4096L * n - 1) / (4096L * n);
+    if (gc > gx) gx = (int)(gc < 1024 ? gc : 1024);
     dim3 grid(gx, n);
     vx_gather_kernel<<<grid, 256, 0, vxh_hs(s)>>>((const uint32_t *)m->qs, (const uint32_t *)m->d,
                                                   m->type, m->n_rows, m->n_cols, m->n_pairs, dev_ids,

@@ -238,8 +238,12 @@ static vx_error dev_alloc_common(vx_model *m)
     /* ss then acc_x in one allocation, so the prologue forward clears both
      * (the sums of squares, the rows it starts from) with one range */
     const size_t n_ss = (size_t)(d->n_layers + 1) * 2 * B;
-    TRY(vxh_malloc((void **)&d->ss, sizeof(double) * (n_ss + (size_t)B * d->d)));
+    d->ld_dec_rec = d->ld_qkv + d->d + d->ld_gu + d->d;
+    const size_t n_dec = (size_t)VXH_PRO_ATTN_MAX_ROWS * (d->n_layers > 0 ? d->n_layers : 1) * d->ld_dec_rec;
+    TRY(vxh_malloc((void **)&d->ss, sizeof(double) * (n_ss + (size_t)B * d->d + n_dec)));
     d->acc_x = d->ss + n_ss;
+    d->acc_dec = d->acc_x + (size_t)B * d->d;
+    TRY(vxh_fill_f32((float *)d->acc_dec, 0.0f, 2 * n_dec, d->stream));
     TRY(vxh_malloc((void **)&d->acc_gu, sizeof(double) * B * (size_t)d->ld_gu));
     TRY(vxh_malloc((void **)&d->acc_lg, sizeof(double) * B * (size_t)d->ld_lg));
     d->acc_dirty = 1;                  /* zeroed before the first forward */
@@ -876,10 +880,17 @@ static vx_error forward_pro(vx_model *m, int M, int n_past, int logits_mode)
 #define SS(l, j) (d->ss + ((size_t)(l) * 2 + (j)) * B)
     if (d->acc_dirty && (e = zero_acc(d)) != VX_OK) return e;
     d->acc_dirty = 1;
+    /* one- and two-row forwards (draft decode): the output projection
+     * combines the attention partials itself, and every layer has its own
+     * accumulators (acc_dec), cleared here with the rest */
+    const int attn_in_o = M <= VXH_PRO_ATTN_MAX_ROWS && d->hd % 4 == 0;
+    const int dec = attn_in_o;
     /* the sums of squares and acc_x's rows (the previous prologue forward's
      * output GEMM may have left its last down projection in acc_x_rows of
-     * them) are cleared by the embedding gather's launch */
-    const long n_clr = (long)(L + 1) * 2 * B + (long)(M > d->acc_x_rows ? M : d->acc_x_rows) * dd;
+     * them) -- and, decoding, all of acc_x and rows 0..M-1 of every layer's
+     * accumulators -- are cleared by the embedding gather's launch */
+    const long n_clr = dec ? (long)(L + 1) * 2 * B + (long)B * dd + (long)M * L * d->ld_dec_rec
+                           : (long)(L + 1) * 2 * B + (long)(M > d->acc_x_rows ? M : d->acc_x_rows) * dd;
     if (d->has_embd)
         TRY(vxh_qmat_gather_rows_clear(&d->embd, d->tok, M, vx_get_synthetic_weight_scale(), d->x, dd, d->ss,
                                        n_clr, s));
@@ -889,9 +900,14 @@ static vx_error forward_pro(vx_model *m, int M, int n_past, int logits_mode)
     }
     d->acc_x_rows = 0;
 
-    /* one- and two-row forwards (draft decode): the output projection
-     * combines the attention partials itself */
-    const int attn_in_o = M <= VXH_PRO_ATTN_MAX_ROWS && d->hd % 4 == 0;
+    /* accumulators of layer l: q|k|v, attention output (y), gate/up, down (x) */
+    const int ld_dec = L * d->ld_dec_rec;
+#define ACC_Q(l) (dec ? d->acc_dec + (size_t)(l) * d->ld_dec_rec : d->acc_qkv)
+#define ACC_Y(l) (dec ? d->acc_dec + (size_t)(l) * d->ld_dec_rec + d->ld_qkv : d->acc_y)
+#define ACC_G(l) (dec ? d->acc_dec + (size_t)(l) * d->ld_dec_rec + d->ld_qkv + dd : d->acc_gu)
+#define ACC_X(l) (dec ? d->acc_dec + (size_t)(l) * d->ld_dec_rec + d->ld_qkv + dd + d->ld_gu : d->acc_x)
+    const int ldq = dec ? ld_dec : d->ld_qkv, ldy = dec ? ld_dec : dd, ldg = dec ? ld_dec : d->ld_gu,
+              ldx = dec ? ld_dec : dd;
     vxh_pro p;
     for (int l = 0; l < L; l++) {
         vx_dev_layer *Ld = &d->layers[l];
@@ -902,30 +918,30 @@ static vx_error forward_pro(vx_model *m, int M, int n_past, int logits_mode)
         memset(&p, 0, sizeof(p));
         p.kind = VXH_PRO_RESID;
         p.x = d->x; p.ldx = dd;
-        p.src = d->acc_x; p.ld_src = dd;
+        if (dec && l > 0) { p.src = ACC_X(l - 1); p.ld_src = ldx; }
+        else { p.src = d->acc_x; p.ld_src = dd; }
         p.w = Ld->attn_norm;
         p.x_out = d->x2; p.ld_xout = dd;
         p.ss = SS(l, 0);
-        p.clear = d->acc_gu; p.n_clear = (size_t)M * d->ld_gu;
-        if ((e = pgemm(d, &Ld->wqkv, &p, M, d->acc_qkv, d->ld_qkv, dd + 2 * kvd, VX_PROF_QKV, dd + 2 * kvd)))
+        if (!dec) { p.clear = d->acc_gu; p.n_clear = (size_t)M * d->ld_gu; }
+        if ((e = pgemm(d, &Ld->wqkv, &p, M, ACC_Q(l), ldq, dd + 2 * kvd, VX_PROF_QKV, dd + 2 * kvd)))
             return e;
         memset(&p, 0, sizeof(p));
         if (attn_in_o) {
             /* partials of the attention, combined by the output projection */
             int n_chunks = 0;
             if (kvh)
-                TRY(vxh_attention_parts_qkv_f16(d->acc_qkv, d->ld_qkv, SS(l, 0), dd, Ld->bq, Ld->bk, Ld->bv,
+                TRY(vxh_attention_parts_qkv_f16(ACC_Q(l), ldq, SS(l, 0), dd, Ld->bq, Ld->bk, Ld->bv,
                                                 d->rope_cos, d->rope_sin, d->n_pos, M, n_past, n_ctx,
                                                 d->n_heads, d->n_kv, d->hd, d->opt.attn_cap, kh, vh, &d->ws,
                                                 &n_chunks, s));
             else
-                TRY(vxh_attention_parts_qkv(d->acc_qkv, d->ld_qkv, SS(l, 0), dd, Ld->bq, Ld->bk, Ld->bv,
+                TRY(vxh_attention_parts_qkv(ACC_Q(l), ldq, SS(l, 0), dd, Ld->bq, Ld->bk, Ld->bv,
                                             d->rope_cos, d->rope_sin, d->n_pos, M, n_past, n_ctx, d->n_heads,
                                             d->n_kv, d->hd, d->opt.attn_cap, kc, vc, &d->ws, &n_chunks, s));
             p.kind = VXH_PRO_ATTN;
             p.part = d->ws.part; p.n_chunks = n_chunks;
             p.n_heads = d->n_heads; p.n_kv_heads = d->n_kv; p.head_dim = d->hd;
-            p.clear = d->acc_qkv; p.n_clear = (size_t)M * d->ld_qkv;
         } else if (M <= VXH_ATTN_QKV_FAST_ROWS && (d->hd == 64 || d->hd == 128)) {
             /* RoPE and the new k/v rows inside the attention's first launch */
             if (kvh)
@@ -948,16 +964,16 @@ static vx_error forward_pro(vx_model *m, int M, int n_past, int logits_mode)
             p.kind = VXH_PRO_ROWS;
             p.x = d->att; p.ldx = dd;
         }
-        if ((e = pgemm(d, &Ld->wo, &p, M, d->acc_y, dd, dd, VX_PROF_O, dd))) return e;
+        if ((e = pgemm(d, &Ld->wo, &p, M, ACC_Y(l), ldy, dd, VX_PROF_O, dd))) return e;
         memset(&p, 0, sizeof(p));
         p.kind = VXH_PRO_RESID;
         p.x = d->x2; p.ldx = dd;
-        p.src = d->acc_y; p.ld_src = dd;
+        p.src = ACC_Y(l); p.ld_src = ldy;
         p.w = Ld->ffn_norm;
         p.x_out = d->x; p.ld_xout = dd;
         p.ss = SS(l, 1);
-        p.clear = d->acc_x; p.n_clear = (size_t)M * dd;
-        if ((e = pgemm(d, &Ld->wgu, &p, M, d->acc_gu, d->ld_gu, d->ld_gu, VX_PROF_GATEUP, 2 * d->F)))
+        if (!dec) { p.clear = d->acc_x; p.n_clear = (size_t)M * dd; }
+        if ((e = pgemm(d, &Ld->wgu, &p, M, ACC_G(l), ldg, d->ld_gu, VX_PROF_GATEUP, 2 * d->F)))
             return e;
         if (M > VXH_PRO_ATTN_MAX_ROWS) {
             /* verify batches: the SwiGLU panel once per forward (each of the
@@ -971,11 +987,11 @@ static vx_error forward_pro(vx_model *m, int M, int n_past, int logits_mode)
         } else {
             memset(&p, 0, sizeof(p));
             p.kind = VXH_PRO_SWIGLU;
-            p.src = d->acc_gu; p.ld_src = d->ld_gu;
+            p.src = ACC_G(l); p.ld_src = ldg;
             p.ss_in = SS(l, 1); p.ss_K = dd;
             p.thr = d->opt.ffn_gate_threshold;
-            p.clear = d->acc_y; p.n_clear = (size_t)M * dd;
-            if ((e = pgemm(d, &Ld->wd, &p, M, d->acc_x, dd, dd, VX_PROF_DOWN, dd))) return e;
+            if (!dec) { p.clear = d->acc_y; p.n_clear = (size_t)M * dd; }
+            if ((e = pgemm(d, &Ld->wd, &p, M, ACC_X(l), ldx, dd, VX_PROF_DOWN, dd))) return e;
         }
     }
     int gu_cleared = 0;
@@ -991,10 +1007,11 @@ static vx_error forward_pro(vx_model *m, int M, int n_past, int logits_mode)
             memset(&p, 0, sizeof(p));
             p.kind = VXH_PRO_RESID;
             p.x = d->x + (size_t)r0 * dd; p.ldx = dd;
-            p.src = d->acc_x + (size_t)r0 * dd; p.ld_src = dd;
+            p.src = L > 0 ? ACC_X(L - 1) + (size_t)r0 * ldx : d->acc_x + (size_t)r0 * dd;
+            p.ld_src = L > 0 ? ldx : dd;
             p.w = d->has_out_norm ? d->out_norm : NULL;
             p.ss = d->has_out_norm ? SS(L, 0) : NULL;
-            p.clear = d->acc_gu; p.n_clear = (size_t)M * d->ld_gu;
+            if (!dec) { p.clear = d->acc_gu; p.n_clear = (size_t)M * d->ld_gu; }
             if ((e = pgemm(d, &d->out, &p, rows, d->acc_lg, d->ld_lg, orows, VX_PROF_OUTPUT, orows)))
                 return e;
             gu_cleared = 1;
@@ -1004,16 +1021,22 @@ static vx_error forward_pro(vx_model *m, int M, int n_past, int logits_mode)
                 TRY(vxh_acc_store(d->acc_lg, d->ld_lg, rows, orows, d->logits, V, NULL, 0, s));
         }
     } else {
-        /* x += last down projection (clears acc_x) */
-        TRY(vxh_acc_store(d->acc_x, dd, M, dd, d->x, dd, d->x, dd, s));
+        /* x += last down projection (clears its accumulator) */
+        if (L > 0) TRY(vxh_acc_store(ACC_X(L - 1), ldx, M, dd, d->x, dd, d->x, dd, s));
         if (logits_mode != VX_LOGITS_NONE) {   /* no output matrix: every logit -1e30 */
             const int rows = logits_mode == VX_LOGITS_LAST ? 1 : M;
             TRY(vxh_fill_rows(d->logits, V, rows, 0, V, -1e30f, s));
         }
     }
-    if (!gu_cleared && L > 0) TRY(vxh_fill_f32((float *)d->acc_gu, 0.0f, 2 * (size_t)M * d->ld_gu, s));
+    if (!dec && !gu_cleared && L > 0) TRY(vxh_fill_f32((float *)d->acc_gu, 0.0f, 2 * (size_t)M * d->ld_gu, s));
 #undef SS
-    d->acc_x_rows = gu_cleared ? M : 0;
+#undef ACC_Q
+#undef ACC_Y
+#undef ACC_G
+#undef ACC_X
+    /* rows of acc_x the output GEMM read and left (decoding reads the last
+     * layer's own accumulator instead) */
+    d->acc_x_rows = (gu_cleared && !dec) ? M : 0;
     d->acc_dirty = 0;
     return VX_OK;
 }

@@ -96,6 +96,12 @@ typedef struct vx_dev {
      * attention norm, 1 FFN norm; l = L is the output norm), added by the
      * prologue GEMMs and applied to their products */
     double *ss;                        /* [(L+1)][2][16]; acc_x follows it in one allocation */
+    /* decode forwards (at most two rows): every layer's own accumulators,
+     * [row][layer][q|k|v, attention output, gate/up, down], after acc_x in
+     * the same allocation, so the embedding gather's launch clears them all
+     * and no GEMM of the forward clears an accumulator */
+    double *acc_dec;
+    int ld_dec_rec;                    /* doubles of one layer's record */
     /* prologue path: the second residual buffer (the residual alternates
      * between x and x2 inside a layer) and the attention projection's
      * accumulator (acc_x holds the down projection's) */
