@@ -363,6 +363,9 @@ def run_spec(args):
             flat[f"verify_{nm}_frac"] = round(p.bytes / (p.ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4) if p.ms > 0 else None
     flat["verify_gemm_mix_frac"] = round(achieved / PEAK_HBM_GBS, 4)
     flat["verify_gemm_only_frac"] = round(achieved_gemm / PEAK_HBM_GBS, 4)
+    for nm, p in zip(names[:5], prof_d[:5]):
+        flat[f"draft_{nm}_us"] = round(1e3 * p.ms / max(p.launches, 1), 2)
+        flat[f"draft_{nm}_frac"] = round(p.bytes / (p.ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4) if p.ms > 0 else None
     flat["draft_gemm_frac"] = round(draft_gbs / PEAK_HBM_GBS, 4)
     flat["draft_gemm_avg_us"] = round(1e3 * ms_d / max(sum(p.launches for p in prof_d[:5]), 1), 2)
     log(f"decode: {value:.1f} tok/s; rounds {tot['rounds']}, accepted {tot['accepted']}/{tot['drafted']}; "
@@ -680,7 +683,7 @@ def run_traffic(args):
                 name, v = d["Kernel_Name"], float(d["Counter_Value"]) * 1024.0
                 if name.startswith("__amd_rocclr_copyBuffer") and v > cal_bytes / 2:
                     cal.append(v)
-                elif name.startswith("void vx_gemm_kernel"):
+                elif name.startswith("void vx_gemm_kernel") or name.startswith("void vx_vg_kernel"):
                     groups.setdefault((name.split("(")[0], d["Grid_Size"]), []).append(v)
         return groups, cal
     fetch, fcal = load(args.fetch, "FETCH_SIZE")
