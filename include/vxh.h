@@ -409,6 +409,14 @@ int vxh_attention_qkv(double *qkv, int ld_qkv, const double *ss, int ss_K, const
                       int n_pos, int M, int n_past, int n_ctx, int n_heads, int n_kv_heads,
                       int head_dim, int cap, float *k_cache_layer, float *v_cache_layer, float *out,
                       int ld_out, vxh_workspace *ws, vxh_stream s);
+/* vxh_attention_qkv that leaves the q|k|v sums as they are, for a caller
+ * whose accumulators are cleared elsewhere (the model forward's per-layer
+ * accumulators, cleared at the start of each forward). */
+int vxh_attention_qkv_keep(double *qkv, int ld_qkv, const double *ss, int ss_K, const float *bq,
+                           const float *bk, const float *bv, const float *cos_tab, const float *sin_tab,
+                           int n_pos, int M, int n_past, int n_ctx, int n_heads, int n_kv_heads,
+                           int head_dim, int cap, float *k_cache_layer, float *v_cache_layer, float *out,
+                           int ld_out, vxh_workspace *ws, vxh_stream s);
 
 /* The first launch of vxh_attention_qkv alone: the partials stay in
  * ws->part for a VXH_PRO_ATTN GEMM, which combines them (and must clear qkv,

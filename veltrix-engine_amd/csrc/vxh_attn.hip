@@ -1101,7 +1101,7 @@ static int vx_attention_run(const float *q, const vx_qkv_args *qa, long n_clr, i
     }
     if (n_chunks_out) *n_chunks_out = n_chunks;
     if (parts_only) return VXH_OK;
-    double *clr = qa ? (double *)qa->qkv : nullptr;
+    double *clr = (qa && n_clr > 0) ? (double *)qa->qkv : nullptr;
     vx_attention_combine_kernel<<<M * n_heads, CMB_THREADS, 0, vxh_hs(s)>>>(
         ws->part, M, n_heads, n_kv_heads, head_dim, n_chunks, out, ld_out, clr, n_clr);
     VXH_LAUNCHED();
@@ -1121,7 +1121,8 @@ static int vx_attention_qkv(double *qkv, int ld_qkv, const double *ss, int ss_K,
                             const float *bk, const float *bv, const float *cos_tab, const float *sin_tab,
                             int n_pos, int M, int n_past, int n_ctx, int n_heads, int n_kv_heads,
                             int head_dim, int cap, float *kc, float *vc, float *out, int ld_out,
-                            vxh_workspace *ws, int *n_chunks_out, vxh_stream s, int kv_half = 0)
+                            vxh_workspace *ws, int *n_chunks_out, vxh_stream s, int kv_half = 0,
+                            bool keep = false)
 {
     if (!qkv || ((uintptr_t)qkv & 15) || ld_qkv % 2 || M < 1 || n_kv_heads < 1 ||
         ld_qkv < (n_heads + 2 * n_kv_heads) * head_dim)
@@ -1141,7 +1142,7 @@ static int vx_attention_qkv(double *qkv, int ld_qkv, const double *ss, int ss_K,
     qa.bv = bv;
     qa.cs = cos_tab;
     qa.sn = sin_tab;
-    return vx_attention_run(nullptr, &qa, (long)M * ld_qkv, M, n_past, n_ctx, n_heads, n_kv_heads,
+    return vx_attention_run(nullptr, &qa, keep ? 0L : (long)M * ld_qkv, M, n_past, n_ctx, n_heads, n_kv_heads,
                             head_dim, cap, kc, vc, out, ld_out, ws, n_chunks_out != nullptr,
                             n_chunks_out, s, kv_half);
 }
@@ -1154,6 +1155,16 @@ extern "C" int vxh_attention_qkv(double *qkv, int ld_qkv, const double *ss, int 
 {
     return vx_attention_qkv(qkv, ld_qkv, ss, ss_K, bq, bk, bv, cos_tab, sin_tab, n_pos, M, n_past, n_ctx,
                             n_heads, n_kv_heads, head_dim, cap, kc, vc, out, ld_out, ws, nullptr, s);
+}
+
+extern "C" int vxh_attention_qkv_keep(double *qkv, int ld_qkv, const double *ss, int ss_K, const float *bq,
+                                      const float *bk, const float *bv, const float *cos_tab,
+                                      const float *sin_tab, int n_pos, int M, int n_past, int n_ctx,
+                                      int n_heads, int n_kv_heads, int head_dim, int cap, float *kc,
+                                      float *vc, float *out, int ld_out, vxh_workspace *ws, vxh_stream s)
+{
+    return vx_attention_qkv(qkv, ld_qkv, ss, ss_K, bq, bk, bv, cos_tab, sin_tab, n_pos, M, n_past, n_ctx,
+                            n_heads, n_kv_heads, head_dim, cap, kc, vc, out, ld_out, ws, nullptr, s, 0, true);
 }
 
 extern "C" int vxh_attention_parts_qkv(double *qkv, int ld_qkv, const double *ss, int ss_K,

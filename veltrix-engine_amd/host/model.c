@@ -239,7 +239,7 @@ static vx_error dev_alloc_common(vx_model *m)
      * (the sums of squares, the rows it starts from) with one range */
     const size_t n_ss = (size_t)(d->n_layers + 1) * 2 * B;
     d->ld_dec_rec = d->ld_qkv + d->d + d->ld_gu + d->d;
-    const size_t n_dec = (size_t)VXH_PRO_ATTN_MAX_ROWS * (d->n_layers > 0 ? d->n_layers : 1) * d->ld_dec_rec;
+    const size_t n_dec = (size_t)B * (d->n_layers > 0 ? d->n_layers : 1) * d->ld_dec_rec;
     TRY(vxh_malloc((void **)&d->ss, sizeof(double) * (n_ss + (size_t)B * d->d + n_dec)));
     d->acc_x = d->ss + n_ss;
     d->acc_dec = d->acc_x + (size_t)B * d->d;
@@ -881,10 +881,13 @@ static vx_error forward_pro(vx_model *m, int M, int n_past, int logits_mode)
     if (d->acc_dirty && (e = zero_acc(d)) != VX_OK) return e;
     d->acc_dirty = 1;
     /* one- and two-row forwards (draft decode): the output projection
-     * combines the attention partials itself, and every layer has its own
-     * accumulators (acc_dec), cleared here with the rest */
+     * combines the attention partials itself.  These and the verify batches
+     * that take the q|k|v attention give every layer its own accumulators
+     * (acc_dec), cleared here with the rest, so no launch of the forward
+     * clears one */
     const int attn_in_o = M <= VXH_PRO_ATTN_MAX_ROWS && d->hd % 4 == 0;
-    const int dec = attn_in_o;
+    const int qkv_fast = M <= VXH_ATTN_QKV_FAST_ROWS && (d->hd == 64 || d->hd == 128);
+    const int dec = attn_in_o || (qkv_fast && !d->opt.kv_half);
     /* the sums of squares and acc_x's rows (the previous prologue forward's
      * output GEMM may have left its last down projection in acc_x_rows of
      * them) -- and, decoding, all of acc_x and rows 0..M-1 of every layer's
@@ -942,12 +945,16 @@ static vx_error forward_pro(vx_model *m, int M, int n_past, int logits_mode)
             p.kind = VXH_PRO_ATTN;
             p.part = d->ws.part; p.n_chunks = n_chunks;
             p.n_heads = d->n_heads; p.n_kv_heads = d->n_kv; p.head_dim = d->hd;
-        } else if (M <= VXH_ATTN_QKV_FAST_ROWS && (d->hd == 64 || d->hd == 128)) {
+        } else if (qkv_fast) {
             /* RoPE and the new k/v rows inside the attention's first launch */
             if (kvh)
                 TRY(vxh_attention_qkv_f16(d->acc_qkv, d->ld_qkv, SS(l, 0), dd, Ld->bq, Ld->bk, Ld->bv,
                                           d->rope_cos, d->rope_sin, d->n_pos, M, n_past, n_ctx, d->n_heads,
                                           d->n_kv, d->hd, d->opt.attn_cap, kh, vh, d->att, dd, &d->ws, s));
+            else if (dec)
+                TRY(vxh_attention_qkv_keep(ACC_Q(l), ldq, SS(l, 0), dd, Ld->bq, Ld->bk, Ld->bv,
+                                           d->rope_cos, d->rope_sin, d->n_pos, M, n_past, n_ctx, d->n_heads,
+                                           d->n_kv, d->hd, d->opt.attn_cap, kc, vc, d->att, dd, &d->ws, s));
             else
                 TRY(vxh_attention_qkv(d->acc_qkv, d->ld_qkv, SS(l, 0), dd, Ld->bq, Ld->bk, Ld->bv,
                                       d->rope_cos, d->rope_sin, d->n_pos, M, n_past, n_ctx, d->n_heads,
@@ -981,9 +988,10 @@ static vx_error forward_pro(vx_model *m, int M, int n_past, int logits_mode)
              * gate/up sums); the panel launch clears acc_gu and acc_y */
             vxh_event pe0, pe1;
             if ((e = prof_slot_panel(d, M, d->F, &pe0, &pe1))) return e;
-            TRY(vxh_swiglu_panel_norm_timed(d->acc_gu, d->ld_gu, M, d->F, d->opt.ffn_gate_threshold, SS(l, 1),
-                                            dd, d->acc_y, (size_t)M * dd, &d->pan_f, pe0, pe1, s));
-            if ((e = gemm(d, &Ld->wd, &d->pan_f, M, d->acc_x, dd, dd, VX_PROF_DOWN, dd))) return e;
+            TRY(vxh_swiglu_panel_norm_timed(ACC_G(l), ldg, M, d->F, d->opt.ffn_gate_threshold, SS(l, 1), dd,
+                                            dec ? NULL : d->acc_y, dec ? 0 : (size_t)M * dd, &d->pan_f, pe0, pe1,
+                                            s));
+            if ((e = gemm(d, &Ld->wd, &d->pan_f, M, ACC_X(l), ldx, dd, VX_PROF_DOWN, dd))) return e;
         } else {
             memset(&p, 0, sizeof(p));
             p.kind = VXH_PRO_SWIGLU;
