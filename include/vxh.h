@@ -42,6 +42,13 @@ int vxh_free(void *dptr);
 int vxh_upload(void *dst, const void *src, size_t bytes, vxh_stream s);
 int vxh_download(void *dst, const void *src, size_t bytes, vxh_stream s);
 int vxh_copy(void *dst, const void *src, size_t bytes, vxh_stream s);
+/* Page-locked host memory (hipHostMalloc), the source vxh_upload_async needs. */
+int vxh_host_alloc(void **p, size_t bytes);
+int vxh_host_free(void *p);
+/* Host -> device copy enqueued on s without waiting for it: src must be
+ * page-locked (vxh_host_alloc) and keep its contents until the stream has
+ * run the copy (a later vxh_stream_sync, or a synchronous vxh_download on s). */
+int vxh_upload_async(void *dst, const void *src, size_t bytes, vxh_stream s);
 int vxh_fill_f32(float *dst, float value, size_t n, vxh_stream s);   /* kernel, graph-safe */
 int vxh_stream_create(vxh_stream *s);
 int vxh_stream_destroy(vxh_stream s);

@@ -75,6 +75,32 @@ extern "C" int vxh_upload(void *dst, const void *src, size_t bytes, vxh_stream s
     return VXH_OK;
 }
 
+extern "C" int vxh_host_alloc(void **p, size_t bytes)
+{
+    int rc = vxh_init();
+    if (rc) return rc;
+    *p = nullptr;
+    if (bytes == 0) bytes = 64;
+    hipError_t e = hipHostMalloc(p, bytes, hipHostMallocDefault);
+    if (e != hipSuccess)
+        return vxh_fail(VXH_ERR_ALLOC, "hipHostMalloc(%zu): %s", bytes, hipGetErrorString(e));
+    return VXH_OK;
+}
+
+extern "C" int vxh_host_free(void *p)
+{
+    if (!p) return VXH_OK;
+    VXH_CHECK(hipHostFree(p));
+    return VXH_OK;
+}
+
+extern "C" int vxh_upload_async(void *dst, const void *src, size_t bytes, vxh_stream s)
+{
+    if (!bytes) return VXH_OK;
+    VXH_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, vxh_hs(s)));
+    return VXH_OK;
+}
+
 extern "C" int vxh_download(void *dst, const void *src, size_t bytes, vxh_stream s)
 {
     if (!bytes) return VXH_OK;

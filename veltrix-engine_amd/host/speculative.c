@@ -45,7 +45,15 @@ struct vx_speculative_state {
     vxh_vocab_ws ws_d, ws_t; /* many-workgroup sampling workspaces, one per
                                 model stream (draft draws, verify decision) */
     int *out_host;
-    float *uh;
+    /* page-locked staging of a round's uploads (vxh_upload_async): the
+     * draft's catch-up tokens, t0, the draft and verify uniforms.  Every
+     * round ends with a synchronous download, so the copies of one round
+     * have run before the next round writes here. */
+    void *stage;
+    int *st_tok;        /* [VX_MAX_BATCH] */
+    int *st_t0;         /* [1]            */
+    float *st_ud;       /* [k]            */
+    float *st_uv;       /* [k+1]          */
     vx_speculative_stats st;
     int *tr_drafts, *tr_emitted, *tr_accepted, tr_max;
     /* state left by vx_speculative_prefill */
@@ -83,10 +91,17 @@ vx_speculative_state *vx_speculative_create(vx_model *draft, vx_model *target, i
              vxh_malloc((void **)&s->u_verify, sizeof(float) * (size_t)(k + 1)) == VXH_OK &&
              vxh_malloc((void **)&s->dtok, sizeof(int) * (size_t)(k + 1)) == VXH_OK &&
              vxh_malloc((void **)&s->out_dev, sizeof(int) * (size_t)(k + 3)) == VXH_OK &&
-             vxh_vocab_ws_alloc(&s->ws_d, 1) == VXH_OK && vxh_vocab_ws_alloc(&s->ws_t, k + 1) == VXH_OK;
+             vxh_vocab_ws_alloc(&s->ws_d, 1) == VXH_OK && vxh_vocab_ws_alloc(&s->ws_t, k + 1) == VXH_OK &&
+             vxh_host_alloc(&s->stage, sizeof(int) * (VX_MAX_BATCH + 1) + sizeof(float) * (size_t)(2 * k + 1)) ==
+                 VXH_OK;
+    if (ok) {
+        s->st_tok = (int *)s->stage;
+        s->st_t0 = s->st_tok + VX_MAX_BATCH;
+        s->st_ud = (float *)(s->st_t0 + 1);
+        s->st_uv = s->st_ud + k;
+    }
     s->out_host = (int *)calloc((size_t)(k + 3), sizeof(int));
-    s->uh = (float *)calloc((size_t)(k + 1), sizeof(float));
-    if (!ok || !s->out_host || !s->uh) {
+    if (!ok || !s->out_host) {
         vx_speculative_destroy(s);
         return NULL;
     }
@@ -100,8 +115,8 @@ void vx_speculative_destroy(vx_speculative_state *s)
     vxh_free(s->dtok); vxh_free(s->out_dev);
     vxh_vocab_ws_free(&s->ws_d);
     vxh_vocab_ws_free(&s->ws_t);
+    vxh_host_free(s->stage);
     free(s->out_host);
-    free(s->uh);
     free(s->committed);
     free(s);
 }
@@ -222,12 +237,13 @@ int vx_speculative_decode(vx_speculative_state *s, int *output, int max_tokens)
             /* catch-up batch: committed[draft_len .. n) */
             int pend = n - draft_len;
             if (pend < 1 || pend > VX_MAX_BATCH) goto done;
-            CHK(vxh_upload(dd->tok, committed + draft_len, sizeof(int) * (size_t)pend, dd->stream));
+            memcpy(s->st_tok, committed + draft_len, sizeof(int) * (size_t)pend);
+            for (int i = 0; i < kk; i++) s->st_ud[i] = vx_uniform(s->seed, 1, (uint64_t)round * k + i);
+            CHK(vxh_upload_async(dd->tok, s->st_tok, sizeof(int) * (size_t)pend, dd->stream));
+            CHK(vxh_upload_async(s->u_draft, s->st_ud, sizeof(float) * (size_t)kk, dd->stream));
             dd->logits = s->D;
             CHKE(vx_dev_forward(dm, pend, draft_len, VX_LOGITS_LAST));
             draft_len = n;
-            for (int i = 0; i < kk; i++) s->uh[i] = vx_uniform(s->seed, 1, (uint64_t)round * k + i);
-            CHK(vxh_upload(s->u_draft, s->uh, sizeof(float) * (size_t)kk, dd->stream));
             for (int i = 0; i < kk; i++) {
                 dd->logits = s->D + (size_t)i * Vd;
                 if (i > 0) CHKE(vx_dev_forward_ids(dm, s->dtok + i, 1, n + i - 1, VX_LOGITS_LAST));
@@ -241,13 +257,14 @@ int vx_speculative_decode(vx_speculative_state *s, int *output, int max_tokens)
         s->st.draft_ms += tb - ta;
 
         /* verify: one target forward over [t0, d_0 .. d_{kk-1}] */
-        CHK(vxh_upload(s->dtok, &t_last, sizeof(int), td->stream));
+        s->st_t0[0] = t_last;
+        for (int j = 0; j < kk; j++) s->st_uv[j] = vx_uniform(s->seed, 2, (uint64_t)round * (k + 1) + j);
+        /* the resample / bonus draw always uses the stream's slot k */
+        s->st_uv[kk] = vx_uniform(s->seed, 2, (uint64_t)round * (k + 1) + k);
+        CHK(vxh_upload_async(s->dtok, s->st_t0, sizeof(int), td->stream));
+        CHK(vxh_upload_async(s->u_verify, s->st_uv, sizeof(float) * (size_t)(kk + 1), td->stream));
         CHKE(vx_dev_forward_ids(tm, s->dtok, kk + 1, n - 1, VX_LOGITS_ALL));
         CHK(vxh_row_stats_mc(td->logits, Vt, kk + 1, Vt, T, td->stats, &s->ws_t, td->stream));
-        for (int j = 0; j < kk; j++) s->uh[j] = vx_uniform(s->seed, 2, (uint64_t)round * (k + 1) + j);
-        /* the resample / bonus draw always uses the stream's slot k */
-        s->uh[kk] = vx_uniform(s->seed, 2, (uint64_t)round * (k + 1) + k);
-        CHK(vxh_upload(s->u_verify, s->uh, sizeof(float) * (size_t)(kk + 1), td->stream));
         CHK(vxh_accept_mc(td->logits, Vt, Vt, td->stats, s->D, Vd, Vd, s->nuc, s->dtok + 1, kk, T,
                           s->u_verify, s->out_dev, &s->ws_t, td->stream));
         CHK(vxh_download(s->out_host, s->out_dev, sizeof(int) * (size_t)(kk + 3), td->stream));
@@ -288,6 +305,10 @@ int vx_speculative_decode(vx_speculative_state *s, int *output, int max_tokens)
     }
 done:
     dd->logits = dlogits;
+    /* an error path may leave staged copies queued: let them run before the
+     * next call rewrites the staging (a no-op after a normal round) */
+    vxh_stream_sync(dd->stream);
+    vxh_stream_sync(td->stream);
     return generated;
 }
 
