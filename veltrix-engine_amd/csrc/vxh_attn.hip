@@ -894,8 +894,11 @@ __global__ __launch_bounds__(ATT_THREADS) __attribute__((amdgpu_waves_per_eu(3))
 // its running (max, sum, acc) is merged across the slices in LDS, so the
 // chunk walk is spread over the workgroup instead of serialised per thread.
 #define CMB_THREADS 256
-#define CMB_BATCH 12   // chunks whose loads a thread issues together (one round trip per batch)
-
+// NB: chunks whose loads a thread issues together (one round trip per
+// batch); the launch picks the smallest of 4, 6, 8, 12 that covers a
+// thread's chunks, so no loads or exponentials go to clamped duplicates
+// (the visiting order, and so the result, does not depend on NB)
+template <int NB>
 __global__ __launch_bounds__(CMB_THREADS) void vx_attention_combine_kernel(
     const float *__restrict__ part, int M, int n_heads, int n_kv, int hd, int n_chunks,
     float *__restrict__ out, int ld_out, double *clr, long n_clr)
@@ -920,11 +923,11 @@ __global__ __launch_bounds__(CMB_THREADS) void vx_attention_combine_kernel(
     float mx = -INFINITY, l = 0.0f;
     float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
     if (sl < S) {
-        for (int c0 = sl; c0 < n_chunks; c0 += CMB_BATCH * S) {
-            float cm[CMB_BATCH], cl[CMB_BATCH];
-            float4 ca[CMB_BATCH];
+        for (int c0 = sl; c0 < n_chunks; c0 += NB * S) {
+            float cm[NB], cl[NB];
+            float4 ca[NB];
 #pragma unroll
-            for (int u = 0; u < CMB_BATCH; u++) {
+            for (int u = 0; u < NB; u++) {
                 const int c = c0 + u * S;
                 const float *pc = pq + (size_t)min(c, n_chunks - 1) * cstride;
                 cm[u] = c < n_chunks ? pc[0] : -INFINITY;
@@ -932,7 +935,7 @@ __global__ __launch_bounds__(CMB_THREADS) void vx_attention_combine_kernel(
                 ca[u] = *(const float4 *)(pc + 4 + 4 * d4);
             }
 #pragma unroll
-            for (int u = 0; u < CMB_BATCH; u++) {
+            for (int u = 0; u < NB; u++) {
                 if (cm[u] == -INFINITY) continue;
                 const float nm = fmaxf(mx, cm[u]);
                 const float fo = mx == -INFINITY ? 0.0f : expf(mx - nm);
@@ -1102,8 +1105,15 @@ static int vx_attention_run(const float *q, const vx_qkv_args *qa, long n_clr, i
     if (n_chunks_out) *n_chunks_out = n_chunks;
     if (parts_only) return VXH_OK;
     double *clr = (qa && n_clr > 0) ? (double *)qa->qkv : nullptr;
-    vx_attention_combine_kernel<<<M * n_heads, CMB_THREADS, 0, vxh_hs(s)>>>(
-        ws->part, M, n_heads, n_kv_heads, head_dim, n_chunks, out, ld_out, clr, n_clr);
+    const int per = (n_chunks + CMB_THREADS / (head_dim / 4) - 1) / (CMB_THREADS / (head_dim / 4));
+#define VX_CMB_LAUNCH(NB_)                                                                                      \
+    vx_attention_combine_kernel<NB_><<<M * n_heads, CMB_THREADS, 0, vxh_hs(s)>>>(                               \
+        ws->part, M, n_heads, n_kv_heads, head_dim, n_chunks, out, ld_out, clr, n_clr)
+    if (per <= 4) VX_CMB_LAUNCH(4);
+    else if (per <= 6) VX_CMB_LAUNCH(6);
+    else if (per <= 8) VX_CMB_LAUNCH(8);
+    else VX_CMB_LAUNCH(12);
+#undef VX_CMB_LAUNCH
     VXH_LAUNCHED();
     return VXH_OK;
 }

@@ -249,9 +249,11 @@ __device__ __forceinline__ void vx_pro_values(const vx_pro_args &p, const vx_pro
 // head, lane d4) and every S-th chunk from t / U (S = 256 / U slices); the
 // slices merge in LDS.
 // chunks of partials whose loads one thread issues together (one round trip
-// per batch; with one partial per 64 positions, 12 cover a 6144-position
-// draft context at 8 slices)
-#define VX_CMB_BATCH 12
+// per batch; with one partial per 64 positions a thread of a one-row slice
+// (8 slices) visits every 8th: 6 cover a 3072-position draft context in one
+// batch without loading clamped duplicates at the usual ~2000-2400, two rows
+// (4 slices) take 12 per batch)
+#define VX_CMB_BATCH(M) ((M) == 1 ? 6 : 12)
 
 template <int M, int PPW>
 __device__ __forceinline__ void vx_pro_attn(const vx_pro_args &p, int p0, int np, uint4 *lds, float *lrs)
@@ -274,11 +276,12 @@ __device__ __forceinline__ void vx_pro_attn(const vx_pro_args &p, int p0, int np
         const int head = e / hd, d4 = (e % hd) / 4;
         const int g = head / p.G, qi = (head % p.G) * M + m;
         const float *pq = p.part + (size_t)g * p.n_chunks * cstride + (size_t)qi * PS;
-        for (int c0 = sl; c0 < p.n_chunks; c0 += VX_CMB_BATCH * S) {
-            float cm[VX_CMB_BATCH], cl[VX_CMB_BATCH];
-            float4 ca[VX_CMB_BATCH];
+        constexpr int NB = VX_CMB_BATCH(M);
+        for (int c0 = sl; c0 < p.n_chunks; c0 += NB * S) {
+            float cm[NB], cl[NB];
+            float4 ca[NB];
 #pragma unroll
-            for (int v = 0; v < VX_CMB_BATCH; v++) {
+            for (int v = 0; v < NB; v++) {
                 const int c = c0 + v * S;
                 const float *pc = pq + (size_t)min(c, p.n_chunks - 1) * cstride;
                 cm[v] = c < p.n_chunks ? pc[0] : -INFINITY;
@@ -286,7 +289,7 @@ __device__ __forceinline__ void vx_pro_attn(const vx_pro_args &p, int p0, int np
                 ca[v] = *(const float4 *)(pc + 4 + 4 * d4);
             }
 #pragma unroll
-            for (int v = 0; v < VX_CMB_BATCH; v++) {
+            for (int v = 0; v < NB; v++) {
                 if (cm[v] == -INFINITY) continue;
                 const float nm = fmaxf(mx, cm[v]);
                 const float fo = mx == -INFINITY ? 0.0f : expf(mx - nm);
