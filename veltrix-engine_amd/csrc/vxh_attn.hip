@@ -273,52 +273,11 @@ __global__ __launch_bounds__(ATT_THREADS) void vx_attention_kernel(
 // vx_attention_kernel writes (the combine kernels read either).
 typedef float vx_f32x4 __attribute__((ext_vector_type(4)));
 
-// Rows of the q|k|v sums as the attention reads them: 4 consecutive elements
-// per load, RoPE'd as two adjacent pairs (rot) with the deferred RMSNorm and
-// the bias applied.  All loads of a batch are issued before the first use and
-// every address is valid (callers clamp), so a wavefront pays one round trip.
-template <int NB>
-__device__ __forceinline__ void vx_qkv4_batch(const vx_qkv_args &a, int row, const int col[NB],
-                                              const int el[NB], const int pr[NB], int rp, int half,
-                                              const float *bias, bool rot, float4 out[NB])
-{
-    const double *rs = a.qkv + (size_t)row * a.ld;
-    const double *ssp = a.ss ? a.ss + row : rs;     // any valid address when there is no norm
-    const float *bp = bias ? bias : a.cs;
-    const float *ct = a.cs + (size_t)rp * half, *st = a.sn + (size_t)rp * half;
-    double2 p0[NB], p1[NB];
-    float4 b4[NB];
-    float c0[NB], c1[NB], s0[NB], s1[NB];
-    const double ssv = *ssp;
-#pragma unroll
-    for (int u = 0; u < NB; u++) {
-        p0[u] = *(const double2 *)(rs + col[u]);
-        p1[u] = *(const double2 *)(rs + col[u] + 2);
-        b4[u] = *(const float4 *)(bp + (bias ? el[u] : 0));
-        if (rot) {
-            c0[u] = ct[pr[u]];
-            c1[u] = ct[pr[u] + 1];
-            s0[u] = st[pr[u]];
-            s1[u] = st[pr[u] + 1];
-        }
-    }
-    const float rin = a.ss ? vx_rms_inv((float)ssv, a.ss_K) : 1.0f;
-#pragma unroll
-    for (int u = 0; u < NB; u++) {
-        const float x0 = bias ? fmaf((float)p0[u].x, rin, b4[u].x) : (float)p0[u].x * rin;
-        const float x1 = bias ? fmaf((float)p0[u].y, rin, b4[u].y) : (float)p0[u].y * rin;
-        const float x2 = bias ? fmaf((float)p1[u].x, rin, b4[u].z) : (float)p1[u].x * rin;
-        const float x3 = bias ? fmaf((float)p1[u].y, rin, b4[u].w) : (float)p1[u].y * rin;
-        if (rot) {
-            const float2 o0 = vx_rope_rot(x0, x1, c0[u], s0[u]), o1 = vx_rope_rot(x2, x3, c1[u], s1[u]);
-            out[u] = make_float4(o0.x, o0.y, o1.x, o1.y);
-        } else {
-            out[u] = make_float4(x0, x1, x2, x3);
-        }
-    }
-}
-
-// vx_qkv4_batch for items of different rows, RoPE positions and biases.
+// Items of the q|k|v sums as the attention reads them: 4 consecutive
+// elements of a row per item, RoPE'd as two adjacent pairs (rot) at the
+// item's position, with the deferred RMSNorm of its row and its bias
+// applied.  All loads of a batch are issued before the first use and every
+// address is valid (callers clamp), so a wavefront pays one round trip.
 template <int NB>
 __device__ __forceinline__ void vx_qkv4_items(const vx_qkv_args &a, const int row[NB], const int col[NB],
                                               const int el[NB], const int pr[NB], const int rp[NB],
