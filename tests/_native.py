@@ -345,6 +345,12 @@ def bind_vxh(L):
     L.vxh_accept.argtypes = [vp, C.c_int, C.c_int, vp, vp, C.c_int, C.c_int, vp, vp, C.c_int,
                              C.c_float, vp, vp, vp]
     L.vxh_stream_sync.argtypes = [vp]
+    L.vxh_stream_create.argtypes = [C.POINTER(vp)]
+    L.vxh_stream_destroy.argtypes = [vp]
+    L.vxh_host_alloc.argtypes = [C.POINTER(vp), C.c_size_t]
+    L.vxh_host_free.argtypes = [vp]
+    L.vxh_upload_async.argtypes = [vp, vp, C.c_size_t, vp]
+    L.vxh_fill_f32.argtypes = [vp, C.c_float, C.c_size_t, vp]
     L.vxh_vocab_ws_alloc.argtypes = [C.POINTER(VxhVocabWs), C.c_int]
     L.vxh_vocab_ws_free.argtypes = [C.POINTER(VxhVocabWs)]
     L.vxh_row_stats_mc.argtypes = [vp, C.c_int, C.c_int, C.c_int, C.c_float, vp, C.POINTER(VxhVocabWs), vp]
