@@ -51,6 +51,37 @@ def test_gemm_q4_0_exact(P, rows, cols, M):
     assert close(Y, exact, atol=2e-5, rtol=2e-5), max_violation(Y, exact, 2e-5, 2e-5)
 
 
+@pytest.mark.parametrize("typ", [2, 8])
+def test_gemm_every_batch_size(P, typ):
+    """Every batch size 1..16 (each has its own kernel instantiation: the
+    one-row and few-row GEMMs, the 64-row-tile verify kernel from 5 rows)
+    on one Q4_0 / Q8_0 matrix whose row count is not a multiple of 64 and
+    whose K spans several slices, against the oracle GEMV at the fp32 bar."""
+    rows, cols = 200, 1536
+    rng = np.random.default_rng(4242 + typ)
+    W = N.rand_q4_0(rng, rows, cols) if typ == 2 else N.rand_q8_0(rng, rows, cols)
+    vals = N.q4_values(W) if typ == 2 else N.q8_values(W)
+    if typ == 8:
+        A = np.zeros(rows * cols, np.float32)
+        O.or_dequantize_row_q8_0(N._ptr(W), A, rows * cols, 1.0)
+        A = A.reshape(rows, cols)
+    for M in range(1, 17):
+        print(f"{'Q4_0' if typ == 2 else 'Q8_0'} {rows}x{cols} M={M}", flush=True)
+        X = rng.normal(0, 1, (M, cols)).astype(np.float32)
+        Y = np.zeros((M, rows), np.float32)
+        if typ == 2:
+            assert P.vx_gemm_q4_0(N._ptr(W), X, cols, Y, M, rows, cols, 0) == 0, N.product_error()
+            ref = oracle_rows(O.or_gemv_q4_0, W, X, rows, cols)
+        else:
+            assert P.vx_gemm_q8_0(N._ptr(W), X, cols, Y, M, rows, cols) == 0, N.product_error()
+            ref = np.zeros((M, rows), np.float32)
+            for m in range(M):
+                O.or_gemv_f32(ref[m], A, np.ascontiguousarray(X[m]), rows, cols)
+        exact = X.astype(np.float64) @ vals.T
+        ok, _ = N.parity(Y, ref, exact)
+        assert ok, (M, max_violation(Y, ref))
+
+
 # every exact shape, plus a draft-size matrix at one row (the decode GEMV)
 AVX2_SHAPES = SHAPES + [(2048, 5632, 1)]
 
