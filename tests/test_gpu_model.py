@@ -202,3 +202,38 @@ def test_kv_truncate_and_reverify(P, tmp_path):
         assert np.array_equal(a, b)
     finally:
         g.close()
+
+
+@pytest.mark.parametrize("hd", [64, 128])
+def test_verify_every_batch_size(P, tmp_path, hd):
+    """Verify batches of every size 1..16 after the same prefix (each size
+    has its own kernel instantiations: the one- and two-row decode path with
+    the attention combine in the output projection, the q|k|v attention at
+    up to 16 rows, the 64-row-tile GEMMs from 5 rows) against the oracle's
+    teacher-forced forward over prefix + block."""
+    h = 4
+    d = h * hd
+    path, raw, (L, d, h, kv, ff, V) = make(tmp_path, 300 + hd, L=2, d=d, h=h, kv=2, ff=2 * d, V=500)
+    g = GpuModel(P, path)
+    om = OracleModel(raw, L, d, h, kv, ff, V, n_ctx=4096)
+    rng = np.random.default_rng(hd)
+    prefix = rng.integers(0, V, 37).astype(np.int32)
+    try:
+        g.forward(prefix)
+        for M in range(1, 17):
+            print(f"verify batch of {M} rows, head_dim {hd}", flush=True)
+            block = rng.integers(0, V, M).astype(np.int32)
+            P.vx_model_kv_truncate(g.mp, 37)
+            got = g.verify(block)
+            ref_all = np.zeros((37 + M, V), np.float32)
+            om.cache_len = 0               # the oracle's forward starts at its cache_len
+            O.or_forward_all(om.ptr, np.concatenate([prefix, block]), 37 + M, ref_all)
+            ref = ref_all[37:]
+            assert close(got, ref), (M, max_violation(got, ref))
+            for j in range(M):
+                top = np.sort(ref[j])[-2:]
+                if top[1] - top[0] > 1e-4:
+                    assert got[j].argmax() == ref[j].argmax(), (M, j)
+            assert g.cache_len == 37 + M
+    finally:
+        g.close()
