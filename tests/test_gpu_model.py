@@ -204,16 +204,17 @@ def test_kv_truncate_and_reverify(P, tmp_path):
         g.close()
 
 
-@pytest.mark.parametrize("hd", [64, 128])
-def test_verify_every_batch_size(P, tmp_path, hd):
+@pytest.mark.parametrize("hd,mtype", [(64, GGML_Q4_0), (128, GGML_Q4_0), (128, GGML_Q8_0)])
+def test_verify_every_batch_size(P, tmp_path, hd, mtype):
     """Verify batches of every size 1..16 after the same prefix (each size
     has its own kernel instantiations: the one- and two-row decode path with
     the attention combine in the output projection, the q|k|v attention at
-    up to 16 rows, the 64-row-tile GEMMs from 5 rows) against the oracle's
-    teacher-forced forward over prefix + block."""
+    up to 16 rows, the 64-row-tile GEMMs from 5 rows; Q4_0 and Q8_0 layers)
+    against the oracle's teacher-forced forward over prefix + block."""
     h = 4
     d = h * hd
-    path, raw, (L, d, h, kv, ff, V) = make(tmp_path, 300 + hd, L=2, d=d, h=h, kv=2, ff=2 * d, V=500)
+    path, raw, (L, d, h, kv, ff, V) = make(tmp_path, 300 + hd + mtype, L=2, d=d, h=h, kv=2, ff=2 * d, V=500,
+                                           matrix_type=mtype)
     g = GpuModel(P, path)
     om = OracleModel(raw, L, d, h, kv, ff, V, n_ctx=4096)
     rng = np.random.default_rng(hd)
@@ -221,7 +222,7 @@ def test_verify_every_batch_size(P, tmp_path, hd):
     try:
         g.forward(prefix)
         for M in range(1, 17):
-            print(f"verify batch of {M} rows, head_dim {hd}", flush=True)
+            print(f"verify batch of {M} rows, head_dim {hd}, matrix type {mtype}", flush=True)
             block = rng.integers(0, V, M).astype(np.int32)
             P.vx_model_kv_truncate(g.mp, 37)
             got = g.verify(block)
