@@ -464,13 +464,17 @@ static void attention(or_model *m, const float *q, const float *k, const float *
     if (pos >= max_ctx) { pos = max_ctx - 1; m->cache_len = pos; }
     int cache_size = pos + 1;
     size_t loff = (size_t)layer * (size_t)max_ctx * kvd;
-    memcpy(m->k_cache + loff + (size_t)pos * kvd, k, sizeof(float) * (size_t)kvd);
-    memcpy(m->v_cache + loff + (size_t)pos * kvd, v, sizeof(float) * (size_t)kvd);
+    float *kr = m->k_cache + loff + (size_t)pos * kvd, *vr = m->v_cache + loff + (size_t)pos * kvd;
+    if (m->kv_keep) {   /* test hook: the caller's row stays; ours goes aside */
+        kr = m->kv_own_k ? m->kv_own_k + (size_t)layer * kvd : NULL;
+        vr = m->kv_own_v ? m->kv_own_v + (size_t)layer * kvd : NULL;
+    }
+    if (kr) memcpy(kr, k, sizeof(float) * (size_t)kvd);
+    if (vr) memcpy(vr, v, sizeof(float) * (size_t)kvd);
     if (m->kv_half)
         for (int i = 0; i < kvd; i++) {
-            float *kr = m->k_cache + loff + (size_t)pos * kvd, *vr = m->v_cache + loff + (size_t)pos * kvd;
-            kr[i] = or_round_half(kr[i]);
-            vr[i] = or_round_half(vr[i]);
+            if (kr) kr[i] = or_round_half(kr[i]);
+            if (vr) vr[i] = or_round_half(vr[i]);
         }
     memset(out, 0, sizeof(float) * (size_t)nh * hd);
     int cs = cache_size;

@@ -99,6 +99,15 @@ typedef struct {
     int flip_tok[OR_MAX_FLIPS];   /* each at token index within the call, layer, column */
     int flip_layer[OR_MAX_FLIPS];
     int flip_col[OR_MAX_FLIPS];
+    /* Test hook of the cache store (the reference has no such hook).  With
+     * kv_keep set, attention() leaves cache row pos as the caller placed it
+     * (another engine's own stored row) and writes the row it computed, in
+     * the cache's format, to kv_own_k / kv_own_v [n_layers][kv_dim] when they
+     * are set.  Two engines then attend over identical cache contents, which
+     * separates a difference in the arithmetic from binary16 rounding of two
+     * fp32 values a few ulps apart landing on neighbouring binary16 values. */
+    int kv_keep;
+    float *kv_own_k, *kv_own_v;
 } or_model;
 
 /* x rounded to the nearest IEEE binary16 value (ties to even), as fp32:

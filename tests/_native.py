@@ -81,6 +81,7 @@ class OrModel(C.Structure):
         ("kv_half", C.c_int),
         ("gate_near", C.c_void_p), ("gate_near_idx", C.c_void_p), ("flip", C.c_int),
         ("flip_tok", C.c_int * 4), ("flip_layer", C.c_int * 4), ("flip_col", C.c_int * 4),
+        ("kv_keep", C.c_int), ("kv_own_k", C.c_void_p), ("kv_own_v", C.c_void_p),
     ]
 
 

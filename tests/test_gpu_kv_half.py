@@ -135,3 +135,95 @@ def test_kv_half_speculative_greedy_equals_target_greedy(P):
             P.vx_speculative_destroy(st)
         for m in (tm, dm, tg):
             P.vx_model_destroy(m)
+
+
+def _half_steps(mine, gpu):
+    """Largest difference between two rows of binary16 values, in binary16
+    steps of the larger magnitude (2^-10 of it), among the elements whose
+    difference exceeds 2^-16 of the row's largest magnitude: fp32 sums over a
+    few hundred terms that cancel can differ by a few 2^-24 of the sum of the
+    terms' magnitudes, many binary16 steps of a small result."""
+    slack = 2.0 ** -16 * float(np.abs(gpu).max())
+    a = mine.astype(np.float64)
+    b = gpu.astype(np.float64)
+    diff = np.abs(a - b)
+    step = 2.0 ** -10 * np.maximum(np.abs(a), np.abs(b))
+    excess = np.where(diff > slack, diff / np.maximum(step, 1e-300), 0.0)
+    return int(np.count_nonzero(diff)), float(excess.max())
+
+
+@pytest.mark.parametrize("hd", [64, 128])
+def test_kv_half_every_batch_size(P, tmp_path, hd):
+    """The fp16 cache at every verify batch size 1..16 after the same prefix,
+    against the oracle with the same rounding.  Two fp32 values a few ulps
+    apart can round to neighbouring binary16 values, and the difference then
+    reaches every later row and layer, so the oracle attends over the GPU's
+    own stored rows (its cache-store hook) and the rows are checked one by
+    one: row j's K/V as the oracle computes them over the GPU's rows before j
+    must be within one binary16 step of what the GPU stored (or 2^-16 of the
+    row's largest magnitude), and the logits
+    to the usual bar.  A run without the hook checks layer 0 of the block,
+    whose inputs are the embeddings alone, against rows the oracle stores
+    itself."""
+    from test_gpu_model import GpuModel, make
+    h = 4
+    path, raw, (L, d, h, kv, ff, V) = make(tmp_path, 500 + hd, L=2, d=h * hd, h=h, kv=2, ff=2 * h * hd, V=500)
+    n_ctx, n_past, kvd = 4096, 37, kv * hd
+    g = GpuModel(P, path)
+    om = OracleModel(raw, L, d, h, kv, ff, V, n_ctx=n_ctx, kv_half=1)
+    kc = om.k_cache.reshape(L, n_ctx, kvd)
+    vc = om.v_cache.reshape(L, n_ctx, kvd)
+    own_k = np.zeros((L, kvd), np.float32)
+    own_v = np.zeros((L, kvd), np.float32)
+    om.m.kv_own_k = own_k.ctypes.data_as(C.c_void_p)
+    om.m.kv_own_v = own_v.ctypes.data_as(C.c_void_p)
+    rng = np.random.default_rng(hd + 1)
+    prefix = rng.integers(0, V, n_past).astype(np.int32)
+    n_diff = n_all = 0
+    try:
+        assert set_kv_half(P, g.mp, 1) == 0, N.product_error()
+        g.forward(prefix)
+        for M in range(1, 17):
+            print(f"kv_half verify batch of {M} rows, head_dim {hd}", flush=True)
+            block = rng.integers(0, V, M).astype(np.int32)
+            P.vx_model_kv_truncate(g.mp, n_past)
+            got = g.verify(block)
+            n = n_past + M
+            gk = np.zeros((L, n, kvd), np.float32)
+            gv = np.zeros((L, n, kvd), np.float32)
+            for l in range(L):
+                assert P.vx_model_read_kv(g.mp, l, n, gk[l], gv[l]) == 0, N.product_error()
+            assert np.array_equal(gk, gk.astype(np.float16).astype(np.float32))
+            assert np.array_equal(gv, gv.astype(np.float16).astype(np.float32))
+            # layer 0 of the block, stored by the oracle itself after the GPU's prefix
+            kc[:, :n] = gk
+            vc[:, :n] = gv
+            om.m.kv_keep = 0
+            om.cache_len = n_past
+            scratch = np.zeros((M, V), np.float32)
+            assert O.or_forward_all(om.ptr, block, M, scratch) == 0
+            for mine, gpu in ((kc[0, n_past:n], gk[0, n_past:]), (vc[0, n_past:n], gv[0, n_past:])):
+                for r in range(M):
+                    nd, worst = _half_steps(mine[r], gpu[r])
+                    assert worst <= 1.0, ("layer 0", M, r, nd, worst)
+            # row by row over the GPU's rows
+            kc[:, :n] = gk
+            vc[:, :n] = gv
+            om.m.kv_keep = 1
+            ref = np.zeros((M, V), np.float32)
+            row = np.zeros((1, V), np.float32)
+            for j in range(M):
+                om.cache_len = n_past + j
+                assert O.or_forward_all(om.ptr, block[j:j + 1], 1, row) == 0
+                ref[j] = row[0]
+                p = n_past + j
+                for mine, gpu in ((own_k, gk[:, p]), (own_v, gv[:, p])):
+                    for l in range(L):
+                        nd, worst = _half_steps(mine[l], gpu[l])
+                        assert worst <= 1.0, (M, j, l, nd, worst)
+                        n_diff += nd
+                        n_all += kvd
+            assert close(got, ref), (M, max_violation(got, ref))
+    finally:
+        g.close()
+    print(f"own K/V elements differing by one binary16 step: {n_diff} of {n_all}")

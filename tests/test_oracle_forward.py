@@ -253,3 +253,43 @@ def test_layer_major_forward_is_bit_identical(tmp_path, case):
             assert np.array_equal(a, b), (all_rows, split, np.abs(a - b).max())
             assert np.array_equal(ak, bk) and np.array_equal(av, bv)
             assert np.array_equal(an, bn) and np.array_equal(ai, bi)
+
+
+@pytest.mark.parametrize("kvh", [0, 1])
+def test_cache_store_hook(tmp_path, kvh):
+    """The cache-store hook (or_model.kv_keep): over cache rows the oracle
+    stored itself, one token at a time with the hook gives the logits of the
+    plain forward bit for bit, leaves the cache as it was, and hands back
+    each layer's computed row (rounded as the cache stores it) equal to the
+    stored one.  A changed caller row is what later tokens attend over."""
+    L, d, h, kv, ff, V, n = 2, 64, 4, 2, 128, 96, 12
+    kvd = kv * (d // h)
+    rng = np.random.default_rng(31 + kvh)
+    path = str(tmp_path / "m.gguf")
+    raw = llama_gguf(path, rng, L, d, h, kv, ff, V, std=0.05, norm_random=True, matrix_type=GGML_Q4_0)
+    tokens = rng.integers(0, V, n).astype(np.int32)
+    om = OracleModel(raw, L, d, h, kv, ff, V, n_ctx=64, kv_half=kvh)
+    full = np.zeros((n, V), np.float32)
+    assert O.or_forward_all(om.ptr, tokens, n, full) == 0
+    kc, vc = om.k_cache.reshape(L, 64, kvd), om.v_cache.reshape(L, 64, kvd)
+    k0, v0 = kc.copy(), vc.copy()
+    own_k = np.zeros((L, kvd), np.float32)
+    own_v = np.zeros((L, kvd), np.float32)
+    om.m.kv_own_k = own_k.ctypes.data_as(C.c_void_p)
+    om.m.kv_own_v = own_v.ctypes.data_as(C.c_void_p)
+    om.m.kv_keep = 1
+    row = np.zeros((1, V), np.float32)
+    for j in range(n):
+        om.cache_len = j
+        assert O.or_forward_all(om.ptr, tokens[j:j + 1], 1, row) == 0
+        assert np.array_equal(row[0], full[j]), j
+        assert np.array_equal(own_k, k0[:, j]) and np.array_equal(own_v, v0[:, j]), j
+    assert np.array_equal(kc, k0) and np.array_equal(vc, v0)
+    # a caller row that differs from the computed one is the one attended over
+    kc[0, 3] += 0.25
+    om.cache_len = 0
+    changed = np.zeros((n, V), np.float32)
+    assert O.or_forward_all(om.ptr, tokens, n, changed) == 0
+    assert np.array_equal(changed[:3], full[:3])
+    assert not np.array_equal(changed[3], full[3])
+    assert np.array_equal(kc[0, 3], k0[0, 3] + 0.25)
