@@ -381,6 +381,9 @@ def bind_attention(P):
     (8, 2, 32, 5, 70, 256, 40, True),            # attention cap below the positions
     (32, 32, 128, 9, 2100, 2304, 4096, False),   # verify-sized cache (69 MB): non-temporal cache loads
     (32, 32, 64, 1, 2100, 2304, 4096, False),    # the same at head_dim 64 (34 MB)
+    (8, 2, 64, 1, 0, 64, 4096, False),           # the first position: one row, nothing cached
+    (8, 8, 128, 9, 0, 64, 4096, True),           # a batch from position 0 across the first chunk edge
+    (8, 8, 128, 9, 28, 128, 4096, False),        # rows 28..36: the chunk edge inside the batch
 ])
 def test_attention_qkv_matches_rope_then_attention(P, H, KV, hd, M, n_past, n_ctx, cap, bias):
     """vxh_attention_qkv against vxh_rope_kv_norm followed by vxh_attention on
@@ -555,7 +558,18 @@ def test_attention_matches_reference(P, H, KV, hd, M, n_past, n_ctx, cap):
     assert rc == 0, P.vxh_last_error()
     assert P.vxh_stream_sync(None) == 0
     got = dout.get(np.float32, M * qd).reshape(M, qd)
-    ref = np.zeros((M, qd))
+    ref = attention_ref(qv, kc, vc, H, KV, hd, n_past, n_ctx, cap)
+    assert close(got, ref, atol=1e-5, rtol=1e-4), max_violation(got, ref, 1e-5, 1e-4)
+    P.vxh_workspace_free(C.byref(ws))
+    for b in (dq, dk, dv, dout):
+        b.free()
+
+
+def attention_ref(qv, kc, vc, H, KV, hd, n_past, n_ctx, cap):
+    """Softmax attention in float64 (src/model.c:300-338): row m attends to
+    [0, min(pos_m + 1, cap)), pos_m = min(n_past + m, n_ctx - 1)."""
+    M = qv.shape[0]
+    ref = np.zeros((M, H * hd))
     G = H // KV
     for m in range(M):
         pos = min(n_past + m, n_ctx - 1)
@@ -567,10 +581,39 @@ def test_attention_matches_reference(P, H, KV, hd, M, n_past, n_ctx, cap):
             s = K @ qv[m, h * hd:(h + 1) * hd].astype(np.float64) / np.sqrt(hd)
             p = np.exp(s - s.max())
             ref[m, h * hd:(h + 1) * hd] = (p @ Vv) / (p.sum() + 1e-10)
-    assert close(got, ref, atol=1e-5, rtol=1e-4), max_violation(got, ref, 1e-5, 1e-4)
+    return ref
+
+
+@pytest.mark.parametrize("hd,M", [(64, 1), (64, 9), (128, 1), (128, 9)])
+def test_attention_at_chunk_boundaries(P, hd, M):
+    """Positions 0..~100 in steps that put the batch's first and last rows on
+    either side of 32-position chunk edges (the first row alone, the edge
+    between rows, the edge at the last row), at the draft's and the verify's
+    head sizes, against float64 softmax attention."""
+    bind_attention(P)
+    H, KV = (8, 2) if hd == 64 else (4, 4)
+    n_ctx, cap = 160, 4096
+    qd, kvd = H * hd, KV * hd
+    ws = Workspace()
+    assert P.vxh_workspace_alloc(C.byref(ws), 32, P.vxh_attention_workspace_floats(M, n_ctx, cap, H, KV, hd)) == 0
+    for n_past in (0, 1, 23, 24, 31, 32, 55, 63, 64, 95, 96):
+        print(f"attention hd={hd} M={M} n_past={n_past}", flush=True)
+        rng = np.random.default_rng(hd * 1000 + M * 100 + n_past)
+        qv = rng.normal(0, 1.0, (M, qd)).astype(np.float32)
+        kc = rng.normal(0, 1.0, (n_ctx, kvd)).astype(np.float32)
+        vc = rng.normal(0, 1.0, (n_ctx, kvd)).astype(np.float32)
+        dq, dk, dv = N.DevBuf(P, qv), N.DevBuf(P, kc), N.DevBuf(P, vc)
+        dout = N.DevBuf(P, np.zeros((M, qd), np.float32))
+        rc = P.vxh_attention(dq.ptr, M, n_past, n_ctx, H, KV, hd, cap, dk.ptr, dv.ptr, dout.ptr, qd, C.byref(ws),
+                             None)
+        assert rc == 0, P.vxh_last_error()
+        assert P.vxh_stream_sync(None) == 0
+        got = dout.get(np.float32, M * qd).reshape(M, qd)
+        for b in (dq, dk, dv, dout):
+            b.free()
+        ref = attention_ref(qv, kc, vc, H, KV, hd, n_past, n_ctx, cap)
+        assert close(got, ref, atol=1e-5, rtol=1e-4), (n_past, max_violation(got, ref, 1e-5, 1e-4))
     P.vxh_workspace_free(C.byref(ws))
-    for b in (dq, dk, dv, dout):
-        b.free()
 
 
 def test_wide_attention_clamp_and_cap_in_model(P, tmp_path):
