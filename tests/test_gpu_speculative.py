@@ -115,20 +115,37 @@ def test_greedy_equals_target_greedy_decode(P, models):
         P.vx_model_destroy(dm)
 
 
-def test_greedy_self_draft_accepts_everything(P, models):
+@pytest.mark.parametrize("k", [1, 2, 5, 8, 15])
+def test_greedy_self_draft_accepts_everything(P, models, k):
+    """The target as its own draft, greedy: every draft is accepted, each
+    round emits k + 1 tokens (verify batches of 2..16 rows, and the one-row
+    draft steps), and the tokens are the target's own greedy sequence."""
     (tpath, traw, tsh), _ = models
-    V = tsh[5]
+    V, n_gen = tsh[5], 36
+    print(f"greedy self-draft k={k}", flush=True)
+    prompt = np.arange(7, dtype=np.int32)
     tm, dm = load(P, tpath), load(P, tpath)
-    st = P.vx_speculative_create(dm, tm, 5)
+    st = P.vx_speculative_create(dm, tm, k)
+    assert st, N.product_error()
     try:
         P.vx_speculative_set_temp(st, 0.0, 1.0)
-        prompt = np.arange(7, dtype=np.int32)
-        out = np.zeros(36, np.int32)
-        assert P.vx_speculative_generate(st, prompt, 7, out, 36) == 36
+        out = np.zeros(n_gen, np.int32)
+        assert P.vx_speculative_generate(st, prompt.copy(), 7, out, n_gen) == n_gen, N.product_error()
         stats = N.VxSpecStats()
         P.vx_speculative_get_stats(st, C.byref(stats))
         assert stats.accepted == stats.drafted, (stats.accepted, stats.drafted)
-        assert stats.rounds == 6   # 6 tokens per round (5 drafts + bonus)
+        assert stats.rounds == (n_gen + k) // (k + 1)
+        # target-only greedy decode on a fresh copy of the target
+        tg = load(P, tpath)
+        try:
+            lg = np.zeros(V, np.float32)
+            assert P.vx_model_forward(tg, prompt, 7, lg) == 0, N.product_error()
+            for i in range(n_gen):
+                t = int(np.argmax(lg))
+                assert out[i] == t, (i, out[:i + 1])
+                assert P.vx_model_forward(tg, np.array([t], np.int32), 1, lg) == 0, N.product_error()
+        finally:
+            P.vx_model_destroy(tg)
     finally:
         P.vx_speculative_destroy(st)
         P.vx_model_destroy(tm)
