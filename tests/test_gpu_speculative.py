@@ -152,11 +152,12 @@ def test_greedy_self_draft_accepts_everything(P, models, k):
         P.vx_model_destroy(dm)
 
 
-@pytest.mark.parametrize("T,top_p", [(0.8, 1.0), (1.0, 0.9)])
-def test_sampled_replay_matches_oracle(P, models, T, top_p):
+@pytest.mark.parametrize("T,top_p,k", [(0.8, 1.0, 4), (1.0, 0.9, 4), (0.8, 1.0, 1), (1.0, 0.9, 15)])
+def test_sampled_replay_matches_oracle(P, models, T, top_p, k):
     (tpath, traw, tsh), (dpath, draw, dsh) = models
     V = tsh[5]
-    k, n_gen, seed = 4, 48, 2024
+    n_gen, seed = 48, 2024
+    print(f"sampled replay T={T} top_p={top_p} k={k}", flush=True)
     prompt = np.random.default_rng(6).integers(0, V, 9).astype(np.int32)
     tm, dm = load(P, tpath), load(P, dpath)
     st = P.vx_speculative_create(dm, tm, k)
