@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 import _native as N
-from _gguf import llama_gguf, GGML_Q8_0, GGML_Q4_0
+from _gguf import llama_gguf, GGML_F32, GGML_Q8_0, GGML_Q4_0
 from _native import close, max_violation
 from _oracle_model import OracleModel
 
@@ -236,5 +236,38 @@ def test_verify_every_batch_size(P, tmp_path, hd, mtype):
                 if top[1] - top[0] > 1e-4:
                     assert got[j].argmax() == ref[j].argmax(), (M, j)
             assert g.cache_len == 37 + M
+    finally:
+        g.close()
+
+
+@pytest.mark.parametrize("emb", [GGML_Q4_0, GGML_F32])
+def test_token_ids_outside_the_vocabulary(P, tmp_path, emb):
+    """Negative ids embed as a zero row (src/model.c:457).  Ids at or past
+    n_vocab do too: the reference's F32 table checks the row against its
+    size (src/model.c:461-463), its quantized lookup reads past the table,
+    and the engine gives zeros for both.  A verify batch, one-row forwards
+    and a prompt long enough for the batched prefill, against the oracle fed
+    -1 in place of every id outside [0, n_vocab)."""
+    path, raw, (L, d, h, kv, ff, V) = make(tmp_path, 91 + emb, emb_type=emb)
+    rng = np.random.default_rng(emb)
+    toks = rng.integers(0, V, 60).astype(np.int32)
+    toks[[1, 9, 20, 33, 52]] = [-1, V, V + 1000, -7, 2**31 - 1]
+    safe = np.where((toks < 0) | (toks >= V), -1, toks).astype(np.int32)
+    ref = np.zeros((60, V), np.float32)
+    om = OracleModel(raw, L, d, h, kv, ff, V, n_ctx=4096)
+    assert O.or_forward_all(om.ptr, safe, 60, ref) == 0
+    g = GpuModel(P, path)
+    try:
+        got = g.verify(toks[:9])                  # rows 0..8 in one verify batch
+        assert close(got, ref[:9]), max_violation(got, ref[:9])
+        for i in range(9, 12):                     # one-row forwards
+            one = g.forward(toks[i:i + 1])
+            assert close(one, ref[i]), (i, max_violation(one, ref[i]))
+    finally:
+        g.close()
+    g = GpuModel(P, path)
+    try:
+        last = g.forward(toks)                     # 60 tokens: the batched prefill
+        assert close(last, ref[59]), max_violation(last, ref[59])
     finally:
         g.close()
