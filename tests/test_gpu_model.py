@@ -271,3 +271,27 @@ def test_token_ids_outside_the_vocabulary(P, tmp_path, emb):
         assert close(last, ref[59]), max_violation(last, ref[59])
     finally:
         g.close()
+
+
+def test_forward_and_verify_argument_checks(P, tmp_path):
+    """The reference's argument checks (src/model.c:391-392): a NULL model,
+    token array or logits buffer is VX_ERR_PARAM; zero or a negative count of
+    tokens runs nothing (VX_OK; the logits and the cache stay as they were)."""
+    path, raw, (L, d, h, kv, ff, V) = make(tmp_path, 61)
+    g = GpuModel(P, path)
+    proto = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p)
+    try:
+        g.forward(np.array([3, 4], np.int32))
+        toks = np.array([5], np.int32)
+        lg = np.full(V, 7.0, np.float32)
+        mp = C.cast(g.mp, C.c_void_p)
+        for name in ("vx_model_forward", "vx_model_verify"):
+            f = proto((name, P))
+            assert f(None, toks.ctypes.data, 1, lg.ctypes.data) == -4
+            assert f(mp, None, 1, lg.ctypes.data) == -4
+            assert f(mp, toks.ctypes.data, 1, None) == -4
+            assert f(mp, toks.ctypes.data, 0, lg.ctypes.data) == 0
+            assert f(mp, toks.ctypes.data, -3, lg.ctypes.data) == 0
+            assert np.all(lg == 7.0) and g.cache_len == 2
+    finally:
+        g.close()
