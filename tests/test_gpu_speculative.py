@@ -318,3 +318,42 @@ def test_draft_context_smaller_than_target(P, models):
         P.vx_speculative_destroy(st)
         P.vx_model_destroy(tm)
         P.vx_model_destroy(dm)
+
+
+def test_generate_argument_checks_and_stream_entry(P, models):
+    """vx_speculative_generate returns 0 tokens for a NULL state, prompt or
+    output, an empty prompt or max_tokens < 1 (src/speculative.c:240-241);
+    vx_speculative_generate_stream(token) is generate over the one-token
+    prompt (src/speculative.c:296-300): same seed, same tokens."""
+    (tpath, traw, tsh), (dpath, draw, dsh) = models
+    proto = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p, C.c_int)
+    gen = proto(("vx_speculative_generate", P))
+    stream = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_int)(("vx_speculative_generate_stream", P))
+    outs = []
+    for use_stream in (False, True):
+        tm, dm = load(P, tpath), load(P, dpath)
+        st = P.vx_speculative_create(dm, tm, 3)
+        assert st, N.product_error()
+        try:
+            P.vx_speculative_set_temp(st, 0.8, 1.0)
+            P.vx_speculative_set_seed(st, 99)
+            prompt = np.array([17], np.int32)
+            out = np.full(20, -5, np.int32)
+            if not use_stream:
+                assert gen(None, prompt.ctypes.data, 1, out.ctypes.data, 20) == 0
+                assert gen(st, None, 1, out.ctypes.data, 20) == 0
+                assert gen(st, prompt.ctypes.data, 1, None, 20) == 0
+                assert gen(st, prompt.ctypes.data, 0, out.ctypes.data, 20) == 0
+                assert gen(st, prompt.ctypes.data, 1, out.ctypes.data, 0) == 0
+                assert np.all(out == -5)
+                assert gen(st, prompt.ctypes.data, 1, out.ctypes.data, 20) == 20, N.product_error()
+            else:
+                assert stream(None, 17, out.ctypes.data, 20) == 0
+                assert stream(st, 17, out.ctypes.data, 20) == 20, N.product_error()
+            outs.append(out.copy())
+        finally:
+            P.vx_speculative_destroy(st)
+            P.vx_model_destroy(tm)
+            P.vx_model_destroy(dm)
+    assert np.array_equal(outs[0], outs[1])
+    assert np.all((outs[0] >= 0) & (outs[0] < tsh[5]))
