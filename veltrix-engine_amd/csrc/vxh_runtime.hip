@@ -31,7 +31,7 @@ extern "C" int vxh_init(void)
     hipDeviceProp_t prop;
     VXH_CHECK(hipGetDeviceProperties(&prop, 0));
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
-        return vxh_fail(VXH_ERR_UNSUPPORTED, "device is %s; this build targets gfx950 only",
+        return vxh_fail(VXH_ERR_UNSUPPORTED, "device is %s; the library's kernels are compiled for gfx950 only",
                         prop.gcnArchName);
     g_inited = 1;
     return VXH_OK;
