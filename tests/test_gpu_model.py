@@ -200,6 +200,15 @@ def test_kv_truncate_and_reverify(P, tmp_path):
         assert g.cache_len == 5
         b = g.verify(toks[5:14])
         assert np.array_equal(a, b)
+        # src/model.c:384-389: a length past cache_len changes nothing, a
+        # negative one empties the cache, a NULL model is ignored
+        P.vx_model_kv_truncate(g.mp, 40)
+        assert g.cache_len == 14
+        C.CFUNCTYPE(None, C.c_void_p, C.c_int)(("vx_model_kv_truncate", P))(None, 3)
+        P.vx_model_kv_truncate(g.mp, -2)
+        assert g.cache_len == 0
+        c = g.verify(toks[:14])
+        assert np.array_equal(c[5:], a)
     finally:
         g.close()
 
