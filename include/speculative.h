@@ -5,7 +5,9 @@
  * model, verifies all k+1 positions of the target in ONE batched forward on
  * the GPU and applies the acceptance rule on the GPU.  Uniform draws come from
  * a seeded counter-based stream (vx_speculative_set_seed in veltrix_gpu.h)
- * instead of libc rand().
+ * instead of libc rand().  max_draft_tokens is 1..15 (a verify batch holds at
+ * most 16 rows); vx_speculative_create returns NULL outside that range or for
+ * a NULL model (the reference accepts any count).
  */
 #ifndef VX_SPECULATIVE_H
 #define VX_SPECULATIVE_H

@@ -357,3 +357,18 @@ def test_generate_argument_checks_and_stream_entry(P, models):
             P.vx_model_destroy(dm)
     assert np.array_equal(outs[0], outs[1])
     assert np.all((outs[0] >= 0) & (outs[0] < tsh[5]))
+    # draft counts 1..15 (a verify batch holds at most 16 rows); NULL models
+    tm, dm = load(P, tpath), load(P, dpath)
+    try:
+        create = C.CFUNCTYPE(C.c_void_p, C.c_void_p, C.c_void_p, C.c_int)(("vx_speculative_create", P))
+        for k in (0, -1, 16, 100):
+            assert not P.vx_speculative_create(dm, tm, k), k
+        assert not create(None, C.cast(tm, C.c_void_p), 4)
+        assert not create(C.cast(dm, C.c_void_p), None, 4)
+        for k in (1, 15):
+            st = P.vx_speculative_create(dm, tm, k)
+            assert st, (k, N.product_error())
+            P.vx_speculative_destroy(st)
+    finally:
+        P.vx_model_destroy(tm)
+        P.vx_model_destroy(dm)
