@@ -1044,7 +1044,8 @@ int or_sample_top_p(const float *l, int n, float T, float top_p, float u, float 
         or_pi *s = (or_pi *)malloc(sizeof(or_pi) * (size_t)n);
         for (int i = 0; i < n; i++) { s[i].p = p[i]; s[i].i = i; }
         qsort(s, (size_t)n, sizeof(or_pi), cmp_desc);
-        uint64_t TP = (uint64_t)ceil((double)top_p * 4294967296.0);
+        /* top_p <= 0: the first sorted token alone (src/speculative.c:67-74) */
+        uint64_t TP = top_p > 0.0f ? (uint64_t)ceil((double)top_p * 4294967296.0) : 0;
         uint64_t c = 0;
         int cut = n;
         for (int r = 0; r < n; r++) {

@@ -77,7 +77,11 @@ def sample_gpu(P, l, T, top_p, u, mc=False):
 @pytest.mark.parametrize("mc", [False, True])
 @pytest.mark.parametrize("V,T,top_p", [(32000, 0.8, 1.0), (32000, 1.0, 0.9), (5000, 0.7, 0.5),
                                        (152064, 1.0, 1.0), (152064, 1.0, 0.95), (1000, 0.0, 1.0),
-                                       (70001, 0.9, 1.0)])
+                                       (70001, 0.9, 1.0),
+                                       # sharp and flat distributions; a nucleus of the top token
+                                       # (top_p <= 0 and 1e-6) and one past the whole mass (1.5)
+                                       (5000, 0.1, 1.0), (5000, 3.0, 0.9), (5000, 0.8, 0.0),
+                                       (5000, 0.8, -0.5), (5000, 0.8, 1e-6), (5000, 0.8, 1.5)])
 def test_sampler_matches_oracle(P, V, T, top_p, mc):
     print(f"sampler V={V} T={T} top_p={top_p} {'many workgroups' if mc else 'one workgroup'}", flush=True)
     rng = np.random.default_rng(V + int(T * 10) + int(top_p * 100))

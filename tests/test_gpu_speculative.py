@@ -152,7 +152,8 @@ def test_greedy_self_draft_accepts_everything(P, models, k):
         P.vx_model_destroy(dm)
 
 
-@pytest.mark.parametrize("T,top_p,k", [(0.8, 1.0, 4), (1.0, 0.9, 4), (0.8, 1.0, 1), (1.0, 0.9, 15)])
+@pytest.mark.parametrize("T,top_p,k", [(0.8, 1.0, 4), (1.0, 0.9, 4), (0.8, 1.0, 1), (1.0, 0.9, 15),
+                                       (0.8, 0.0, 4)])
 def test_sampled_replay_matches_oracle(P, models, T, top_p, k):
     (tpath, traw, tsh), (dpath, draw, dsh) = models
     V = tsh[5]

@@ -190,3 +190,22 @@ def test_emitted_token_is_target_distributed_at_temperature(T, top_p):
     assert np.allclose(counts / n_trials, want, atol=0.012, rtol=0)
     # the T = 1 distribution differs from the target by more than the tolerance
     assert np.max(np.abs(softmax_t(L[0], 1.0) - want)) > 0.03
+
+
+@pytest.mark.parametrize("top_p", [0.0, -0.5, 1e-12])
+def test_nucleus_of_a_non_positive_top_p_is_the_first_token(top_p):
+    """The reference's cutoff loop (src/speculative.c:67-74) stops at the
+    first sorted token once cumsum >= top_p, so top_p <= 0 (or below one
+    2^-32 unit) keeps exactly the most probable token, the lowest index
+    among equal maxima: every draw returns it and q is one-hot."""
+    rng = np.random.default_rng(5)
+    V = 40
+    l = rng.normal(0, 1.0, V).astype(np.float32)
+    l[[7, 23]] = l.max() + 1.0          # two equal maxima: the lower index wins
+    q = np.zeros(V, np.float32)
+    for u in (0.0, 0.3, 0.999):
+        t = O.or_sample_top_p(l, V, 0.8, top_p, u, q.ctypes.data_as(C.c_void_p))
+        assert t == 7
+        want = np.zeros(V, np.float32)
+        want[7] = 1.0
+        assert np.array_equal(q, want)

@@ -255,7 +255,10 @@ __global__ __launch_bounds__(SB) void vx_sample_kernel(const float *__restrict__
     float tau = -1.0f;
     int tie_cut = V - 1;
     if (top_p < 1.0f) {
-        const uint64_t TP = (uint64_t)ceil((double)top_p * 4294967296.0);
+        // at least one unit: the reference's nucleus always holds its first
+        // token, also for top_p <= 0 (src/speculative.c:67-74)
+        const double tpu = top_p > 0.0f ? ceil((double)top_p * 4294967296.0) : 0.0;
+        const uint64_t TP = tpu < 1.0 ? 1ull : (uint64_t)tpu;
         // largest probability value tau with mass(p >= tau) >= TP (bisection
         // over the bit patterns of non-negative floats, which are ordered)
         uint32_t lo = 0u, hi = 0x3F800000u;     // mass(p >= 0) = all >= TP
