@@ -81,7 +81,9 @@ def sample_gpu(P, l, T, top_p, u, mc=False):
                                        # sharp and flat distributions; a nucleus of the top token
                                        # (top_p <= 0 and 1e-6) and one past the whole mass (1.5)
                                        (5000, 0.1, 1.0), (5000, 3.0, 0.9), (5000, 0.8, 0.0),
-                                       (5000, 0.8, -0.5), (5000, 0.8, 1e-6), (5000, 0.8, 1.5)])
+                                       (5000, 0.8, -0.5), (5000, 0.8, 1e-6), (5000, 0.8, 1.5),
+                                       # vocabularies of one to three entries
+                                       (1, 0.8, 1.0), (2, 0.8, 0.5), (3, 1.0, 1.0)])
 def test_sampler_matches_oracle(P, V, T, top_p, mc):
     print(f"sampler V={V} T={T} top_p={top_p} {'many workgroups' if mc else 'one workgroup'}", flush=True)
     rng = np.random.default_rng(V + int(T * 10) + int(top_p * 100))
@@ -190,7 +192,8 @@ def oracle_accept(L, D, drafts, T, top_p, u):
 
 @pytest.mark.parametrize("mc", [False, True])
 @pytest.mark.parametrize("V,k,T,top_p", [(32000, 8, 0.8, 1.0), (32000, 4, 1.0, 0.95), (2000, 8, 0.8, 1.0),
-                                         (32000, 8, 0.0, 1.0), (152064, 8, 1.0, 1.0)])
+                                         (32000, 8, 0.0, 1.0), (152064, 8, 1.0, 1.0), (2, 8, 0.8, 1.0),
+                                         (3, 4, 1.0, 0.0)])
 def test_accept_matches_oracle(P, V, k, T, top_p, mc):
     print(f"accept V={V} k={k} T={T} top_p={top_p} {'many workgroups' if mc else 'one workgroup'}", flush=True)
     rng = np.random.default_rng(V + k)
