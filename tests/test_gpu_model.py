@@ -304,3 +304,34 @@ def test_forward_and_verify_argument_checks(P, tmp_path):
             assert np.all(lg == 7.0) and g.cache_len == 2
     finally:
         g.close()
+
+
+@pytest.mark.parametrize("mtype", [GGML_Q4_0, GGML_Q8_0])
+def test_odd_shapes(P, tmp_path, mtype):
+    """Widths with an odd number of 32-element blocks (n_embd 96: 3 blocks,
+    n_ff 160: 5), three heads of 32, one kv head, and a vocabulary that is
+    not a multiple of 32 rows (77): the padded block and row tiles must not
+    leak into any sum.  One-row forwards, a verify batch and a prompt long
+    enough for the batched prefill against the oracle."""
+    path, raw, (L, d, h, kv, ff, V) = make(tmp_path, 131 + mtype, L=2, d=96, h=3, kv=1, ff=160, V=77,
+                                           matrix_type=mtype)
+    rng = np.random.default_rng(mtype + 3)
+    toks = rng.integers(0, V, 64).astype(np.int32)
+    ref = np.zeros((64, V), np.float32)
+    om = OracleModel(raw, L, d, h, kv, ff, V, n_ctx=4096)
+    assert O.or_forward_all(om.ptr, toks, 64, ref) == 0
+    g = GpuModel(P, path)
+    try:
+        for i in range(3):
+            one = g.forward(toks[i:i + 1])
+            assert close(one, ref[i]), (i, max_violation(one, ref[i]))
+        got = g.verify(toks[3:12])
+        assert close(got, ref[3:12]), max_violation(got, ref[3:12])
+    finally:
+        g.close()
+    g = GpuModel(P, path)
+    try:
+        last = g.forward(toks)
+        assert close(last, ref[63]), max_violation(last, ref[63])
+    finally:
+        g.close()
