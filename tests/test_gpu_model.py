@@ -335,3 +335,29 @@ def test_odd_shapes(P, tmp_path, mtype):
         assert close(last, ref[63]), max_violation(last, ref[63])
     finally:
         g.close()
+
+
+@pytest.mark.parametrize("d,h,kv", [(384, 6, 2), (640, 5, 1)])
+def test_uneven_query_groups(P, tmp_path, d, h, kv):
+    """Query heads per kv head that are not powers of two (3 at head_dim 64,
+    5 at 128), so that the (head, row) query vectors of a kv head fill the
+    attention's 16-vector groups unevenly, at one row and verify batches of
+    9 and 15, against the oracle."""
+    path, raw, (L, d, h, kv, ff, V) = make(tmp_path, 150 + h, L=2, d=d, h=h, kv=kv, ff=2 * d, V=300)
+    rng = np.random.default_rng(h)
+    toks = rng.integers(0, V, 40).astype(np.int32)
+    ref = np.zeros((40, V), np.float32)
+    om = OracleModel(raw, L, d, h, kv, ff, V, n_ctx=4096)
+    assert O.or_forward_all(om.ptr, toks, 40, ref) == 0
+    g = GpuModel(P, path)
+    try:
+        got = g.verify(toks[:15])
+        assert close(got, ref[:15]), max_violation(got, ref[:15])
+        one = g.forward(toks[15:16])
+        assert close(one, ref[15]), max_violation(one, ref[15])
+        got = g.verify(toks[16:25])
+        assert close(got, ref[16:25]), max_violation(got, ref[16:25])
+        got = g.verify(toks[25:40])
+        assert close(got, ref[25:40]), max_violation(got, ref[25:40])
+    finally:
+        g.close()
