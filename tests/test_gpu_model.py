@@ -361,3 +361,26 @@ def test_uneven_query_groups(P, tmp_path, d, h, kv):
         assert close(got, ref[25:40]), max_violation(got, ref[25:40])
     finally:
         g.close()
+
+
+@pytest.mark.parametrize("emb", [GGML_Q4_0, GGML_Q8_0, GGML_F32])
+def test_tied_output_matrix(P, tmp_path, emb):
+    """A model without output.weight projects its logits with the token
+    embedding (src/format.c:237-238), here Q4_0, Q8_0 or F32: one-row
+    forwards and a verify batch against the oracle."""
+    path, raw, (L, d, h, kv, ff, V) = make(tmp_path, 170 + emb, emb_type=emb, with_output=False)
+    assert "output.weight" not in raw
+    rng = np.random.default_rng(emb + 11)
+    toks = rng.integers(0, V, 12).astype(np.int32)
+    ref = np.zeros((12, V), np.float32)
+    om = OracleModel(raw, L, d, h, kv, ff, V, n_ctx=4096)
+    assert O.or_forward_all(om.ptr, toks, 12, ref) == 0
+    g = GpuModel(P, path)
+    try:
+        for i in range(3):
+            one = g.forward(toks[i:i + 1])
+            assert close(one, ref[i]), (i, max_violation(one, ref[i]))
+        got = g.verify(toks[3:12])
+        assert close(got, ref[3:12]), max_violation(got, ref[3:12])
+    finally:
+        g.close()
