@@ -384,3 +384,34 @@ def test_tied_output_matrix(P, tmp_path, emb):
         assert close(got, ref[3:12]), max_violation(got, ref[3:12])
     finally:
         g.close()
+
+
+@pytest.mark.parametrize("mtype,q4_kernel", [(GGML_Q4_0, 0), (GGML_Q4_0, 1), (GGML_Q8_0, 0)])
+def test_synthetic_weight_scale_in_the_forward(P, tmp_path, mtype, q4_kernel):
+    """vx_set_synthetic_weight_scale multiplies every dequantized weight of
+    the reference's forward (src/quantize.c:7-15 via vx_dequantize): the
+    embedding rows and the exact-mode matrices; the x86 Q4_0 kernel reads
+    its blocks directly and is not scaled (src/model.c:212-244).  Scale 0.5
+    against the oracle with the same scale, one-row forwards and a verify
+    batch."""
+    path, raw, (L, d, h, kv, ff, V) = make(tmp_path, 190 + mtype + q4_kernel, matrix_type=mtype)
+    rng = np.random.default_rng(mtype + q4_kernel)
+    toks = rng.integers(0, V, 12).astype(np.int32)
+    ref = np.zeros((12, V), np.float32)
+    om = OracleModel(raw, L, d, h, kv, ff, V, n_ctx=4096, q4_mode=q4_kernel, wscale=0.5)
+    assert O.or_forward_all(om.ptr, toks, 12, ref) == 0
+    unscaled = np.zeros((12, V), np.float32)
+    om1 = OracleModel(raw, L, d, h, kv, ff, V, n_ctx=4096, q4_mode=q4_kernel)
+    assert O.or_forward_all(om1.ptr, toks, 12, unscaled) == 0
+    assert not close(ref, unscaled)     # the scale changes the logits
+    g = GpuModel(P, path, q4_kernel=q4_kernel)
+    P.vx_set_synthetic_weight_scale(0.5)
+    try:
+        for i in range(3):
+            one = g.forward(toks[i:i + 1])
+            assert close(one, ref[i]), (i, max_violation(one, ref[i]))
+        got = g.verify(toks[3:12])
+        assert close(got, ref[3:12]), max_violation(got, ref[3:12])
+    finally:
+        P.vx_set_synthetic_weight_scale(1.0)
+        g.close()
