@@ -415,3 +415,35 @@ def test_synthetic_weight_scale_in_the_forward(P, tmp_path, mtype, q4_kernel):
     finally:
         P.vx_set_synthetic_weight_scale(1.0)
         g.close()
+
+
+def test_prompt_longer_than_the_context(P, tmp_path):
+    """A 110-token prompt into an 80-position cache: the batched prefill
+    fills the 80 positions, the other 30 tokens run one at a time on the
+    last slot (src/model.c:279-286); the last logits, cache_len and every
+    cached row against the oracle, then a verify batch that keeps
+    overwriting that slot."""
+    path, raw, (L, d, h, kv, ff, V) = make(tmp_path, 201, L=2, d=128, h=4, kv=2, ff=256, V=200)
+    kvd = kv * (d // h)
+    g = GpuModel(P, path, n_ctx=80)
+    om = OracleModel(raw, L, d, h, kv, ff, V, n_ctx=80)
+    toks = np.random.default_rng(201).integers(0, V, 119).astype(np.int32)
+    try:
+        last = g.forward(toks[:110])
+        ref = np.zeros((110, V), np.float32)
+        assert O.or_forward_all(om.ptr, toks[:110], 110, ref) == 0
+        assert close(last, ref[109]), max_violation(last, ref[109])
+        assert g.cache_len == om.cache_len == 80
+        kc = om.k_cache.reshape(L, 80, kvd)
+        vc = om.v_cache.reshape(L, 80, kvd)
+        for l in range(L):
+            kk = np.zeros((80, kvd), np.float32)
+            vv = np.zeros((80, kvd), np.float32)
+            assert P.vx_model_read_kv(g.mp, l, 80, kk, vv) == 0, N.product_error()
+            assert close(kk, kc[l]) and close(vv, vc[l]), l
+        got = g.verify(toks[110:119])
+        ref = np.zeros((9, V), np.float32)
+        assert O.or_forward_all(om.ptr, toks[110:119], 9, ref) == 0
+        assert close(got, ref), max_violation(got, ref)
+    finally:
+        g.close()
