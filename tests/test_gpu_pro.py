@@ -538,6 +538,8 @@ def test_pro_attn_combines_partials(P, H, KV, hd, M, typ):
     (16, 2, 32, 3, 90, 256, 4096),        # head_dim 32: 32-position chunks
     (8, 2, 128, 64, 300, 512, 200),       # prompt-prefill batch: 64 rows, cap inside a two-chunk wavefront
     (32, 32, 64, 2, 2100, 2304, 4096),    # 34 MB of cache rows: read with non-temporal loads
+    (8, 2, 128, 9, 30000, 32768, 0),      # 32K context, no cap: ~940 chunk partials per query
+    (8, 1, 64, 1, 32760, 32768, 0),       # the last positions of a 32K cache, one row
 ])
 def test_attention_matches_reference(P, H, KV, hd, M, n_past, n_ctx, cap):
     """vxh_attention against softmax attention in float64 on the same cache
