@@ -384,6 +384,7 @@ def bind_attention(P):
     (8, 2, 64, 1, 0, 64, 4096, False),           # the first position: one row, nothing cached
     (8, 8, 128, 9, 0, 64, 4096, True),           # a batch from position 0 across the first chunk edge
     (8, 8, 128, 9, 28, 128, 4096, False),        # rows 28..36: the chunk edge inside the batch
+    (8, 2, 128, 9, 30000, 32768, 0, True),       # 32K context, no cap
 ])
 def test_attention_qkv_matches_rope_then_attention(P, H, KV, hd, M, n_past, n_ctx, cap, bias):
     """vxh_attention_qkv against vxh_rope_kv_norm followed by vxh_attention on
