@@ -373,3 +373,38 @@ def test_generate_argument_checks_and_stream_entry(P, models):
     finally:
         P.vx_model_destroy(tm)
         P.vx_model_destroy(dm)
+
+
+@pytest.mark.parametrize("n_gen", [1, 2, 3])
+def test_fewer_tokens_than_one_round(P, models, n_gen):
+    """max_tokens below k + 1: the round drafts only what can still be
+    emitted (src/speculative.c:258-263) and generate returns exactly
+    max_tokens tokens, the target's own greedy ones."""
+    (tpath, traw, tsh), _ = models
+    V = tsh[5]
+    prompt = np.arange(3, 12, dtype=np.int32)
+    tm, dm = load(P, tpath), load(P, tpath)
+    st = P.vx_speculative_create(dm, tm, 8)
+    assert st, N.product_error()
+    try:
+        P.vx_speculative_set_temp(st, 0.0, 1.0)
+        out = np.full(8, -5, np.int32)
+        assert P.vx_speculative_generate(st, prompt.copy(), len(prompt), out, n_gen) == n_gen, N.product_error()
+        assert np.all(out[n_gen:] == -5)
+        stats = N.VxSpecStats()
+        P.vx_speculative_get_stats(st, C.byref(stats))
+        assert stats.rounds == 1 and stats.drafted == n_gen - 1 and stats.emitted == n_gen
+    finally:
+        P.vx_speculative_destroy(st)
+        P.vx_model_destroy(tm)
+        P.vx_model_destroy(dm)
+    tg = load(P, tpath)
+    try:
+        lg = np.zeros(V, np.float32)
+        assert P.vx_model_forward(tg, prompt, len(prompt), lg) == 0
+        for i in range(n_gen):
+            t = int(np.argmax(lg))
+            assert out[i] == t, (i, out[:n_gen])
+            assert P.vx_model_forward(tg, np.array([t], np.int32), 1, lg) == 0
+    finally:
+        P.vx_model_destroy(tg)
